@@ -1,0 +1,134 @@
+/*
+ * molten_hip.h -- C ABI of the MI355X (gfx950) quantized-matmul hot path of
+ * molten (zhangshuibai/molten).
+ *
+ * This header is the drop-in boundary.  Each launcher replaces one operator
+ * wrapper of the reference's Rust/Metal operator layer; the replaced wrapper
+ * is cited as file:line under /root/reference.  The Rust side binds these
+ * with a thin `src/hip.rs` and keeps the operator
+ * signatures of the src/kernels/ modules.
+ *
+ * Conventions
+ *   - All tensors are device pointers (hipMalloc'd or views into one).
+ *     bf16 tensors are uint16_t bit patterns; ids/counts are uint32_t.
+ *   - Operators borrow their arguments and never allocate device memory.
+ *     Scratch words (argmax keys, counters) are caller-owned, must be zero on
+ *     entry and are left zero on exit where stated (the reference contract,
+ *     src/kernels/lfm.rs:259-263, :822-825).
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the default stream)
+ *     in call order.  Launchers do not synchronize.
+ *   - Return value: 0 = OK; < 0 = argument rejected before anything was
+ *     launched (message in mh_last_error()); > 0 = hipError_t at launch.
+ *
+ * Quantized weights use molten's MLX affine layout (src/weights.rs:11-30):
+ * codes U32 [out, in*bits/32], code j of a row at bit bits*j of the row's
+ * little-endian byte stream (Q4: 8 codes per word, low nibble first; Q6: 4
+ * codes per 3 bytes); scales and biases bf16 [out, in/group_size];
+ * w = scale*q + bias.  Stacked experts are one matrix of E*rows rows.
+ */
+#ifndef MOLTEN_HIP_H
+#define MOLTEN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------ status --- */
+
+enum {
+    MH_OK = 0,
+    MH_ERR_INVALID = -1,     /* bad shape, null pointer or out-of-range value */
+    MH_ERR_ALIGN = -2,       /* pointer or stride misaligned for the kernel   */
+    MH_ERR_UNSUPPORTED = -3, /* valid request this build has no kernel for   */
+    MH_ERR_RUNTIME = -4      /* runtime query failed before launch           */
+};
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char* mh_last_error(void);
+
+/* Library version, e.g. "molten-hip 0.1.0 gfx950". */
+const char* mh_version(void);
+
+typedef void* mh_stream_t; /* hipStream_t */
+typedef void* mh_event_t;  /* hipEvent_t  */
+
+/* MLX affine quantized matrix: molten's QuantWeights (src/weights.rs:11-30). */
+typedef struct mh_quant_weights {
+    const uint32_t* codes;  /* U32  [out_features, in_features*bits/32] */
+    const uint16_t* scales; /* bf16 [out_features, in_features/group_size] */
+    const uint16_t* biases; /* bf16 [out_features, in_features/group_size] */
+    uint32_t out_features;
+    uint32_t in_features;
+    uint32_t group_size;
+    uint32_t bits;
+} mh_quant_weights;
+
+/* ------------------------------------------------- device runtime ---
+ * Replaces MetalContext / ComputePass / Tensor host access
+ * (src/metal.rs:92-416, src/tensor.rs:100-192).  A "pass" is a stream:
+ * dispatches run serially in call order; commit = mh_event_record,
+ * PendingPass::wait = mh_event_synchronize. */
+int mh_device_count(int* count);
+int mh_set_device(int device);
+int mh_stream_create(mh_stream_t* stream);
+int mh_stream_destroy(mh_stream_t stream);
+int mh_stream_synchronize(mh_stream_t stream);
+int mh_event_create(mh_event_t* event);
+int mh_event_destroy(mh_event_t event);
+int mh_event_record(mh_event_t event, mh_stream_t stream);
+int mh_event_synchronize(mh_event_t event);
+int mh_malloc(void** ptr, size_t bytes);
+int mh_free(void* ptr);
+/* kind: 1 host->device, 2 device->host, 3 device->device.  Ordered on
+ * `stream`; returns after the copy completed. */
+int mh_memcpy(void* dst, const void* src, size_t bytes, int kind, mh_stream_t stream);
+/* Stream-ordered zero fill with a kernel (no hipMemsetAsync, so it is safe
+ * inside graph capture). */
+int mh_zero(void* dst, size_t bytes, mh_stream_t stream);
+
+/* ------------------------------------------------------ dequantize ---
+ * src/kernels/quant.rs:69 dequant_to_bf16 and :95 dequant_q4_bf16_bulk:
+ * out[r, j] = bf16(fma(scale, q, bias)), out bf16 [out, in]. */
+int mh_dequant_to_bf16(const mh_quant_weights* w, uint16_t* out, mh_stream_t stream);
+int mh_dequant_q4_bf16_bulk(const mh_quant_weights* w, uint16_t* out, mh_stream_t stream);
+
+/* --------------------------------------------------- decode GEMVs ---
+ * src/kernels/lfm.rs:112 gemv_quant: y[b, :] = bf16(W x[b, :]), f32
+ * accumulation in the chunk order, bits 4 or 6.  `batch` rows of x
+ * (1..8; the reference has batch 1).  x bf16 [batch, in], y bf16
+ * [batch, out]. */
+int mh_gemv_quant(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint32_t batch,
+                  mh_stream_t stream);
+
+/* src/kernels/lfm.rs:826 gemv_head_argmax: the head GEMV with an argmax
+ * epilogue; logits are not stored.  best[b] (u64, zero on entry) receives
+ * the orderable key of row b's argmax (value desc, index asc over the
+ * bf16-rounded logits); mh_token_tail reads and clears it. */
+int mh_gemv_head_argmax(const mh_quant_weights* w, const uint16_t* x, uint64_t* best,
+                        uint32_t batch, mh_stream_t stream);
+
+/* Head GEMV that stores the bf16 logits (y, may be NULL) AND folds the
+ * argmax keys into best[batch] (zero on entry).  With done != NULL (one u32,
+ * zero on entry) the last workgroup to finish writes ids[b] = argmax token of
+ * row b and leaves best and done zero again: one launch, no tail kernel.
+ * No reference counterpart for the stored-logits form: BASELINE configs 2/5. */
+int mh_gemv_quant_argmax(const mh_quant_weights* w, const uint16_t* x, uint16_t* y,
+                         uint64_t* best, uint32_t* done, uint32_t* ids, uint32_t batch,
+                         mh_stream_t stream);
+
+/* src/kernels/lfm.rs:850 token_tail without `next`: out_tok[b] = token of
+ * key best[b]; best[b] is cleared. */
+int mh_token_tail(uint64_t* best, uint32_t* out_tok, uint32_t batch, mh_stream_t stream);
+
+/* src/kernels/lfm.rs:794 argmax_bf16: two-stage argmax of a bf16 row,
+ * ties to the lowest index.  partials: scratch of >= 64*8 bytes. */
+int mh_argmax_bf16(const uint16_t* x, uint32_t n, void* partials, uint32_t* out,
+                   mh_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOLTEN_HIP_H */

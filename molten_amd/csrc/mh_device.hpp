@@ -1,0 +1,238 @@
+// mh_device.hpp -- device-side building blocks shared by the gfx950 kernels.
+//
+// Every floating-point step that feeds an integer decision (argmax ids, top-k
+// ids) is written as explicit IEEE operations in a fixed order, the "chunk
+// order":
+//   a K-long dot product is cut into C = K/32 chunks of 32 elements;
+//   p_c  = fma chain over the chunk's 32 elements in ascending k from +0;
+//   xs_c = ascending sum of the chunk's x from +0;
+//   h_c  = fma(s_g, p_c, b_g * xs_c)  (quantized; dense rows use h_c = p_c);
+//   virtual lane l (0..63) sums h_l, h_{l+64}, ... in ascending order from +0;
+//   the row value is the xor-butterfly (masks 1, 2, 4, 8, 16, 32) of the 64
+//   lane sums.
+// Files are built with -ffp-contract=off, so a*b+c is a multiply and an add
+// unless written as __builtin_fmaf, and f32 denormals are kept.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mh {
+
+constexpr int kWave = 64;
+
+// ------------------------------------------------------------------ bf16 ---
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Low / high bf16 of a packed pair.
+__device__ __forceinline__ float bf16lo(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+
+// Round to nearest even; NaN becomes a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        return static_cast<uint16_t>((u >> 16) | 0x0040u);
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// ------------------------------------------------------------------ exp ----
+// exp(x) in f32: Cody-Waite reduction x = n*ln2 + r with ln2 split into a
+// 16-bit head and a tail, degree-7 Taylor polynomial (coefficients 1/k!
+// rounded to f32) in Horner form with fma, and scaling by 2^n as two exact
+// power-of-two multiplies so an underflowing result rounds once.  Written out
+// so the CPU restatement reproduces it bit for bit.
+
+__device__ __forceinline__ float pow2i(int k) {  // 2^k, k in [-126, 127]
+    return __uint_as_float(static_cast<uint32_t>(k + 127) << 23);
+}
+
+__device__ __forceinline__ float expf_fixed(float x) {
+    if (x != x) {
+        return x + x;
+    }
+    if (x > 0x1.62e430p+6f) {
+        return __uint_as_float(0x7f800000u);
+    }
+    if (x < -0x1.9fe36ap+6f) {
+        return 0.0f;
+    }
+    const float n = __builtin_rintf(x * 0x1.715476p+0f);
+    float r = __builtin_fmaf(-n, 0x1.62e400p-1f, x);
+    r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+    p = __builtin_fmaf(p, r, 0x1.000000p-1f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int ni = static_cast<int>(n);
+    const int n1 = ni / 2;
+    const int n2 = ni - n1;
+    return (p * pow2i(n1)) * pow2i(n2);
+}
+
+// bf16(silu(g)) with silu(g) = g / (1 + exp(-g)), IEEE division.
+__device__ __forceinline__ float silu_bf16(float g) {
+    return round_bf16(g / (1.0f + expf_fixed(-g)));
+}
+
+// ------------------------------------------------------- wave reductions ---
+
+// xor-butterfly sum over the 64 lanes; every lane ends with the same value
+// (float addition is commutative, so a_l + a_{l^m} == a_{l^m} + a_l).
+__device__ __forceinline__ float wave_butterfly(float v) {
+    v = v + __shfl_xor(v, 1);
+    v = v + __shfl_xor(v, 2);
+    v = v + __shfl_xor(v, 4);
+    v = v + __shfl_xor(v, 8);
+    v = v + __shfl_xor(v, 16);
+    v = v + __shfl_xor(v, 32);
+    return v;
+}
+
+// The same tree with DPP lane moves (no LDS traffic), result valid in lane 63.
+// row_shr:1/2/4/8 pair lane l with l-1, l-2, l-4, l-8 inside each 16-lane
+// row; the lanes read below always have bits 0..(level-1) set, so each partner
+// is exactly l ^ m and the pairing is the xor butterfly's.  row_bcast:15 adds
+// row r-1's total into rows 1 and 3, row_bcast:31 adds rows 0-1 into rows
+// 2-3, so lane 63 = ((S0 + S1) + (S2 + S3)) with S_r the row tree sums.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+    v = v + dpp_move<0x111, 0xf>(v);  // row_shr:1
+    v = v + dpp_move<0x112, 0xf>(v);  // row_shr:2
+    v = v + dpp_move<0x114, 0xf>(v);  // row_shr:4
+    v = v + dpp_move<0x118, 0xf>(v);  // row_shr:8
+    v = v + dpp_move<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+    v = v + dpp_move<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+    return v;
+}
+
+// Lane 63's value as a wave-uniform scalar.
+__device__ __forceinline__ float lane63(float v) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// ------------------------------------------------------------ argmax key ---
+// "value desc, index asc" as one orderable u64 (lfm.metal:1119-1124):
+// -0 ties +0, NaN candidates are never produced by the merge below.
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t i) {
+    uint32_t u = __float_as_uint(v);
+    if ((u << 1) == 0u) {
+        u = 0u;
+    }
+    const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (static_cast<unsigned long long>(o) << 32) | static_cast<unsigned long long>(~i);
+}
+
+__device__ __forceinline__ void argmax_merge(float& bv, uint32_t& bi, float v, uint32_t i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+// ----------------------------------------------------------- chunk dots ---
+// Byte j of v as f32 (compiles to v_cvt_f32_ubyte{j}).
+__device__ __forceinline__ float ubyte_f32(uint32_t v, int j) {
+    return static_cast<float>((v >> (8 * j)) & 0xffu);
+}
+
+// Opaque copy: hides a value's known bits from the optimizer so that a whole
+// word masked once is converted byte by byte with v_cvt_f32_ubyte{0..3},
+// instead of being re-extracted per byte.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// Q4 chunk: 32 nibble codes in four words, low nibble first.  xr holds the
+// chunk's x with odd positions pre-multiplied by 1/16: the high nibble of a
+// byte is converted as 16*q and multiplied by x/16.  Both are exact (a bf16
+// times 2^-4 is an f32, denormals kept), so every fma sees the exact product
+// q*x and the chain equals fma(q_k, x_k, p) in ascending k.
+__device__ __forceinline__ float q4_chunk_dot(const uint32_t (&w)[4], const float* xr) {
+    float p = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const uint32_t lo = opaque(w[d] & 0x0f0f0f0fu);
+        const uint32_t hi = opaque(w[d] & 0xf0f0f0f0u);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            p = __builtin_fmaf(ubyte_f32(lo, j), xr[8 * d + 2 * j], p);
+            p = __builtin_fmaf(ubyte_f32(hi, j), xr[8 * d + 2 * j + 1], p);
+        }
+    }
+    return p;
+}
+
+// Q6 chunk: 32 six-bit codes in six words (code i at bit 6i).  xr is plain x.
+__device__ __forceinline__ float q6_chunk_dot(const uint32_t (&w)[6], const float* xr) {
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const int bit = 6 * i;
+        const int d = bit >> 5;
+        const int o = bit & 31;
+        uint32_t v;
+        if (o + 6 <= 32) {
+            v = (w[d] >> o) & 63u;
+        } else {
+            v = __builtin_amdgcn_alignbit(w[d + 1], w[d], o) & 63u;
+        }
+        p = __builtin_fmaf(static_cast<float>(v), xr[i], p);
+    }
+    return p;
+}
+
+// ---------------------------------------------------------- chunk loads ---
+template <int BITS>
+struct Chunk;
+
+template <>
+struct Chunk<4> {
+    uint32_t w[4];
+    __device__ __forceinline__ void load(const uint32_t* p) {  // 16-byte aligned
+        const uint4 v = *reinterpret_cast<const uint4*>(p);
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    }
+    __device__ __forceinline__ void zero() { w[0] = w[1] = w[2] = w[3] = 0u; }
+    __device__ __forceinline__ float dot(const float* xr) const { return q4_chunk_dot(w, xr); }
+};
+
+template <>
+struct Chunk<6> {
+    uint32_t w[6];
+    __device__ __forceinline__ void load(const uint32_t* p) {  // 8-byte aligned
+        const uint2* q = reinterpret_cast<const uint2*>(p);
+        const uint2 a = q[0], b = q[1], c = q[2];
+        w[0] = a.x; w[1] = a.y; w[2] = b.x; w[3] = b.y; w[4] = c.x; w[5] = c.y;
+    }
+    __device__ __forceinline__ void zero() { w[0] = w[1] = w[2] = w[3] = w[4] = w[5] = 0u; }
+    __device__ __forceinline__ float dot(const float* xr) const { return q6_chunk_dot(w, xr); }
+};
+
+// x prepared for a chunk dot: Q4 scales odd positions by 1/16.
+template <int BITS>
+__device__ __forceinline__ float prep_x(float x, int pos_in_chunk) {
+    if (BITS == 4 && (pos_in_chunk & 1)) {
+        return x * 0.0625f;
+    }
+    return x;
+}
+
+}  // namespace mh

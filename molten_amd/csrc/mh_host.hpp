@@ -1,0 +1,60 @@
+// mh_host.hpp -- host-side helpers for the extern "C" launchers: the error
+// convention, argument validation and device queries.
+//
+// Error convention (mirrors the reference's `anyhow::ensure!` before any
+// dispatch, src/metal.rs:337-353): a launcher validates every argument
+// before it touches the HIP runtime.  It returns
+//   0                on success,
+//   MH_ERR_* (< 0)   when an argument is rejected; nothing was launched and
+//                    mh_last_error() holds the message,
+//   hipError_t (> 0) when the runtime reports an error at launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "molten_hip.h"
+
+namespace mh {
+
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_error(hipError_t e, const char* what);
+
+// Number of compute units of the current device (cached per device).
+int cu_count();
+
+inline hipStream_t as_stream(mh_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned(const void* p, uintptr_t a) {
+    return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+// Shared checks for MLX affine weights (src/kernels/quant.rs:42-66 check_quant):
+// bits in {4, 6}; group size a multiple of 32 that divides K (a 32-code chunk
+// never crosses a group); codes aligned for the vector loads.
+int check_quant(const mh_quant_weights* w, const char* op);
+
+// Launch status after hipLaunchKernelGGL.
+inline int launch_status(const char* what) {
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? MH_OK : hip_error(e, what);
+}
+
+}  // namespace mh
+
+#define MH_ENSURE(cond, code, ...)                      \
+    do {                                                \
+        if (!(cond)) {                                  \
+            return ::mh::set_error((code), __VA_ARGS__); \
+        }                                               \
+    } while (0)
+
+#define MH_TRY(expr)                 \
+    do {                             \
+        const int mh_rc_ = (expr);   \
+        if (mh_rc_ != MH_OK) {       \
+            return mh_rc_;           \
+        }                            \
+    } while (0)

@@ -1,0 +1,209 @@
+/*
+ * oracle.h -- CPU restatement of molten's quantized-matmul hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (molten_amd/, include/)
+ * includes, links or calls this code.  Only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg load it, and only as the checker / the
+ * timed CPU baseline.  It is plain C99 + OpenMP, built by oracle/Makefile
+ * with -ffp-contract=off so that every floating-point operation below is the
+ * one written (explicit fmaf() where a fused multiply-add is meant).
+ *
+ * Semantics follow the reference (zhangshuibai/molten) file:line cited at
+ * each function.  Where the reference leaves an order unspecified (Metal
+ * simd_sum trees, fast-math contraction) this oracle fixes one canonical
+ * order, the "chunk order" below, and the HIP kernels follow the same order,
+ * so that outputs that feed integer decisions (argmax ids, top-k ids) are
+ * bit-identical between CPU and GPU.
+ *
+ * Chunk order (every GEMV-family dot product of length K, K % 32 == 0):
+ *   C = K / 32 chunks of 32 consecutive elements.
+ *   p_c  = +0.0f; for k = 32c .. 32c+31 ascending: p_c = fmaf(q_k, x_k, p_c)
+ *          (dense weights: fmaf(w_k, x_k, p_c))
+ *   xs_c = +0.0f; for k ascending: xs_c = xs_c + x_k
+ *   h_c  = fmaf(s_g, p_c, b_g * xs_c), g = 32c / group_size   (dense: h_c = p_c)
+ *   a_l  = +0.0f; for c = l, l+64, l+128, ... < C: a_l = a_l + h_c   (l = 0..63)
+ *   v    = butterfly over the 64 lane sums: for m = 1,2,4,8,16,32:
+ *          a_l = a_l + a_{l^m}  (all l simultaneously); v = a_0.
+ *
+ * Parity status of each function is stated at its declaration; the checks
+ * that pin it live in tests/test_oracle_*.py.
+ */
+#ifndef MOLTEN_ORACLE_H
+#define MOLTEN_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* MLX affine quantized matrix, molten's QuantWeights (src/weights.rs:11-30):
+ * codes U32 [n, k*bits/32] (code j of a row at bit bits*j of the row's
+ * little-endian byte stream), scales/biases bf16 [n, k/gs]. */
+typedef struct orc_qw {
+    const uint32_t* codes;
+    const uint16_t* scales;
+    const uint16_t* biases;
+    uint32_t n, k, gs, bits;
+} orc_qw;
+
+/* ---- scalar helpers ---------------------------------------------------- */
+
+/* bf16 -> f32 is exact; f32 -> bf16 rounds to nearest even (NaN -> quiet NaN).
+ * Pinned: exhaustive over all 65536 bf16 values against numpy, and RNE ties. */
+float orc_bf16_to_f32(uint16_t h);
+uint16_t orc_f32_to_bf16(float f);
+
+/* exp(x) in f32: Cody-Waite reduction x = n*ln2 + r (ln2 split hi/lo),
+ * degree-7 Taylor polynomial in Horner form with fmaf, scaling by 2^n as
+ * exact power-of-two multiplies.  Used by sigmoid, SiLU and softmax so the
+ * GPU can reproduce it bit for bit.  Pinned: max error vs float64 exp over a
+ * dense sweep (tests/test_oracle_math.py). */
+float orc_expf(float x);
+
+/* ---- a2 / a3: unpack and pack (lfm.metal:102-109, :186-199;
+ *      quant_nax.metal:2947-2953, :2975-2986) --------------------------------
+ * q[j] = (stream >> bits*j) & (2^bits - 1).  bits in {4, 6, 8}.
+ * Pinned: known-answer words (0x76543210 -> 0..7; Q6 [1,2,3,4] -> 81 30 10)
+ * and pack/unpack round trips. */
+void orc_unpack(const uint32_t* codes, uint32_t bits, size_t n_codes, uint8_t* q);
+void orc_pack(const uint8_t* q, uint32_t bits, size_t n_codes, uint32_t* codes);
+
+/* ---- dequant_to_bf16 / dequant_q4_bf16_bulk (src/kernels/quant.rs:69, :95;
+ *      quant.metal:45-114; MLX dequantize quant_nax.metal:2908-2993) --------
+ * out[r, j] = bf16(fmaf(s, q, b)).  Pinned: closed form vs numpy float64
+ * (one rounding of s*q+b) and the all-zero / s=0 special cases. */
+void orc_dequant_bf16(const orc_qw* w, uint16_t* out);
+
+/* ---- a4 / a5: affine quantized GEMV (lfm.metal:100-297, GEMV_Q4_BODY,
+ *      lfm_gemv_q6_bf16_x4; src/kernels/lfm.rs:112-149) ---------------------
+ * y[b, r] = bf16(v) with v the chunk-order value of row r against x[b, :].
+ * batch rows are independent.  yf (nullable) receives v before rounding.
+ * Pinned: numpy float64 of the dequantized matrix (tolerance), closed forms
+ * (all codes 0, s = 0, one-hot x, x = 1), and a pure-Python replay of the
+ * chunk order on tiny shapes (bit-exact). */
+void orc_gemv_quant(const orc_qw* w, const uint16_t* x, uint32_t batch,
+                    uint16_t* y, float* yf);
+/* Only the listed rows (for sampled checks at full size): y[b * n_rows + i]. */
+void orc_gemv_quant_rows(const orc_qw* w, const uint16_t* x, uint32_t batch,
+                         const uint32_t* rows, uint32_t n_rows, uint16_t* y);
+
+/* ---- a6: argmax over bf16 logits (lfm.metal:1113-1282) ------------------
+ * value desc, index asc; -0 == +0; NaN never taken; none -> 0.  Pinned by
+ * known-answer ties and numpy argmax on tie-free rows. */
+uint32_t orc_argmax_bf16(const uint16_t* x, size_t n);
+/* Orderable 64-bit key (lfm.metal:1119-1124): larger key = larger value, or
+ * equal value at a lower index. */
+uint64_t orc_argmax_key(float v, uint32_t i);
+
+/* ---- a7 / a12: dense router GEMV (src/kernels/lfm.rs:314-335, :366-388;
+ *      lfm.metal:368-428, :470-537) ----------------------------------------
+ * y[t, e] = chunk-order dot of W[e, :] and x[t, :] (h_c = p_c), f32 out.
+ * w_is_f32: 1 -> W is f32 [n, k] (the reference's router), 0 -> bf16 [n, k]
+ * (BASELINE's router).  Pinned: numpy float64 (tolerance) and Python replay
+ * (bit-exact) on tiny shapes. */
+void orc_gemv_dense(const void* w, int w_is_f32, const uint16_t* x,
+                    uint32_t m, uint32_t n, uint32_t k, float* y);
+
+/* ---- a8 / a12: top-k routing (lfm.metal:541-703, :1558-1602) ------------
+ * mode 0 (reference): s = 1/(1+exp(-z)); rank on s + bias[e]; weights
+ *        bf16(s_r / (eps + sum_r s_r)), sum in rank order from eps.
+ * mode 1 (BASELINE): rank on the logits z; weights
+ *        bf16(e_r / (e_0 + ... + e_{k-1})), e_r = exp(z_r - z_top1).
+ * Ties go to the lower expert id.  bias may be NULL (treated as 0).
+ * Pinned: constructed ties, numpy ranking, softmax/sigmoid closed forms. */
+void orc_route(const float* logits, const float* bias, uint32_t m, uint32_t e,
+               uint32_t topk, int mode, float eps, uint32_t* ids, uint16_t* w);
+
+/* ---- a9 / a11: gate/up GEMV + SwiGLU (lfm.metal:1392-1498) ---------------
+ * act[r, j] = bf16( bf16(silu(g)) * u ), g = f32(bf16(gate row)),
+ * u = f32(bf16(up row)), silu(g) = g / (1 + exp(-g)).
+ * Rows of expert ids[r] are ids[r]*n_inter + j of the stacked matrices.
+ * ids == NULL: dense (one slot, rows j).  Pinned: composition of pinned
+ * parts (GEMV, expf, bf16) plus a float64 end-to-end check. */
+void orc_gather_act(const orc_qw* gate, const orc_qw* up, uint32_t n_inter,
+                    const uint16_t* x, const uint32_t* ids, uint32_t topk,
+                    uint16_t* act);
+
+/* ---- a10: down GEMV + weighted combine (lfm.metal:1503-1554) --------------
+ * p_r = bf16(down row ids[r]*n_out + i against act[r]);
+ * out[i] = bf16( sum_r f32(bf16(w_r * p_r)) ), r ascending from +0.0f. */
+void orc_down_combine(const orc_qw* down, uint32_t n_out, const uint16_t* act,
+                      const uint32_t* ids, const uint16_t* w, uint32_t topk,
+                      uint16_t* out);
+
+/* ---- a19 decode: whole MoE decode step (src/lfm.rs:967-1011) ------------
+ * router -> route -> gather_act -> down_combine.  logits/ids/w/act are
+ * outputs too (any may be NULL). */
+void orc_moe_decode(const void* router, int router_is_f32, const float* bias,
+                    int mode, float eps, const orc_qw* gate, const orc_qw* up,
+                    const orc_qw* down, uint32_t n_experts, uint32_t topk,
+                    uint32_t d_model, uint32_t n_inter, const uint16_t* x,
+                    uint16_t* out, float* logits, uint32_t* ids, uint16_t* w,
+                    uint16_t* act);
+
+/* ---- a13: counting sort (lfm.metal:1604-1685) ----------------------------
+ * counts[e] = #slots routed to e; offsets = exclusive scan; stable scatter in
+ * token-major, rank-major order: ids_sorted[pos] = t, slotpos[t*topk+r] = pos.
+ * Pinned: numpy bincount / cumsum / argsort(kind="stable"). */
+void orc_moe_count(const uint32_t* ids, uint32_t s, uint32_t e, uint32_t* counts);
+void orc_moe_offsets(const uint32_t* counts, uint32_t e, uint32_t* offsets);
+void orc_moe_sorted(const uint32_t* ids, const uint32_t* offsets, uint32_t m,
+                    uint32_t e, uint32_t topk, uint32_t* ids_sorted,
+                    uint32_t* slotpos);
+
+/* ---- a14: block maps (lfm.metal:1687-1770; src/lfm.rs:896-933) ------------
+ * Entry i of expert e: uint4(m0, e*N + n0, n0, m_end), row tiles of bm,
+ * column tiles of bn, expert order; the tail up to max_* is zero.
+ * Pinned: brute-force enumeration from the definition in Python. */
+void orc_moe_block_offsets(const uint32_t* counts, uint32_t e, uint32_t bm,
+                           uint32_t bn, uint32_t gu_n, uint32_t dn_n,
+                           uint32_t* gu_off, uint32_t* dn_off);
+void orc_moe_blocks(const uint32_t* counts, const uint32_t* offsets,
+                    const uint32_t* gu_off, const uint32_t* dn_off, uint32_t e,
+                    uint32_t bm, uint32_t bn, uint32_t gu_n, uint32_t dn_n,
+                    uint32_t* gu, uint32_t max_gu, uint32_t* dn, uint32_t max_dn);
+
+/* ---- a15 / a17 / a18: gather, SwiGLU, combine (elementwise.metal:7-52;
+ *      lfm.metal:859-940) ---------------------------------------------------- */
+void orc_gather_rows_bf16(const uint16_t* table, const uint32_t* ids, uint32_t m,
+                          uint32_t h, uint16_t* out);
+void orc_silu_mul_bf16(const uint16_t* gate, const uint16_t* up, size_t n,
+                       uint16_t* out);
+void orc_moe_combine_rows(const uint16_t* sorted, const uint32_t* slotpos,
+                          const uint16_t* w, uint32_t m, uint32_t h,
+                          uint32_t topk, uint16_t* out);
+
+/* ---- a16: block-mapped grouped Q4 GEMM (src/kernels/quant.rs:151-266;
+ *      quant_nax.metal:4091-4234, :4392-4699) ------------------------------
+ * For every entry (m0, e*N + n0, n0, m_end) of blocks[0..n_blocks):
+ *   C[m, n0 + j] = bf16( sum_k f32(A[m, k]) * f32(bf16(fmaf(s, q, b))) ),
+ *   m in [m0, m_end), j in [0, bn), f32 accumulation in ascending k.
+ * Pinned: reduction to per-expert dense GEMMs checked with numpy float64. */
+void orc_gemm_q4_grouped(const uint16_t* a, const orc_qw* w, uint16_t* c,
+                         const uint32_t* blocks, uint32_t n_blocks, uint32_t n,
+                         uint32_t bn);
+
+/* Whole prefill MoE for m tokens (src/lfm.rs:847-965): router_prefill ->
+ * route -> counting sort -> gather -> grouped gate/up -> SwiGLU -> grouped
+ * down -> combine.  The grouped GEMMs are computed per sorted row directly
+ * (the block map only partitions the same sums).  Intermediates are outputs
+ * when non-NULL. */
+void orc_moe_prefill(const void* router, int router_is_f32, const float* bias,
+                     int mode, float eps, const orc_qw* gate, const orc_qw* up,
+                     const orc_qw* down, uint32_t n_experts, uint32_t topk,
+                     uint32_t d_model, uint32_t n_inter, uint32_t m,
+                     const uint16_t* x, uint16_t* out, uint32_t* ids,
+                     uint16_t* gw, uint32_t* counts, uint32_t* offsets,
+                     uint32_t* ids_sorted, uint32_t* slotpos, uint16_t* act,
+                     uint16_t* ed);
+
+/* OpenMP thread count used by the heavy loops (0 = library default). */
+void orc_set_threads(int n);
+int orc_get_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,441 @@
+/*
+ * oracle_core.c -- scalar helpers, unpack/pack, dequant, the chunk-order
+ * GEMV family, argmax, routing and the decode MoE step.
+ * TEST INFRASTRUCTURE ONLY (see oracle.h).
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static int g_threads = 0;
+
+void orc_set_threads(int n) { g_threads = n; }
+
+int orc_get_threads(void) {
+#ifdef _OPENMP
+    return g_threads > 0 ? g_threads : omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+#define ORC_THREADS (orc_get_threads())
+
+/* ------------------------------------------------------------ scalars --- */
+
+float orc_bf16_to_f32(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+uint16_t orc_f32_to_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) {
+        return (uint16_t)((u >> 16) | 0x0040u);
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+static inline float bfr(float f) { return orc_bf16_to_f32(orc_f32_to_bf16(f)); }
+
+static inline float pow2f(int k) { /* 2^k for k in [-126, 127] */
+    uint32_t u = (uint32_t)(k + 127) << 23;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+float orc_expf(float x) {
+    if (x != x) {
+        return x + x;
+    }
+    if (x > 0x1.62e430p+6f) {
+        return INFINITY;
+    }
+    if (x < -0x1.9fe36ap+6f) {
+        return 0.0f;
+    }
+    const float n = rintf(x * 0x1.715476p+0f);
+    float r = fmaf(-n, 0x1.62e400p-1f, x);
+    r = fmaf(-n, 0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;
+    p = fmaf(p, r, 0x1.6c16c2p-10f);
+    p = fmaf(p, r, 0x1.111112p-7f);
+    p = fmaf(p, r, 0x1.555556p-5f);
+    p = fmaf(p, r, 0x1.555556p-3f);
+    p = fmaf(p, r, 0x1.000000p-1f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    const int ni = (int)n;
+    const int n1 = ni / 2;
+    const int n2 = ni - n1;
+    return (p * pow2f(n1)) * pow2f(n2);
+}
+
+/* -------------------------------------------------------- unpack/pack --- */
+
+static inline uint32_t code_at(const uint32_t* row, uint32_t bits, uint32_t j) {
+    const uint32_t bit = bits * j;
+    const uint32_t w = bit >> 5;
+    const uint32_t o = bit & 31u;
+    uint32_t v = row[w] >> o;
+    if (o + bits > 32u) {
+        v |= row[w + 1] << (32u - o);
+    }
+    return v & ((1u << bits) - 1u);
+}
+
+void orc_unpack(const uint32_t* codes, uint32_t bits, size_t n_codes, uint8_t* q) {
+    for (size_t j = 0; j < n_codes; ++j) {
+        const size_t bit = (size_t)bits * j;
+        const size_t w = bit >> 5;
+        const uint32_t o = (uint32_t)(bit & 31u);
+        uint32_t v = codes[w] >> o;
+        if (o + bits > 32u) {
+            v |= codes[w + 1] << (32u - o);
+        }
+        q[j] = (uint8_t)(v & ((1u << bits) - 1u));
+    }
+}
+
+void orc_pack(const uint8_t* q, uint32_t bits, size_t n_codes, uint32_t* codes) {
+    const size_t n_words = (n_codes * bits + 31) / 32;
+    memset(codes, 0, n_words * 4);
+    for (size_t j = 0; j < n_codes; ++j) {
+        const size_t bit = (size_t)bits * j;
+        const size_t w = bit >> 5;
+        const uint32_t o = (uint32_t)(bit & 31u);
+        const uint32_t v = (uint32_t)q[j] & ((1u << bits) - 1u);
+        codes[w] |= v << o;
+        if (o + bits > 32u) {
+            codes[w + 1] |= v >> (32u - o);
+        }
+    }
+}
+
+/* ------------------------------------------------------------ dequant --- */
+
+static inline size_t row_words(const orc_qw* w) { return (size_t)w->k * w->bits / 32; }
+
+void orc_dequant_bf16(const orc_qw* w, uint16_t* out) {
+    const uint32_t groups = w->k / w->gs;
+#pragma omp parallel for schedule(static) num_threads(ORC_THREADS)
+    for (long r = 0; r < (long)w->n; ++r) {
+        const uint32_t* row = w->codes + (size_t)r * row_words(w);
+        for (uint32_t j = 0; j < w->k; ++j) {
+            const uint32_t g = j / w->gs;
+            const float s = orc_bf16_to_f32(w->scales[(size_t)r * groups + g]);
+            const float b = orc_bf16_to_f32(w->biases[(size_t)r * groups + g]);
+            const float q = (float)code_at(row, w->bits, j);
+            out[(size_t)r * w->k + j] = orc_f32_to_bf16(fmaf(s, q, b));
+        }
+    }
+}
+
+/* ----------------------------------------------------- chunk-order dot --- */
+
+static inline float butterfly64(float* a) {
+    float t[64];
+    for (uint32_t m = 1; m < 64; m <<= 1) {
+        for (uint32_t l = 0; l < 64; ++l) {
+            t[l] = a[l] + a[l ^ m];
+        }
+        memcpy(a, t, sizeof(t));
+    }
+    return a[0];
+}
+
+/* x-sums of every 32-element chunk of xf[0..k). */
+static void chunk_xsums(const float* xf, uint32_t k, float* xs) {
+    for (uint32_t c = 0; c < k / 32; ++c) {
+        float s = 0.0f;
+        for (uint32_t i = 0; i < 32; ++i) {
+            s = s + xf[32 * c + i];
+        }
+        xs[c] = s;
+    }
+}
+
+/* Chunk-order value of quantized row r against f32 x (xs = chunk x-sums). */
+static float qrow_value(const orc_qw* w, uint32_t r, const float* xf, const float* xs) {
+    const uint32_t C = w->k / 32;
+    const uint32_t groups = w->k / w->gs;
+    const uint32_t* row = w->codes + (size_t)r * row_words(w);
+    float a[64];
+    for (uint32_t l = 0; l < 64; ++l) {
+        a[l] = 0.0f;
+    }
+    for (uint32_t c = 0; c < C; ++c) {
+        float p = 0.0f;
+        for (uint32_t i = 0; i < 32; ++i) {
+            const uint32_t kk = 32 * c + i;
+            p = fmaf((float)code_at(row, w->bits, kk), xf[kk], p);
+        }
+        const uint32_t g = (32 * c) / w->gs;
+        const float s = orc_bf16_to_f32(w->scales[(size_t)r * groups + g]);
+        const float b = orc_bf16_to_f32(w->biases[(size_t)r * groups + g]);
+        const float h = fmaf(s, p, b * xs[c]);
+        a[c & 63u] = a[c & 63u] + h;
+    }
+    return butterfly64(a);
+}
+
+static float* to_f32(const uint16_t* x, size_t n) {
+    float* f = (float*)malloc(n * sizeof(float));
+    for (size_t i = 0; i < n; ++i) {
+        f[i] = orc_bf16_to_f32(x[i]);
+    }
+    return f;
+}
+
+void orc_gemv_quant(const orc_qw* w, const uint16_t* x, uint32_t batch, uint16_t* y,
+                    float* yf) {
+    const uint32_t K = w->k, C = K / 32;
+    float* xf = to_f32(x, (size_t)batch * K);
+    float* xs = (float*)malloc((size_t)batch * C * sizeof(float));
+    for (uint32_t b = 0; b < batch; ++b) {
+        chunk_xsums(xf + (size_t)b * K, K, xs + (size_t)b * C);
+    }
+#pragma omp parallel for schedule(static) num_threads(ORC_THREADS)
+    for (long r = 0; r < (long)w->n; ++r) {
+        for (uint32_t b = 0; b < batch; ++b) {
+            const float v = qrow_value(w, (uint32_t)r, xf + (size_t)b * K, xs + (size_t)b * C);
+            if (y) {
+                y[(size_t)b * w->n + r] = orc_f32_to_bf16(v);
+            }
+            if (yf) {
+                yf[(size_t)b * w->n + r] = v;
+            }
+        }
+    }
+    free(xs);
+    free(xf);
+}
+
+void orc_gemv_quant_rows(const orc_qw* w, const uint16_t* x, uint32_t batch,
+                         const uint32_t* rows, uint32_t n_rows, uint16_t* y) {
+    const uint32_t K = w->k, C = K / 32;
+    float* xf = to_f32(x, (size_t)batch * K);
+    float* xs = (float*)malloc((size_t)batch * C * sizeof(float));
+    for (uint32_t b = 0; b < batch; ++b) {
+        chunk_xsums(xf + (size_t)b * K, K, xs + (size_t)b * C);
+    }
+#pragma omp parallel for schedule(static) num_threads(ORC_THREADS)
+    for (long i = 0; i < (long)n_rows; ++i) {
+        for (uint32_t b = 0; b < batch; ++b) {
+            const float v = qrow_value(w, rows[i], xf + (size_t)b * K, xs + (size_t)b * C);
+            y[(size_t)b * n_rows + i] = orc_f32_to_bf16(v);
+        }
+    }
+    free(xs);
+    free(xf);
+}
+
+/* ------------------------------------------------------------- argmax --- */
+
+uint32_t orc_argmax_bf16(const uint16_t* x, size_t n) {
+    float bv = -INFINITY;
+    uint32_t bi = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const float v = orc_bf16_to_f32(x[i]);
+        if (v > bv || (v == bv && (uint32_t)i < bi)) {
+            bv = v;
+            bi = (uint32_t)i;
+        }
+    }
+    return bi;
+}
+
+uint64_t orc_argmax_key(float v, uint32_t i) {
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    if ((u << 1) == 0u) {
+        u = 0u;
+    }
+    const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint64_t)(~i);
+}
+
+/* --------------------------------------------------------- dense GEMV --- */
+
+void orc_gemv_dense(const void* w, int w_is_f32, const uint16_t* x, uint32_t m,
+                    uint32_t n, uint32_t k, float* y) {
+    const uint32_t C = k / 32;
+    float* xf = to_f32(x, (size_t)m * k);
+#pragma omp parallel for collapse(2) schedule(static) num_threads(ORC_THREADS)
+    for (long t = 0; t < (long)m; ++t) {
+        for (long e = 0; e < (long)n; ++e) {
+            const float* xr = xf + (size_t)t * k;
+            float a[64];
+            for (uint32_t l = 0; l < 64; ++l) {
+                a[l] = 0.0f;
+            }
+            for (uint32_t c = 0; c < C; ++c) {
+                float p = 0.0f;
+                for (uint32_t i = 0; i < 32; ++i) {
+                    const size_t kk = 32 * c + i;
+                    const float wv = w_is_f32
+                        ? ((const float*)w)[(size_t)e * k + kk]
+                        : orc_bf16_to_f32(((const uint16_t*)w)[(size_t)e * k + kk]);
+                    p = fmaf(wv, xr[kk], p);
+                }
+                a[c & 63u] = a[c & 63u] + p;
+            }
+            y[(size_t)t * n + e] = butterfly64(a);
+        }
+    }
+    free(xf);
+}
+
+/* ------------------------------------------------------------ routing --- */
+
+static void route_one(const float* z, const float* bias, uint32_t e, uint32_t topk,
+                      int mode, float eps, uint32_t* ids, uint16_t* w) {
+    float s[256];
+    float cand[256];
+    unsigned char used[256];
+    for (uint32_t i = 0; i < e; ++i) {
+        if (mode == 0) {
+            s[i] = 1.0f / (1.0f + orc_expf(-z[i]));
+            cand[i] = s[i] + (bias ? bias[i] : 0.0f);
+        } else {
+            s[i] = z[i];
+            cand[i] = z[i];
+        }
+        used[i] = 0;
+    }
+    uint32_t chosen[16];
+    for (uint32_t r = 0; r < topk; ++r) {
+        float best = -INFINITY;
+        uint32_t best_e = 0;
+        for (uint32_t i = 0; i < e; ++i) {
+            if (used[i]) {
+                continue;
+            }
+            const float v = cand[i];
+            if (v > best || (v == best && i < best_e)) {
+                best = v;
+                best_e = i;
+            }
+        }
+        chosen[r] = best_e;
+        used[best_e] = 1;
+    }
+    if (mode == 0) {
+        float denom = eps;
+        for (uint32_t r = 0; r < topk; ++r) {
+            denom += s[chosen[r]];
+        }
+        for (uint32_t r = 0; r < topk; ++r) {
+            ids[r] = chosen[r];
+            w[r] = orc_f32_to_bf16(s[chosen[r]] / denom);
+        }
+    } else {
+        const float top = z[chosen[0]];
+        float ev[16];
+        float denom = 0.0f;
+        for (uint32_t r = 0; r < topk; ++r) {
+            ev[r] = orc_expf(z[chosen[r]] - top);
+            denom = denom + ev[r];
+        }
+        for (uint32_t r = 0; r < topk; ++r) {
+            ids[r] = chosen[r];
+            w[r] = orc_f32_to_bf16(ev[r] / denom);
+        }
+    }
+}
+
+void orc_route(const float* logits, const float* bias, uint32_t m, uint32_t e,
+               uint32_t topk, int mode, float eps, uint32_t* ids, uint16_t* w) {
+#pragma omp parallel for schedule(static) num_threads(ORC_THREADS)
+    for (long t = 0; t < (long)m; ++t) {
+        route_one(logits + (size_t)t * e, bias, e, topk, mode, eps, ids + (size_t)t * topk,
+                  w + (size_t)t * topk);
+    }
+}
+
+/* ------------------------------------------------- decode expert GEMVs --- */
+
+static inline float silu_bf16(float g) {
+    return bfr(g / (1.0f + orc_expf(-g)));
+}
+
+void orc_gather_act(const orc_qw* gate, const orc_qw* up, uint32_t n_inter,
+                    const uint16_t* x, const uint32_t* ids, uint32_t topk, uint16_t* act) {
+    const uint32_t K = gate->k, C = K / 32;
+    const uint32_t slots = ids ? topk : 1;
+    float* xf = to_f32(x, K);
+    float* xs = (float*)malloc(C * sizeof(float));
+    chunk_xsums(xf, K, xs);
+#pragma omp parallel for collapse(2) schedule(static) num_threads(ORC_THREADS)
+    for (long r = 0; r < (long)slots; ++r) {
+        for (long j = 0; j < (long)n_inter; ++j) {
+            const uint32_t row = (ids ? ids[r] * n_inter : 0u) + (uint32_t)j;
+            const float gv = bfr(qrow_value(gate, row, xf, xs));
+            const float uv = bfr(qrow_value(up, row, xf, xs));
+            act[(size_t)r * n_inter + j] = orc_f32_to_bf16(silu_bf16(gv) * uv);
+        }
+    }
+    free(xs);
+    free(xf);
+}
+
+void orc_down_combine(const orc_qw* down, uint32_t n_out, const uint16_t* act,
+                      const uint32_t* ids, const uint16_t* w, uint32_t topk, uint16_t* out) {
+    const uint32_t K = down->k, C = K / 32;
+    float* af = to_f32(act, (size_t)topk * K);
+    float* xs = (float*)malloc((size_t)topk * C * sizeof(float));
+    for (uint32_t r = 0; r < topk; ++r) {
+        chunk_xsums(af + (size_t)r * K, K, xs + (size_t)r * C);
+    }
+#pragma omp parallel for schedule(static) num_threads(ORC_THREADS)
+    for (long i = 0; i < (long)n_out; ++i) {
+        float total = 0.0f;
+        for (uint32_t r = 0; r < topk; ++r) {
+            const float p = bfr(qrow_value(down, ids[r] * n_out + (uint32_t)i,
+                                           af + (size_t)r * K, xs + (size_t)r * C));
+            total = total + bfr(orc_bf16_to_f32(w[r]) * p);
+        }
+        out[i] = orc_f32_to_bf16(total);
+    }
+    free(xs);
+    free(af);
+}
+
+void orc_moe_decode(const void* router, int router_is_f32, const float* bias, int mode,
+                    float eps, const orc_qw* gate, const orc_qw* up, const orc_qw* down,
+                    uint32_t n_experts, uint32_t topk, uint32_t d_model, uint32_t n_inter,
+                    const uint16_t* x, uint16_t* out, float* logits, uint32_t* ids,
+                    uint16_t* w, uint16_t* act) {
+    float* lg = (float*)malloc(n_experts * sizeof(float));
+    uint32_t id[16];
+    uint16_t wt[16];
+    uint16_t* a = (uint16_t*)malloc((size_t)topk * n_inter * sizeof(uint16_t));
+    orc_gemv_dense(router, router_is_f32, x, 1, n_experts, d_model, lg);
+    orc_route(lg, bias, 1, n_experts, topk, mode, eps, id, wt);
+    orc_gather_act(gate, up, n_inter, x, id, topk, a);
+    orc_down_combine(down, d_model, a, id, wt, topk, out);
+    if (logits) {
+        memcpy(logits, lg, n_experts * sizeof(float));
+    }
+    if (ids) {
+        memcpy(ids, id, topk * sizeof(uint32_t));
+    }
+    if (w) {
+        memcpy(w, wt, topk * sizeof(uint16_t));
+    }
+    if (act) {
+        memcpy(act, a, (size_t)topk * n_inter * sizeof(uint16_t));
+    }
+    free(a);
+    free(lg);
+}

@@ -1,0 +1,86 @@
+"""The C ABI on the CPU: the library loads, exports every declared symbol,
+and rejects bad arguments before touching the GPU runtime."""
+import ctypes
+
+import pytest
+
+from molten_amd import hip
+
+
+def test_library_exports_every_declared_symbol():
+    lib = hip.load()
+    names = hip.declared_functions()
+    assert len(names) > 10
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert missing == []
+    # and the Python binding covers every one of them
+    assert sorted(set(names) - set(hip._SIGNATURES)) == []
+
+
+def test_version():
+    assert b"gfx950" in hip.load().mh_version()
+
+
+def _qw(**kw):
+    base = dict(codes=0x1000, scales=0x2000, biases=0x3000, out_features=64, in_features=2048,
+                group_size=64, bits=4)
+    base.update(kw)
+    return hip.QuantWeights(base["codes"], base["scales"], base["biases"], base["out_features"],
+                            base["in_features"], base["group_size"], base["bits"])
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(bits=3), hip.MH_ERR_UNSUPPORTED),
+    (dict(bits=8), hip.MH_ERR_UNSUPPORTED),
+    (dict(group_size=48), hip.MH_ERR_UNSUPPORTED),
+    (dict(in_features=2000), hip.MH_ERR_INVALID),
+    (dict(out_features=0), hip.MH_ERR_INVALID),
+    (dict(codes=0x1008), hip.MH_ERR_ALIGN),
+    (dict(codes=None), hip.MH_ERR_INVALID),
+])
+def test_gemv_rejects_bad_weights(kw, code):
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.gemv_quant(_qw(**kw), 0x4000, 0x5000, stream=0)
+    assert ei.value.code == code
+    assert hip.load().mh_last_error()  # message set
+
+
+def test_gemv_rejects_bad_batch_and_pointers():
+    for batch in (0, 9):
+        with pytest.raises(hip.MoltenError) as ei:
+            hip.gemv_quant(_qw(), 0x4000, 0x5000, batch=batch, stream=0)
+        assert ei.value.code == hip.MH_ERR_UNSUPPORTED
+    with pytest.raises(hip.MoltenError):
+        hip.gemv_quant(_qw(), None, 0x5000, stream=0)
+    with pytest.raises(hip.MoltenError):
+        hip.gemv_quant(_qw(), 0x4000, None, stream=0)
+    # Q6 codes need 8-byte alignment only
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.gemv_quant(_qw(bits=6, codes=0x1004), 0x4000, 0x5000, stream=0)
+    assert ei.value.code == hip.MH_ERR_ALIGN
+
+
+def test_argmax_arguments():
+    with pytest.raises(hip.MoltenError):
+        hip.gemv_head_argmax(_qw(), 0x4000, None, stream=0)
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.gemv_quant_argmax(_qw(), 0x4000, 0x5000, 0x6004, stream=0)
+    assert ei.value.code == hip.MH_ERR_ALIGN
+    with pytest.raises(hip.MoltenError):  # done without ids
+        hip.gemv_quant_argmax(_qw(), 0x4000, 0x5000, 0x6000, done=0x7000, stream=0)
+    with pytest.raises(hip.MoltenError):
+        hip.token_tail(0x6000, 0x7000, batch=0, stream=0)
+    with pytest.raises(hip.MoltenError):
+        hip.argmax_bf16(0x4000, 0, 0x6000, 0x7000, stream=0)
+
+
+def test_bulk_dequant_needs_k_multiple_of_128():
+    with pytest.raises(hip.MoltenError):
+        hip.dequant_q4_bf16_bulk(_qw(in_features=64 * 3), 0x8000, stream=0)
+    with pytest.raises(hip.MoltenError):
+        hip.dequant_q4_bf16_bulk(_qw(bits=6), 0x8000, stream=0)
+
+
+def test_memcpy_kind_checked():
+    lib = hip.load()
+    assert lib.mh_memcpy(None, None, 0, 7, None) == hip.MH_ERR_INVALID

@@ -1,0 +1,150 @@
+"""GPU parity of the decode GEMV family through the C ABI (BASELINE configs
+1, 2 and 5).  The kernels follow the oracle's chunk order, so logits are
+compared bit for bit and argmax ids exactly."""
+import numpy as np
+import pytest
+import torch
+
+from molten_amd import hip, layout
+from tests.devutil import dev_quant, empty_dev, from_dev, to_dev, zeros_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+@pytest.mark.parametrize("bits", [4, 6])
+@pytest.mark.parametrize("n,k,batch", [
+    (2048, 2048, 1),   # config 1 shape
+    (1536, 2048, 1),   # expert gate/up shape
+    (2048, 1536, 1),   # expert down shape (48 live lanes)
+    (300, 2048, 1),    # ragged last row group
+    (96, 11776, 1),    # dense down shape: staged-x path
+    (512, 2048, 2),
+    (512, 2048, 8),    # config 5 batch
+    (130, 1536, 5),
+])
+def test_gemv_bit_exact(dev, orc, bits, n, k, batch):
+    _log(f"gemv bits={bits} n={n} k={k} batch={batch}")
+    rng = np.random.default_rng(n * 131 + k + batch + bits)
+    h = layout.synth_quant(rng, n, k, bits)
+    x = layout.synth_bf16(rng, (batch, k))
+    want = orc.gemv_quant(h, x, batch)
+    w, keep = dev_quant(h)
+    xd = to_dev(x)
+    y = empty_dev((batch, n), np.uint16)
+    hip.gemv_quant(w, xd, y, batch)
+    got = from_dev(y, np.uint16)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("bits", [4, 6])
+@pytest.mark.parametrize("gs", [32, 128])
+def test_gemv_other_group_sizes(dev, orc, bits, gs):
+    rng = np.random.default_rng(gs + bits)
+    h = layout.synth_quant(rng, 256, 2048, bits, group_size=gs)
+    x = layout.synth_bf16(rng, (1, 2048))
+    w, keep = dev_quant(h)
+    y = empty_dev((1, 256), np.uint16)
+    hip.gemv_quant(w, to_dev(x), y, 1)
+    np.testing.assert_array_equal(from_dev(y, np.uint16), orc.gemv_quant(h, x, 1))
+
+
+@pytest.mark.parametrize("bits,batch", [(4, 1), (6, 1), (6, 8), (4, 3)])
+def test_argmax_paths_agree_with_oracle(dev, orc, bits, batch):
+    _log(f"argmax bits={bits} batch={batch}")
+    rng = np.random.default_rng(77 + bits * 10 + batch)
+    n, k = 4096, 2048
+    h = layout.synth_quant(rng, n, k, bits)
+    x = layout.synth_bf16(rng, (batch, k))
+    logits = orc.gemv_quant(h, x, batch)
+    want = [orc.argmax_bf16(logits[b]) for b in range(batch)]
+    w, keep = dev_quant(h)
+    xd = to_dev(x)
+    # (1) stored logits + finisher ids, run twice to check the scratch is re-zeroed
+    y = empty_dev((batch, n), np.uint16)
+    best = zeros_dev((batch,), np.uint64)
+    done = zeros_dev((1,), np.uint32)
+    ids = empty_dev((batch,), np.uint32)
+    for _ in range(2):
+        hip.gemv_quant_argmax(w, xd, y, best, done, ids, batch)
+        assert from_dev(ids, np.uint32).tolist() == want
+        assert from_dev(best, np.uint64).tolist() == [0] * batch
+        assert from_dev(done, np.uint32).tolist() == [0]
+    np.testing.assert_array_equal(from_dev(y, np.uint16), logits)
+    # (2) reference pair: head argmax (no logits) + token tail
+    tok = empty_dev((batch,), np.uint32)
+    hip.gemv_head_argmax(w, xd, best, batch)
+    hip.token_tail(best, tok, batch)
+    assert from_dev(tok, np.uint32).tolist() == want
+    assert from_dev(best, np.uint64).tolist() == [0] * batch
+
+
+def test_argmax_ties_take_lowest_index(dev, orc):
+    # identical rows -> identical logits: the lowest row must win
+    rng = np.random.default_rng(5)
+    h = layout.synth_quant(rng, 8, 2048, 4)
+    rep = 700
+    hb = layout.HostQuant(np.tile(h.codes[3:4], (rep, 1)), np.tile(h.scales[3:4], (rep, 1)),
+                          np.tile(h.biases[3:4], (rep, 1)), rep, 2048, 64, 4)
+    # make rows 0..99 smaller by zeroing their codes
+    hb.codes[:100] = 0
+    x = layout.synth_bf16(rng, (1, 2048))
+    logits = orc.gemv_quant(hb, x, 1)[0]
+    want = orc.argmax_bf16(logits)
+    w, keep = dev_quant(hb)
+    best = zeros_dev((1,), np.uint64)
+    done = zeros_dev((1,), np.uint32)
+    ids = empty_dev((1,), np.uint32)
+    hip.gemv_quant_argmax(w, to_dev(x), None, best, done, ids, 1)
+    assert from_dev(ids, np.uint32)[0] == want
+
+
+def test_two_stage_argmax(dev, orc):
+    rng = np.random.default_rng(9)
+    for n in (1, 63, 64, 1000, 65536, 128000):
+        x = layout.synth_bf16(rng, (n,))
+        if n > 10:
+            x[n // 3] = x[n // 2] = layout.f32_to_bf16(np.float32([50.0]))[0]
+        partials = empty_dev((64 * 2,), np.uint32)
+        out = empty_dev((1,), np.uint32)
+        hip.argmax_bf16(to_dev(x), n, partials, out)
+        assert from_dev(out, np.uint32)[0] == orc.argmax_bf16(x)
+
+
+@pytest.mark.parametrize("bits", [4, 6])
+def test_dequant_bit_exact(dev, orc, bits):
+    rng = np.random.default_rng(bits)
+    h = layout.synth_quant(rng, 96, 2048, bits)
+    w, keep = dev_quant(h)
+    out = empty_dev((96, 2048), np.uint16)
+    hip.dequant_to_bf16(w, out)
+    np.testing.assert_array_equal(from_dev(out, np.uint16), orc.dequant_bf16(h))
+    if bits == 4:
+        out.zero_()
+        hip.dequant_q4_bf16_bulk(w, out)
+        np.testing.assert_array_equal(from_dev(out, np.uint16), orc.dequant_bf16(h))
+
+
+@pytest.mark.parametrize("bits,batch", [(4, 1), (6, 1), (6, 8)])
+def test_lm_head_full_size(dev, orc, bits, batch):
+    """Configs 2 and 5 at their full 65536 x 2048 shape: every logit is
+    bit-exact against the oracle and the ids are the oracle's argmax."""
+    _log(f"lm head full bits={bits} batch={batch}")
+    rng = np.random.default_rng(2026 + bits + batch)
+    n, k = 65536, 2048
+    h = layout.synth_quant(rng, n, k, bits)
+    x = layout.synth_bf16(rng, (batch, k))
+    w, keep = dev_quant(h)
+    y = empty_dev((batch, n), np.uint16)
+    best = zeros_dev((batch,), np.uint64)
+    done = zeros_dev((1,), np.uint32)
+    ids = empty_dev((batch,), np.uint32)
+    hip.gemv_quant_argmax(w, to_dev(x), y, best, done, ids, batch)
+    got = from_dev(y, np.uint16)
+    got_ids = from_dev(ids, np.uint32)
+    want = orc.gemv_quant(h, x, batch)
+    np.testing.assert_array_equal(got, want)
+    assert got_ids.tolist() == [orc.argmax_bf16(want[b]) for b in range(batch)]
