@@ -52,6 +52,15 @@ const char* mh_last_error(void);
 /* Library version, e.g. "molten-hip 0.1.0 gfx950". */
 const char* mh_version(void);
 
+/* Routing rule of the top-k (lfm.metal:541-703): MH_ROUTE_SIGMOID_BIAS is
+ * molten's (rank on sigmoid(z) + bias, weights s_r / (eps + sum s));
+ * MH_ROUTE_SOFTMAX ranks on the logits and renormalises the softmax over the
+ * chosen experts.  Ties go to the lower expert id in both. */
+enum { MH_ROUTE_SIGMOID_BIAS = 0, MH_ROUTE_SOFTMAX = 1 };
+
+/* Element type of a dense router matrix. */
+enum { MH_DTYPE_F32 = 0, MH_DTYPE_BF16 = 1 };
+
 typedef void* mh_stream_t; /* hipStream_t */
 typedef void* mh_event_t;  /* hipEvent_t  */
 
@@ -127,6 +136,73 @@ int mh_token_tail(uint64_t* best, uint32_t* out_tok, uint32_t batch, mh_stream_t
  * ties to the lowest index.  partials: scratch of >= 64*8 bytes. */
 int mh_argmax_bf16(const uint16_t* x, uint32_t n, void* partials, uint32_t* out,
                    mh_stream_t stream);
+
+/* ------------------------------------------------- router / routing ---
+ * src/kernels/lfm.rs:314 gemv_f32: y[e] = W[e, :] . x, W f32 [n, k], x bf16
+ * [k], y f32 [n], chunk order (so expert ids are reproducible bit for bit). */
+int mh_gemv_f32(const float* w, const uint16_t* x, float* y, uint32_t n, uint32_t k,
+                mh_stream_t stream);
+/* The same with a bf16 router matrix (BASELINE config 3's router). */
+int mh_gemv_bf16(const uint16_t* w, const uint16_t* x, float* y, uint32_t n, uint32_t k,
+                 mh_stream_t stream);
+
+/* src/kernels/lfm.rs:391 route_token: top-k of one token's logits [e] ->
+ * ids u32 [topk], weights bf16 [topk].  bias f32 [e] (may be NULL = 0) is
+ * used by MH_ROUTE_SIGMOID_BIAS only.  e <= 256, topk <= 8. */
+int mh_route_token(const float* logits, const float* bias, uint32_t* ids, uint16_t* weights,
+                   uint32_t e, uint32_t topk, int mode, float eps, mh_stream_t stream);
+
+/* src/kernels/lfm.rs:266 router_addnorm_route without the residual add +
+ * RMSNorm prologue: router GEMV (x already normalised) and top-k in one
+ * launch; the last workgroup to finish routes.  logits f32 [e] are written
+ * too.  counter: one u32, zero on entry, left zero. */
+int mh_router_route(const void* w, int w_dtype, const uint16_t* x, float* logits,
+                    const float* bias, uint32_t* ids, uint16_t* weights, uint32_t* counter,
+                    uint32_t e, uint32_t k, uint32_t topk, int mode, float eps,
+                    mh_stream_t stream);
+
+/* ------------------------------------------------- decode experts ---
+ * src/kernels/lfm.rs:421 gemv_gather_act: for slot r < topk and row
+ * j < n_inter, act[r, j] = bf16(bf16(silu(g)) * u) with g, u the bf16 gate
+ * and up rows ids[r]*n_inter + j of the stacked matrices against x.
+ * in_features <= 2048, 4-bit weights. */
+int mh_gemv_gather_act(const mh_quant_weights* gate, const mh_quant_weights* up,
+                       const uint16_t* x, const uint32_t* ids, uint16_t* act, uint32_t topk,
+                       uint32_t n_inter, mh_stream_t stream);
+
+/* src/kernels/lfm.rs:464 gemv_gu_act: the dense (unrouted) form, act[j]. */
+int mh_gemv_gu_act(const mh_quant_weights* gate, const mh_quant_weights* up, const uint16_t* x,
+                   uint16_t* act, mh_stream_t stream);
+
+/* src/kernels/lfm.rs:499 gemv_gather_down_combine4: p_r = bf16(down row
+ * ids[r]*n_out + i . act[r]); out[i] = bf16(sum_r bf16(w_r * p_r)), r
+ * ascending.  topk 1..4, in_features <= 2048, 4-bit weights. */
+int mh_gemv_gather_down_combine(const mh_quant_weights* down, const uint16_t* act,
+                                const uint32_t* ids, const uint16_t* weights, uint16_t* out,
+                                uint32_t topk, uint32_t n_out, mh_stream_t stream);
+
+/* One MoE decode step (src/lfm.rs:967-1011 moe_decode with the routing of
+ * :266): router GEMV + top-k -> gate/up + SwiGLU -> down + combine.
+ * Stacked experts: gate/up [E*n_inter, d_model], down [E*d_model, n_inter].
+ * logits f32 [E], ids [topk], weights bf16 [topk], act bf16 [topk, n_inter]
+ * are written as intermediates; counter: one u32, zero on entry, left zero. */
+int mh_moe_decode(const void* router, int router_dtype, const float* bias, int mode, float eps,
+                  const mh_quant_weights* gate, const mh_quant_weights* up,
+                  const mh_quant_weights* down, uint32_t n_experts, uint32_t topk,
+                  const uint16_t* x, uint16_t* out, float* logits, uint32_t* ids,
+                  uint16_t* weights, uint16_t* act, uint32_t* counter, mh_stream_t stream);
+
+/* ------------------------------------------------- prefill routing ---
+ * src/kernels/lfm.rs:366 router_prefill: logits f32 [m, e] = x [m, k] W^T,
+ * W f32 or bf16 [e, k], chunk order. */
+int mh_router_prefill(const uint16_t* x, const void* w, int w_dtype, float* out, uint32_t m,
+                      uint32_t k, uint32_t e, mh_stream_t stream);
+
+/* src/kernels/lfm.rs:536 moe_route_batch: route_token for m tokens; ids u32
+ * [m, topk], gw bf16 [m, topk]. */
+int mh_moe_route_batch(const float* logits, const float* bias, uint32_t* ids, uint16_t* gw,
+                       uint32_t m, uint32_t e, uint32_t topk, int mode, float eps,
+                       mh_stream_t stream);
 
 #ifdef __cplusplus
 }

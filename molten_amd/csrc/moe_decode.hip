@@ -1,0 +1,655 @@
+// moe_decode.hip -- router GEMVs, top-k routing and the decode MoE expert
+// GEMVs for gfx950.
+//
+// Replaces lfm.metal:368-428 (router GEMV), :464-537 (prefill router),
+// :541-703 (top-k), :705-855 (fused router + route, minus the add+RMSNorm
+// prologue), :1392-1554 (expert gate/up + SwiGLU, dense gate/up, expert down
+// + combine) and :1558-1602 (batch routing).
+//
+// All dot products use the chunk order of mh_device.hpp, so router logits
+// (and hence expert ids) and every expert output are bit-identical to the CPU
+// oracle.
+#include "mh_device.hpp"
+#include "mh_host.hpp"
+#include "mh_route.hpp"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / mh::kWave;
+constexpr int kXPitch = 36;
+
+// ------------------------------------------------------------ dense GEMV ---
+// y[t, e] = chunk-order dot(W[e, :], x[t, :]) for a tile of TT tokens per
+// workgroup (x staged once in LDS) and EPW experts per wave.
+
+template <typename WT>
+__device__ __forceinline__ void load_wchunk(const WT* w, float (&wr)[32]);
+
+template <>
+__device__ __forceinline__ void load_wchunk<float>(const float* w, float (&wr)[32]) {
+    const float4* p = reinterpret_cast<const float4*>(w);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const float4 v = p[q];
+        wr[4 * q] = v.x; wr[4 * q + 1] = v.y; wr[4 * q + 2] = v.z; wr[4 * q + 3] = v.w;
+    }
+}
+
+template <>
+__device__ __forceinline__ void load_wchunk<uint16_t>(const uint16_t* w, float (&wr)[32]) {
+    const uint4* p = reinterpret_cast<const uint4*>(w);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint4 v = p[q];
+        const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            wr[8 * q + 2 * j] = mh::bf16lo(u[j]);
+            wr[8 * q + 2 * j + 1] = mh::bf16hi(u[j]);
+        }
+    }
+}
+
+struct DenseArgs {
+    const void* w;     // [n, k] f32 or bf16
+    const uint16_t* x; // bf16 [m, k]
+    float* y;          // f32 [m, n]
+    uint32_t m, n, k;
+    // fused routing (decode): when done != null the last workgroup routes
+    const float* bias;
+    uint32_t* ids;
+    uint16_t* weights;
+    uint32_t* done;
+    uint32_t topk;
+    int mode;
+    float eps;
+};
+
+// Stage x rows [t0, t0 + nt) into LDS as padded f32 chunks.
+__device__ inline void stage_x(const uint16_t* x, uint32_t t0, uint32_t nt, uint32_t k,
+                               float* xl, int tt) {
+    const uint32_t C = k / 32u;
+    for (uint32_t i = threadIdx.x; i < static_cast<uint32_t>(tt) * C * 16u; i += kThreads) {
+        const uint32_t t = i / (C * 16u), rem = i % (C * 16u);
+        const uint32_t c = rem / 16u, q = rem % 16u;
+        uint32_t u = 0;
+        if (t < nt) {
+            const uint16_t* xp = x + static_cast<size_t>(t0 + t) * k + 32u * c + 2u * q;
+            u = static_cast<uint32_t>(xp[0]) | (static_cast<uint32_t>(xp[1]) << 16);
+        }
+        float* d = xl + (static_cast<size_t>(t) * C + c) * kXPitch + 2u * q;
+        d[0] = mh::bf16lo(u);
+        d[1] = mh::bf16hi(u);
+    }
+}
+
+template <typename WT, int TT, int EPW>
+__global__ __launch_bounds__(kThreads) void k_dense_gemv(DenseArgs a) {
+    extern __shared__ float xl[];  // [TT][C][kXPitch]
+    __shared__ uint32_t last;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t C = a.k / 32u;
+    const uint32_t t0 = blockIdx.x * TT;
+    const uint32_t nt = min(static_cast<uint32_t>(TT), a.m - t0);
+    stage_x(a.x, t0, nt, a.k, xl, TT);
+    __syncthreads();
+    const WT* w = static_cast<const WT*>(a.w);
+#pragma unroll 1
+    for (int j = 0; j < EPW; ++j) {
+        const uint32_t e = (blockIdx.y * kWaves + wave) * EPW + j;
+        if (e >= a.n) {
+            break;
+        }
+        float acc[TT];
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            acc[t] = 0.0f;
+        }
+        for (uint32_t c = lane; c < C; c += 64) {
+            float wr[32];
+            load_wchunk<WT>(w + static_cast<size_t>(e) * a.k + 32u * c, wr);
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                const float4* xs = reinterpret_cast<const float4*>(xl + (static_cast<size_t>(t) * C + c) * kXPitch);
+                float p = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const float4 v = xs[q];
+                    p = __builtin_fmaf(wr[4 * q], v.x, p);
+                    p = __builtin_fmaf(wr[4 * q + 1], v.y, p);
+                    p = __builtin_fmaf(wr[4 * q + 2], v.z, p);
+                    p = __builtin_fmaf(wr[4 * q + 3], v.w, p);
+                }
+                acc[t] = acc[t] + p;
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            const float v = mh::lane63(mh::wave_sum_lane63(acc[t]));
+            if (lane == 0 && static_cast<uint32_t>(t) < nt) {
+                float* dst = a.y + static_cast<size_t>(t0 + t) * a.n + e;
+                if (a.done != nullptr) {
+                    // published with a returning atomic so the finisher below
+                    // reads it from the coherence point without a cache flush
+                    const uint32_t old = __hip_atomic_exchange(
+                        reinterpret_cast<uint32_t*>(dst), __float_as_uint(v), __ATOMIC_RELAXED,
+                        __HIP_MEMORY_SCOPE_AGENT);
+                    if (old == 0x7fc00001u) {
+                        last = 0;
+                    }
+                } else {
+                    *dst = v;
+                }
+            }
+        }
+    }
+    if (a.done == nullptr) {
+        return;
+    }
+    // Fused decode routing: the last workgroup to finish routes token 0.
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t total = gridDim.x * gridDim.y;
+        const uint32_t prev =
+            __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = (prev == total - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!last) {
+        return;
+    }
+    __shared__ float s[mh::kMaxExperts], cand[mh::kMaxExperts];
+    __shared__ unsigned char used[mh::kMaxExperts];
+    for (uint32_t i = threadIdx.x; i < a.n; i += kThreads) {
+        const float z = __uint_as_float(__hip_atomic_fetch_or(reinterpret_cast<uint32_t*>(a.y) + i,
+                                                              0u, __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT));
+        mh::route_score(z, a.bias ? a.bias[i] : 0.0f, a.mode, s[i], cand[i]);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        mh::route_select(s, cand, used, a.n, a.topk, a.mode, a.eps, a.ids, a.weights);
+        __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+template <typename WT, int TT, int EPW>
+int launch_dense(const DenseArgs& a, hipStream_t stream) {
+    const uint32_t C = a.k / 32u;
+    const size_t lds = static_cast<size_t>(TT) * C * kXPitch * sizeof(float);
+    const uint32_t per_wg = kWaves * EPW;
+    const dim3 grid((a.m + TT - 1) / TT, (a.n + per_wg - 1) / per_wg);
+    if (lds > 64u * 1024u) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dense_gemv<WT, TT, EPW>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 static_cast<int>(lds));
+        if (e != hipSuccess) {
+            return mh::hip_error(e, "k_dense_gemv: LDS attribute");
+        }
+    }
+    hipLaunchKernelGGL((k_dense_gemv<WT, TT, EPW>), grid, dim3(kThreads), lds, stream, a);
+    return mh::launch_status("k_dense_gemv");
+}
+
+template <typename WT>
+int dispatch_dense(const DenseArgs& a, hipStream_t stream) {
+    if (a.m == 1) {
+        return launch_dense<WT, 1, 1>(a, stream);
+    }
+    return launch_dense<WT, 8, 4>(a, stream);
+}
+
+int dense_common(const char* op, const void* w, bool w_f32, const uint16_t* x, float* y,
+                 uint32_t m, uint32_t n, uint32_t k, DenseArgs& a) {
+    MH_ENSURE(w && x && y, MH_ERR_INVALID, "%s: NULL argument", op);
+    MH_ENSURE(m > 0 && n > 0 && k > 0, MH_ERR_INVALID, "%s: empty shape m=%u n=%u k=%u", op, m, n, k);
+    MH_ENSURE(k % 32 == 0, MH_ERR_UNSUPPORTED, "%s: K=%u is not a multiple of 32", op, k);
+    MH_ENSURE(static_cast<size_t>(8) * (k / 32) * kXPitch * 4 <= 160u * 1024u, MH_ERR_UNSUPPORTED,
+              "%s: K=%u too large for the LDS tile", op, k);
+    MH_ENSURE(mh::aligned(w, 16) && mh::aligned(x, 4) && mh::aligned(y, 4), MH_ERR_ALIGN,
+              "%s: W must be 16-byte aligned, x and y 4-byte aligned", op);
+    (void)w_f32;
+    a = DenseArgs{};
+    a.w = w;
+    a.x = x;
+    a.y = y;
+    a.m = m;
+    a.n = n;
+    a.k = k;
+    return MH_OK;
+}
+
+// ------------------------------------------------------------ top-k route ---
+
+__global__ __launch_bounds__(64) void k_route(const float* logits, const float* bias,
+                                              uint32_t* ids, uint16_t* w, uint32_t e,
+                                              uint32_t topk, int mode, float eps) {
+    __shared__ float s[mh::kMaxExperts], cand[mh::kMaxExperts];
+    __shared__ unsigned char used[mh::kMaxExperts];
+    const uint32_t t = blockIdx.x;
+    for (uint32_t i = threadIdx.x; i < e; i += 64) {
+        mh::route_score(logits[static_cast<size_t>(t) * e + i], bias ? bias[i] : 0.0f, mode, s[i],
+                        cand[i]);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        mh::route_select(s, cand, used, e, topk, mode, eps, ids + static_cast<size_t>(t) * topk,
+                         w + static_cast<size_t>(t) * topk);
+    }
+}
+
+int route_checks(const char* op, const float* logits, uint32_t* ids, uint16_t* w, uint32_t m,
+                 uint32_t e, uint32_t topk, int mode) {
+    MH_ENSURE(logits && ids && w, MH_ERR_INVALID, "%s: NULL argument", op);
+    MH_ENSURE(m > 0, MH_ERR_INVALID, "%s: no tokens", op);
+    MH_ENSURE(e >= 1 && e <= static_cast<uint32_t>(mh::kMaxExperts), MH_ERR_UNSUPPORTED,
+              "%s: %u experts (1..%d supported)", op, e, mh::kMaxExperts);
+    MH_ENSURE(topk >= 1 && topk <= e && topk <= static_cast<uint32_t>(mh::kMaxTopk),
+              MH_ERR_INVALID, "%s: topk %u not in 1..min(%u, %d)", op, topk, e, mh::kMaxTopk);
+    MH_ENSURE(mode == MH_ROUTE_SIGMOID_BIAS || mode == MH_ROUTE_SOFTMAX, MH_ERR_INVALID,
+              "%s: unknown routing mode %d", op, mode);
+    return MH_OK;
+}
+
+// --------------------------------------------------- expert gate/up act ---
+
+struct ActArgs {
+    const uint32_t* gc; const uint16_t* gsc; const uint16_t* gbi;
+    const uint32_t* uc; const uint16_t* usc; const uint16_t* ubi;
+    const uint16_t* x;
+    const uint32_t* ids;  // [slots] or null (dense)
+    uint16_t* act;        // [slots, n_inter]
+    uint32_t slots, n_inter, n_experts, k, gs, row_words, groups;
+};
+
+struct ActLoad {
+    mh::Chunk<4> g, u;
+    float gs, gb, us, ub;
+};
+
+__device__ __forceinline__ void load_act_row(const ActArgs& a, uint32_t v, int lane, bool live,
+                                             ActLoad& o) {
+    const uint32_t vv = min(v, a.slots * a.n_inter - 1);
+    const uint32_t slot = vv / a.n_inter, j = vv % a.n_inter;
+    uint32_t e = a.ids ? a.ids[slot] : 0u;
+    e = e < a.n_experts ? e : 0u;  // an out-of-range id reads expert 0, never past W
+    const size_t row = static_cast<size_t>(e) * a.n_inter + j;
+    if (live) {
+        o.g.load(a.gc + row * a.row_words + 4u * lane);
+        o.u.load(a.uc + row * a.row_words + 4u * lane);
+        const uint32_t g = (32u * lane) / a.gs;
+        o.gs = mh::bf16_to_f32(a.gsc[row * a.groups + g]);
+        o.gb = mh::bf16_to_f32(a.gbi[row * a.groups + g]);
+        o.us = mh::bf16_to_f32(a.usc[row * a.groups + g]);
+        o.ub = mh::bf16_to_f32(a.ubi[row * a.groups + g]);
+    } else {
+        o.g.zero();
+        o.u.zero();
+        o.gs = o.gb = o.us = o.ub = 0.0f;
+    }
+}
+
+// x (K <= 2048) in registers; each wave takes R virtual rows (slot, j) at a
+// time, both matrices, with the next group's loads in flight.
+template <int R>
+__global__ __launch_bounds__(kThreads) void k_gather_act(ActArgs a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t C = a.k / 32u;
+    const bool live = lane < static_cast<int>(C);
+    float xr[32];
+    float xs = 0.0f;
+    {
+        const uint16_t* xp = a.x + 32u * (live ? lane : 0);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const uint32_t u = static_cast<uint32_t>(xp[2 * q]) | (static_cast<uint32_t>(xp[2 * q + 1]) << 16);
+            const float lo = mh::bf16lo(u), hi = mh::bf16hi(u);
+            xs = xs + lo;
+            xs = xs + hi;
+            xr[2 * q] = mh::prep_x<4>(lo, 2 * q);
+            xr[2 * q + 1] = mh::prep_x<4>(hi, 2 * q + 1);
+        }
+    }
+    const uint32_t rows = a.slots * a.n_inter;
+    const uint32_t n_rg = (rows + R - 1) / R;
+    const uint32_t stride = gridDim.x * kWaves;
+    uint32_t rg = blockIdx.x * kWaves + wave;
+    ActLoad cur[R];
+    if (rg < n_rg) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) load_act_row(a, rg * R + r, lane, live, cur[r]);
+    }
+    while (rg < n_rg) {
+        const uint32_t next = rg + stride;
+        ActLoad nxt[R];
+        if (next < n_rg) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) load_act_row(a, next * R + r, lane, live, nxt[r]);
+        }
+        uint16_t mine = 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float pg = cur[r].g.dot(xr);
+            const float pu = cur[r].u.dot(xr);
+            const float hg = __builtin_fmaf(cur[r].gs, pg, cur[r].gb * xs);
+            const float hu = __builtin_fmaf(cur[r].us, pu, cur[r].ub * xs);
+            const float gsum = mh::lane63(mh::wave_sum_lane63(live ? 0.0f + hg : 0.0f));
+            const float usum = mh::lane63(mh::wave_sum_lane63(live ? 0.0f + hu : 0.0f));
+            const float g = mh::round_bf16(gsum);
+            const float u = mh::round_bf16(usum);
+            const uint16_t v = mh::f32_to_bf16(mh::silu_bf16(g) * u);
+            if (lane == r) {
+                mine = v;
+            }
+        }
+        const uint32_t my = rg * R + lane;
+        if (lane < R && my < rows) {
+            a.act[my] = mine;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) cur[r] = nxt[r];
+        rg = next;
+    }
+}
+
+int launch_gather_act(const ActArgs& a, hipStream_t stream) {
+    constexpr int R = 2;
+    const uint32_t n_rg = (a.slots * a.n_inter + R - 1) / R;
+    const uint32_t want = (n_rg + kWaves - 1) / kWaves;
+    const uint32_t cap = static_cast<uint32_t>(mh::cu_count()) * 4u;
+    hipLaunchKernelGGL(k_gather_act<R>, dim3(want < cap ? want : cap), dim3(kThreads), 0, stream, a);
+    return mh::launch_status("k_gather_act");
+}
+
+int act_common(const char* op, const mh_quant_weights* gate, const mh_quant_weights* up,
+               const uint16_t* x, const uint32_t* ids, uint16_t* act, uint32_t slots,
+               uint32_t n_inter, ActArgs& a) {
+    MH_TRY(mh::check_quant(gate, op));
+    MH_TRY(mh::check_quant(up, op));
+    MH_ENSURE(x && act, MH_ERR_INVALID, "%s: NULL argument", op);
+    MH_ENSURE(gate->bits == 4 && up->bits == 4, MH_ERR_UNSUPPORTED, "%s: expert GEMVs are 4-bit", op);
+    MH_ENSURE(gate->out_features == up->out_features && gate->in_features == up->in_features &&
+                  gate->group_size == up->group_size,
+              MH_ERR_INVALID, "%s: gate/up shapes differ", op);
+    MH_ENSURE(gate->in_features <= 2048, MH_ERR_UNSUPPORTED,
+              "%s: in_features %u > 2048 (x is held in registers)", op, gate->in_features);
+    MH_ENSURE(n_inter > 0 && gate->out_features % n_inter == 0, MH_ERR_INVALID,
+              "%s: %u stacked rows are not a multiple of n_inter %u", op, gate->out_features, n_inter);
+    MH_ENSURE(slots >= 1 && slots <= static_cast<uint32_t>(mh::kMaxTopk), MH_ERR_INVALID,
+              "%s: %u slots not in 1..%d", op, slots, mh::kMaxTopk);
+    MH_ENSURE(mh::aligned(x, 2) && mh::aligned(act, 2), MH_ERR_ALIGN, "%s: x/act alignment", op);
+    a = ActArgs{};
+    a.gc = gate->codes; a.gsc = gate->scales; a.gbi = gate->biases;
+    a.uc = up->codes; a.usc = up->scales; a.ubi = up->biases;
+    a.x = x;
+    a.ids = ids;
+    a.act = act;
+    a.slots = slots;
+    a.n_inter = n_inter;
+    a.n_experts = gate->out_features / n_inter;
+    a.k = gate->in_features;
+    a.gs = gate->group_size;
+    a.row_words = gate->in_features / 8u;
+    a.groups = gate->in_features / gate->group_size;
+    return MH_OK;
+}
+
+// --------------------------------------------------- expert down+combine ---
+
+struct DownArgs {
+    const uint32_t* codes; const uint16_t* scales; const uint16_t* biases;
+    const uint16_t* act;      // bf16 [topk, k]
+    const uint32_t* ids;      // [topk]
+    const uint16_t* weights;  // bf16 [topk]
+    uint16_t* out;            // bf16 [n_out]
+    uint32_t n_out, n_experts, k, gs, row_words, groups;
+};
+
+template <int TK>
+__global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t C = a.k / 32u;
+    const bool live = lane < static_cast<int>(C);
+    float xr[TK][32];
+    float xs[TK];
+    uint32_t e[TK];
+    float wt[TK];
+#pragma unroll
+    for (int r = 0; r < TK; ++r) {
+        const uint16_t* xp = a.act + static_cast<size_t>(r) * a.k + 32u * (live ? lane : 0);
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const uint32_t u = static_cast<uint32_t>(xp[2 * q]) | (static_cast<uint32_t>(xp[2 * q + 1]) << 16);
+            const float lo = mh::bf16lo(u), hi = mh::bf16hi(u);
+            s = s + lo;
+            s = s + hi;
+            xr[r][2 * q] = mh::prep_x<4>(lo, 2 * q);
+            xr[r][2 * q + 1] = mh::prep_x<4>(hi, 2 * q + 1);
+        }
+        xs[r] = s;
+        const uint32_t id = a.ids[r];
+        e[r] = id < a.n_experts ? id : 0u;
+        wt[r] = mh::bf16_to_f32(a.weights[r]);
+    }
+    auto load = [&](uint32_t i, mh::Chunk<4>(&ch)[TK], float(&s)[TK], float(&b)[TK]) {
+#pragma unroll
+        for (int r = 0; r < TK; ++r) {
+            const size_t row = static_cast<size_t>(e[r]) * a.n_out + min(i, a.n_out - 1);
+            if (live) {
+                ch[r].load(a.codes + row * a.row_words + 4u * lane);
+                const uint32_t g = (32u * lane) / a.gs;
+                s[r] = mh::bf16_to_f32(a.scales[row * a.groups + g]);
+                b[r] = mh::bf16_to_f32(a.biases[row * a.groups + g]);
+            } else {
+                ch[r].zero();
+                s[r] = b[r] = 0.0f;
+            }
+        }
+    };
+    const uint32_t stride = gridDim.x * kWaves;
+    uint32_t i = blockIdx.x * kWaves + wave;
+    mh::Chunk<4> cur[TK];
+    float cs[TK], cb[TK];
+    if (i < a.n_out) load(i, cur, cs, cb);
+    while (i < a.n_out) {
+        const uint32_t next = i + stride;
+        mh::Chunk<4> nxt[TK];
+        float ns[TK], nb[TK];
+        if (next < a.n_out) load(next, nxt, ns, nb);
+        float total = 0.0f;
+#pragma unroll
+        for (int r = 0; r < TK; ++r) {
+            const float p = cur[r].dot(xr[r]);
+            const float h = __builtin_fmaf(cs[r], p, cb[r] * xs[r]);
+            const float v = mh::round_bf16(mh::lane63(mh::wave_sum_lane63(live ? 0.0f + h : 0.0f)));
+            total = total + mh::round_bf16(wt[r] * v);
+        }
+        if (lane == 0) {
+            a.out[i] = mh::f32_to_bf16(total);
+        }
+#pragma unroll
+        for (int r = 0; r < TK; ++r) {
+            cur[r] = nxt[r];
+            cs[r] = ns[r];
+            cb[r] = nb[r];
+        }
+        i = next;
+    }
+}
+
+int launch_down(const DownArgs& a, uint32_t topk, hipStream_t stream) {
+    const uint32_t want = (a.n_out + kWaves - 1) / kWaves;
+    const uint32_t cap = static_cast<uint32_t>(mh::cu_count()) * 4u;
+    const dim3 grid(want < cap ? want : cap);
+    switch (topk) {
+        case 1: hipLaunchKernelGGL(k_down_combine<1>, grid, dim3(kThreads), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL(k_down_combine<2>, grid, dim3(kThreads), 0, stream, a); break;
+        case 3: hipLaunchKernelGGL(k_down_combine<3>, grid, dim3(kThreads), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL(k_down_combine<4>, grid, dim3(kThreads), 0, stream, a); break;
+        default: return mh::set_error(MH_ERR_UNSUPPORTED, "down combine: topk %u not in 1..4", topk);
+    }
+    return mh::launch_status("k_down_combine");
+}
+
+int down_common(const char* op, const mh_quant_weights* down, const uint16_t* act,
+                const uint32_t* ids, const uint16_t* weights, uint16_t* out, uint32_t topk,
+                uint32_t n_out, DownArgs& a) {
+    MH_TRY(mh::check_quant(down, op));
+    MH_ENSURE(act && ids && weights && out, MH_ERR_INVALID, "%s: NULL argument", op);
+    MH_ENSURE(down->bits == 4, MH_ERR_UNSUPPORTED, "%s: expert GEMVs are 4-bit", op);
+    MH_ENSURE(topk >= 1 && topk <= 4, MH_ERR_UNSUPPORTED, "%s: topk %u not in 1..4", op, topk);
+    MH_ENSURE(down->in_features <= 2048, MH_ERR_UNSUPPORTED,
+              "%s: in_features %u > 2048 (act is held in registers)", op, down->in_features);
+    MH_ENSURE(n_out > 0 && down->out_features % n_out == 0, MH_ERR_INVALID,
+              "%s: %u stacked rows are not a multiple of n_out %u", op, down->out_features, n_out);
+    MH_ENSURE(mh::aligned(act, 2) && mh::aligned(out, 2), MH_ERR_ALIGN, "%s: alignment", op);
+    a = DownArgs{};
+    a.codes = down->codes; a.scales = down->scales; a.biases = down->biases;
+    a.act = act;
+    a.ids = ids;
+    a.weights = weights;
+    a.out = out;
+    a.n_out = n_out;
+    a.n_experts = down->out_features / n_out;
+    a.k = down->in_features;
+    a.gs = down->group_size;
+    a.row_words = down->in_features / 8u;
+    a.groups = down->in_features / down->group_size;
+    return MH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mh_gemv_f32(const float* w, const uint16_t* x, float* y, uint32_t n, uint32_t k,
+                mh_stream_t stream) {
+    DenseArgs a;
+    MH_TRY(dense_common("mh_gemv_f32", w, true, x, y, 1, n, k, a));
+    return dispatch_dense<float>(a, mh::as_stream(stream));
+}
+
+int mh_gemv_bf16(const uint16_t* w, const uint16_t* x, float* y, uint32_t n, uint32_t k,
+                 mh_stream_t stream) {
+    DenseArgs a;
+    MH_TRY(dense_common("mh_gemv_bf16", w, false, x, y, 1, n, k, a));
+    return dispatch_dense<uint16_t>(a, mh::as_stream(stream));
+}
+
+int mh_router_prefill(const uint16_t* x, const void* w, int w_dtype, float* out, uint32_t m,
+                      uint32_t k, uint32_t e, mh_stream_t stream) {
+    MH_ENSURE(w_dtype == MH_DTYPE_F32 || w_dtype == MH_DTYPE_BF16, MH_ERR_INVALID,
+              "mh_router_prefill: router dtype %d", w_dtype);
+    DenseArgs a;
+    MH_TRY(dense_common("mh_router_prefill", w, w_dtype == MH_DTYPE_F32, x, out, m, e, k, a));
+    return w_dtype == MH_DTYPE_F32 ? dispatch_dense<float>(a, mh::as_stream(stream))
+                                   : dispatch_dense<uint16_t>(a, mh::as_stream(stream));
+}
+
+int mh_route_token(const float* logits, const float* bias, uint32_t* ids, uint16_t* weights,
+                   uint32_t e, uint32_t topk, int mode, float eps, mh_stream_t stream) {
+    MH_TRY(route_checks("mh_route_token", logits, ids, weights, 1, e, topk, mode));
+    hipLaunchKernelGGL(k_route, dim3(1), dim3(64), 0, mh::as_stream(stream), logits, bias, ids,
+                       weights, e, topk, mode, eps);
+    return mh::launch_status("mh_route_token");
+}
+
+int mh_moe_route_batch(const float* logits, const float* bias, uint32_t* ids, uint16_t* gw,
+                       uint32_t m, uint32_t e, uint32_t topk, int mode, float eps,
+                       mh_stream_t stream) {
+    MH_TRY(route_checks("mh_moe_route_batch", logits, ids, gw, m, e, topk, mode));
+    hipLaunchKernelGGL(k_route, dim3(m), dim3(64), 0, mh::as_stream(stream), logits, bias, ids, gw,
+                       e, topk, mode, eps);
+    return mh::launch_status("mh_moe_route_batch");
+}
+
+int mh_router_route(const void* w, int w_dtype, const uint16_t* x, float* logits,
+                    const float* bias, uint32_t* ids, uint16_t* weights, uint32_t* counter,
+                    uint32_t e, uint32_t k, uint32_t topk, int mode, float eps,
+                    mh_stream_t stream) {
+    MH_ENSURE(w_dtype == MH_DTYPE_F32 || w_dtype == MH_DTYPE_BF16, MH_ERR_INVALID,
+              "mh_router_route: router dtype %d", w_dtype);
+    MH_ENSURE(counter != nullptr, MH_ERR_INVALID, "mh_router_route: counter is NULL");
+    MH_TRY(route_checks("mh_router_route", logits, ids, weights, 1, e, topk, mode));
+    DenseArgs a;
+    MH_TRY(dense_common("mh_router_route", w, w_dtype == MH_DTYPE_F32, x, logits, 1, e, k, a));
+    a.bias = bias;
+    a.ids = ids;
+    a.weights = weights;
+    a.done = counter;
+    a.topk = topk;
+    a.mode = mode;
+    a.eps = eps;
+    return w_dtype == MH_DTYPE_F32 ? launch_dense<float, 1, 1>(a, mh::as_stream(stream))
+                                   : launch_dense<uint16_t, 1, 1>(a, mh::as_stream(stream));
+}
+
+int mh_gemv_gather_act(const mh_quant_weights* gate, const mh_quant_weights* up,
+                       const uint16_t* x, const uint32_t* ids, uint16_t* act, uint32_t topk,
+                       uint32_t n_inter, mh_stream_t stream) {
+    MH_ENSURE(ids != nullptr, MH_ERR_INVALID, "mh_gemv_gather_act: ids is NULL");
+    ActArgs a;
+    MH_TRY(act_common("mh_gemv_gather_act", gate, up, x, ids, act, topk, n_inter, a));
+    return launch_gather_act(a, mh::as_stream(stream));
+}
+
+int mh_gemv_gu_act(const mh_quant_weights* gate, const mh_quant_weights* up, const uint16_t* x,
+                   uint16_t* act, mh_stream_t stream) {
+    MH_ENSURE(gate != nullptr, MH_ERR_INVALID, "mh_gemv_gu_act: gate is NULL");
+    ActArgs a;
+    MH_TRY(act_common("mh_gemv_gu_act", gate, up, x, nullptr, act, 1, gate->out_features, a));
+    return launch_gather_act(a, mh::as_stream(stream));
+}
+
+int mh_gemv_gather_down_combine(const mh_quant_weights* down, const uint16_t* act,
+                                const uint32_t* ids, const uint16_t* weights, uint16_t* out,
+                                uint32_t topk, uint32_t n_out, mh_stream_t stream) {
+    DownArgs a;
+    MH_TRY(down_common("mh_gemv_gather_down_combine", down, act, ids, weights, out, topk, n_out, a));
+    return launch_down(a, topk, mh::as_stream(stream));
+}
+
+int mh_moe_decode(const void* router, int router_dtype, const float* bias, int mode, float eps,
+                  const mh_quant_weights* gate, const mh_quant_weights* up,
+                  const mh_quant_weights* down, uint32_t n_experts, uint32_t topk,
+                  const uint16_t* x, uint16_t* out, float* logits, uint32_t* ids,
+                  uint16_t* weights, uint16_t* act, uint32_t* counter, mh_stream_t stream) {
+    const char* op = "mh_moe_decode";
+    MH_ENSURE(gate && up && down, MH_ERR_INVALID, "%s: NULL weights", op);
+    MH_ENSURE(n_experts > 0 && gate->out_features % n_experts == 0 &&
+                  down->out_features % n_experts == 0,
+              MH_ERR_INVALID, "%s: stacked rows not divisible by %u experts", op, n_experts);
+    const uint32_t n_inter = gate->out_features / n_experts;
+    const uint32_t d_model = down->out_features / n_experts;
+    MH_ENSURE(gate->in_features == d_model && down->in_features == n_inter, MH_ERR_INVALID,
+              "%s: gate [%u x %u] / down [%u x %u] do not chain", op, n_inter, gate->in_features,
+              d_model, down->in_features);
+    // validate all three stages before launching any of them
+    DenseArgs ra;
+    MH_ENSURE(router_dtype == MH_DTYPE_F32 || router_dtype == MH_DTYPE_BF16, MH_ERR_INVALID,
+              "%s: router dtype %d", op, router_dtype);
+    MH_ENSURE(counter != nullptr, MH_ERR_INVALID, "%s: counter is NULL", op);
+    MH_TRY(route_checks(op, logits, ids, weights, 1, n_experts, topk, mode));
+    MH_TRY(dense_common(op, router, router_dtype == MH_DTYPE_F32, x, logits, 1, n_experts, d_model, ra));
+    ActArgs aa;
+    MH_TRY(act_common(op, gate, up, x, ids, act, topk, n_inter, aa));
+    DownArgs da;
+    MH_TRY(down_common(op, down, act, ids, weights, out, topk, d_model, da));
+    ra.bias = bias;
+    ra.ids = ids;
+    ra.weights = weights;
+    ra.done = counter;
+    ra.topk = topk;
+    ra.mode = mode;
+    ra.eps = eps;
+    const hipStream_t s = mh::as_stream(stream);
+    const int rc = router_dtype == MH_DTYPE_F32 ? launch_dense<float, 1, 1>(ra, s)
+                                                : launch_dense<uint16_t, 1, 1>(ra, s);
+    MH_TRY(rc);
+    MH_TRY(launch_gather_act(aa, s));
+    return launch_down(da, topk, s);
+}
+
+}  // extern "C"

@@ -31,6 +31,10 @@ class MoltenError(RuntimeError):
 
 
 MH_OK = 0
+ROUTE_SIGMOID_BIAS = 0
+ROUTE_SOFTMAX = 1
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
 MH_ERR_INVALID = -1
 MH_ERR_ALIGN = -2
 MH_ERR_UNSUPPORTED = -3
@@ -79,6 +83,18 @@ _SIGNATURES = {
     "mh_gemv_quant_argmax": [_qw, _vp, _vp, _vp, _vp, _vp, _u32, _vp],
     "mh_token_tail": [_vp, _vp, _u32, _vp],
     "mh_argmax_bf16": [_vp, _u32, _vp, _vp, _vp],
+    "mh_gemv_f32": [_vp, _vp, _vp, _u32, _u32, _vp],
+    "mh_gemv_bf16": [_vp, _vp, _vp, _u32, _u32, _vp],
+    "mh_route_token": [_vp, _vp, _vp, _vp, _u32, _u32, _i32, _f32, _vp],
+    "mh_router_route": [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _i32, _f32,
+                        _vp],
+    "mh_gemv_gather_act": [_qw, _qw, _vp, _vp, _vp, _u32, _u32, _vp],
+    "mh_gemv_gu_act": [_qw, _qw, _vp, _vp, _vp],
+    "mh_gemv_gather_down_combine": [_qw, _vp, _vp, _vp, _vp, _u32, _u32, _vp],
+    "mh_moe_decode": [_vp, _i32, _vp, _i32, _f32, _qw, _qw, _qw, _u32, _u32, _vp, _vp, _vp, _vp,
+                      _vp, _vp, _vp, _vp],
+    "mh_router_prefill": [_vp, _vp, _i32, _vp, _u32, _u32, _u32, _vp],
+    "mh_moe_route_batch": [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _i32, _f32, _vp],
 }
 _RESTYPES = {"mh_last_error": ctypes.c_char_p, "mh_version": ctypes.c_char_p}
 
@@ -211,3 +227,80 @@ def argmax_bf16(x, n: int, partials, out, stream=None) -> None:
 
 def zero(buf, nbytes: int, stream=None) -> None:
     check(load().mh_zero(_ptr(buf), nbytes, _stream(stream)), "zero")
+
+
+def _dtype_of(w) -> int:
+    """MH_DTYPE_* of a router tensor (torch f32 -> F32, 2-byte -> BF16)."""
+    es = w.element_size() if hasattr(w, "element_size") else w.itemsize
+    return DTYPE_F32 if es == 4 else DTYPE_BF16
+
+
+# ----------------------------------------------------------- router / MoE --
+
+def gemv_f32(w, x, y, n: int, k: int, stream=None) -> None:
+    """src/kernels/lfm.rs:314 (f32 router)."""
+    check(load().mh_gemv_f32(_ptr(w), _ptr(x), _ptr(y), n, k, _stream(stream)), "gemv_f32")
+
+
+def gemv_bf16(w, x, y, n: int, k: int, stream=None) -> None:
+    """bf16-router counterpart of gemv_f32."""
+    check(load().mh_gemv_bf16(_ptr(w), _ptr(x), _ptr(y), n, k, _stream(stream)), "gemv_bf16")
+
+
+def route_token(logits, bias, ids, weights, e: int, topk: int, mode: int = ROUTE_SIGMOID_BIAS,
+                eps: float = 1e-6, stream=None) -> None:
+    """src/kernels/lfm.rs:391."""
+    check(load().mh_route_token(_ptr(logits), _ptr(bias), _ptr(ids), _ptr(weights), e, topk, mode,
+                                eps, _stream(stream)), "route_token")
+
+
+def router_route(w, x, logits, bias, ids, weights, counter, e: int, k: int, topk: int,
+                 mode: int = ROUTE_SIGMOID_BIAS, eps: float = 1e-6, stream=None) -> None:
+    """src/kernels/lfm.rs:266 without the add+RMSNorm prologue."""
+    check(load().mh_router_route(_ptr(w), _dtype_of(w), _ptr(x), _ptr(logits), _ptr(bias),
+                                 _ptr(ids), _ptr(weights), _ptr(counter), e, k, topk, mode, eps,
+                                 _stream(stream)), "router_route")
+
+
+def gemv_gather_act(gate: QuantWeights, up: QuantWeights, x, ids, act, topk: int, n_inter: int,
+                    stream=None) -> None:
+    """src/kernels/lfm.rs:421."""
+    check(load().mh_gemv_gather_act(_qref(gate), _qref(up), _ptr(x), _ptr(ids), _ptr(act), topk,
+                                    n_inter, _stream(stream)), "gemv_gather_act")
+
+
+def gemv_gu_act(gate: QuantWeights, up: QuantWeights, x, act, stream=None) -> None:
+    """src/kernels/lfm.rs:464."""
+    check(load().mh_gemv_gu_act(_qref(gate), _qref(up), _ptr(x), _ptr(act), _stream(stream)),
+          "gemv_gu_act")
+
+
+def gemv_gather_down_combine4(down: QuantWeights, act, ids, weights, out, topk: int = 4,
+                              n_out: int = 2048, stream=None) -> None:
+    """src/kernels/lfm.rs:499 (topk 1..4 here)."""
+    check(load().mh_gemv_gather_down_combine(_qref(down), _ptr(act), _ptr(ids), _ptr(weights),
+                                             _ptr(out), topk, n_out, _stream(stream)),
+          "gemv_gather_down_combine4")
+
+
+def moe_decode(router, bias, gate: QuantWeights, up: QuantWeights, down: QuantWeights,
+               n_experts: int, topk: int, x, out, logits, ids, weights, act, counter,
+               mode: int = ROUTE_SIGMOID_BIAS, eps: float = 1e-6, stream=None) -> None:
+    """One MoE decode step (src/lfm.rs:967-1011)."""
+    check(load().mh_moe_decode(_ptr(router), _dtype_of(router), _ptr(bias), mode, eps,
+                               _qref(gate), _qref(up), _qref(down), n_experts, topk, _ptr(x),
+                               _ptr(out), _ptr(logits), _ptr(ids), _ptr(weights), _ptr(act),
+                               _ptr(counter), _stream(stream)), "moe_decode")
+
+
+def router_prefill(x, w, out, m: int, k: int, e: int, stream=None) -> None:
+    """src/kernels/lfm.rs:366."""
+    check(load().mh_router_prefill(_ptr(x), _ptr(w), _dtype_of(w), _ptr(out), m, k, e,
+                                   _stream(stream)), "router_prefill")
+
+
+def moe_route_batch(logits, bias, ids, gw, m: int, e: int, topk: int,
+                    mode: int = ROUTE_SIGMOID_BIAS, eps: float = 1e-6, stream=None) -> None:
+    """src/kernels/lfm.rs:536."""
+    check(load().mh_moe_route_batch(_ptr(logits), _ptr(bias), _ptr(ids), _ptr(gw), m, e, topk,
+                                    mode, eps, _stream(stream)), "moe_route_batch")

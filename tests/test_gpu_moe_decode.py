@@ -1,0 +1,168 @@
+"""GPU parity of the router, top-k and decode MoE expert kernels through the
+C ABI.  Every output, float included, is compared bit
+for bit: the kernels follow the oracle's chunk order and its exp."""
+import numpy as np
+import pytest
+
+from molten_amd import hip, layout
+from tests.devutil import dev_quant, empty_dev, from_dev, to_dev, zeros_dev
+from tests.synth import moe_weights, router_weights
+
+pytestmark = pytest.mark.gpu
+
+E, H, I, TOPK = 64, 2048, 1536, 4
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def experts():
+    """Config 3's 64 experts (uploaded once for the module)."""
+    rng = np.random.default_rng(33)
+    gate, up, down = moe_weights(rng, E, H, I)
+    dg, kg = dev_quant(gate)
+    du, ku = dev_quant(up)
+    dd, kd = dev_quant(down)
+    return dict(h=(gate, up, down), d=(dg, du, dd), keep=(kg, ku, kd))
+
+
+@pytest.mark.parametrize("f32", [True, False])
+@pytest.mark.parametrize("n,k", [(64, 2048), (64, 4096), (100, 1536)])
+def test_router_gemv_bit_exact(dev, orc, f32, n, k):
+    rng = np.random.default_rng(n + k + f32)
+    w = router_weights(rng, n, k, f32)
+    x = layout.synth_bf16(rng, (1, k))
+    y = empty_dev((n,), np.float32)
+    (hip.gemv_f32 if f32 else hip.gemv_bf16)(to_dev(w), to_dev(x), y, n, k)
+    np.testing.assert_array_equal(from_dev(y, np.float32).view(np.uint32),
+                                  orc.gemv_dense(w, x)[0].view(np.uint32))
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_route_token_bit_exact(dev, orc, mode):
+    rng = np.random.default_rng(4 + mode)
+    for trial in range(20):
+        z = rng.normal(0, 2, (1, E)).astype(np.float32)
+        if trial % 4 == 0:
+            z[0, 7] = z[0, 40] = np.float32(z.max() + 0.5)
+        bias = rng.normal(0, 0.1, E).astype(np.float32) if mode == 0 else None
+        ids = empty_dev((TOPK,), np.uint32)
+        w = empty_dev((TOPK,), np.uint16)
+        hip.route_token(to_dev(z), None if bias is None else to_dev(bias), ids, w, E, TOPK, mode)
+        want_ids, want_w = orc.route(z, bias, TOPK, mode)
+        assert from_dev(ids, np.uint32).tolist() == want_ids[0].tolist()
+        np.testing.assert_array_equal(from_dev(w, np.uint16), want_w[0])
+
+
+@pytest.mark.parametrize("mode,f32", [(0, True), (1, False)])
+def test_router_route_fused(dev, orc, mode, f32):
+    rng = np.random.default_rng(9 + mode)
+    w = router_weights(rng, E, H, f32)
+    bias = rng.normal(0, 0.05, E).astype(np.float32) if mode == 0 else None
+    wd = to_dev(w)
+    bd = None if bias is None else to_dev(bias)
+    counter = zeros_dev((1,), np.uint32)
+    logits = empty_dev((E,), np.float32)
+    ids = empty_dev((TOPK,), np.uint32)
+    wt = empty_dev((TOPK,), np.uint16)
+    for trial in range(8):
+        x = layout.synth_bf16(rng, (1, H))
+        hip.router_route(wd, to_dev(x), logits, bd, ids, wt, counter, E, H, TOPK, mode)
+        want_logits = orc.gemv_dense(w, x)
+        want_ids, want_w = orc.route(want_logits, bias, TOPK, mode)
+        np.testing.assert_array_equal(from_dev(logits, np.float32), want_logits[0])
+        assert from_dev(ids, np.uint32).tolist() == want_ids[0].tolist()
+        np.testing.assert_array_equal(from_dev(wt, np.uint16), want_w[0])
+        assert from_dev(counter, np.uint32)[0] == 0
+
+
+def test_gather_act_bit_exact(dev, orc, experts):
+    gate, up, down = experts["h"]
+    dg, du, dd = experts["d"]
+    rng = np.random.default_rng(1)
+    for trial in range(3):
+        x = layout.synth_bf16(rng, (1, H))[0]
+        ids = rng.choice(E, TOPK, replace=False).astype(np.uint32)
+        act = empty_dev((TOPK, I), np.uint16)
+        hip.gemv_gather_act(dg, du, to_dev(x), to_dev(ids), act, TOPK, I)
+        np.testing.assert_array_equal(from_dev(act, np.uint16), orc.gather_act(gate, up, I, x, ids))
+
+
+def test_gu_act_dense_bit_exact(dev, orc):
+    rng = np.random.default_rng(3)
+    n, k = 11776, 2048  # the model's dense FFN
+    gate = layout.synth_quant(rng, n, k, 4)
+    up = layout.synth_quant(rng, n, k, 4)
+    x = layout.synth_bf16(rng, (1, k))[0]
+    dg, kg = dev_quant(gate)
+    du, ku = dev_quant(up)
+    act = empty_dev((n,), np.uint16)
+    hip.gemv_gu_act(dg, du, to_dev(x), act)
+    np.testing.assert_array_equal(from_dev(act, np.uint16), orc.gather_act(gate, up, n, x, None)[0])
+
+
+@pytest.mark.parametrize("topk", [4, 2, 1])
+def test_down_combine_bit_exact(dev, orc, experts, topk):
+    gate, up, down = experts["h"]
+    dg, du, dd = experts["d"]
+    rng = np.random.default_rng(10 + topk)
+    act = layout.synth_bf16(rng, (topk, I), std=2.0)
+    ids = rng.choice(E, topk, replace=False).astype(np.uint32)
+    w = layout.f32_to_bf16(rng.dirichlet(np.ones(topk)).astype(np.float32))
+    out = empty_dev((H,), np.uint16)
+    hip.gemv_gather_down_combine4(dd, to_dev(act), to_dev(ids), to_dev(w), out, topk, H)
+    np.testing.assert_array_equal(from_dev(out, np.uint16), orc.down_combine(down, H, act, ids, w))
+
+
+@pytest.mark.parametrize("mode,f32", [(1, False), (0, True)])
+def test_moe_decode_step_bit_exact(dev, orc, experts, mode, f32):
+    """Config 3: router -> top-4 -> gate/up/SwiGLU -> down -> combine, all
+    intermediates and the output bit-exact, for several inputs (different
+    routings), with the counter left zero between steps."""
+    _log(f"moe decode mode={mode} f32={f32}")
+    gate, up, down = experts["h"]
+    dg, du, dd = experts["d"]
+    rng = np.random.default_rng(100 + mode)
+    router = router_weights(rng, E, H, f32)
+    bias = rng.normal(0, 0.05, E).astype(np.float32) if mode == 0 else None
+    rd = to_dev(router)
+    bd = None if bias is None else to_dev(bias)
+    out = empty_dev((H,), np.uint16)
+    logits = empty_dev((E,), np.float32)
+    ids = empty_dev((TOPK,), np.uint32)
+    wt = empty_dev((TOPK,), np.uint16)
+    act = empty_dev((TOPK, I), np.uint16)
+    counter = zeros_dev((1,), np.uint32)
+    seen = set()
+    for trial in range(4):
+        x = layout.synth_bf16(rng, (1, H))[0]
+        hip.moe_decode(rd, bd, dg, du, dd, E, TOPK, to_dev(x), out, logits, ids, wt, act, counter,
+                       mode=mode)
+        want = orc.moe_decode(router, bias, mode, gate, up, down, E, TOPK, H, I, x)
+        assert from_dev(ids, np.uint32).tolist() == want["ids"].tolist()
+        np.testing.assert_array_equal(from_dev(logits, np.float32), want["logits"])
+        np.testing.assert_array_equal(from_dev(wt, np.uint16), want["w"])
+        np.testing.assert_array_equal(from_dev(act, np.uint16), want["act"])
+        np.testing.assert_array_equal(from_dev(out, np.uint16), want["out"])
+        assert from_dev(counter, np.uint32)[0] == 0
+        seen.add(tuple(want["ids"].tolist()))
+    assert len(seen) > 1  # the inputs exercised different routings
+
+
+def test_prefill_router_and_route_batch(dev, orc):
+    rng = np.random.default_rng(77)
+    m = 300
+    w = router_weights(rng, E, H, False)
+    x = layout.synth_bf16(rng, (m, H))
+    logits = empty_dev((m, E), np.float32)
+    hip.router_prefill(to_dev(x), to_dev(w), logits, m, H, E)
+    want = orc.gemv_dense(w, x)
+    np.testing.assert_array_equal(from_dev(logits, np.float32), want)
+    ids = empty_dev((m, TOPK), np.uint32)
+    gw = empty_dev((m, TOPK), np.uint16)
+    hip.moe_route_batch(logits, None, ids, gw, m, E, TOPK, mode=1)
+    want_ids, want_w = orc.route(want, None, TOPK, 1)
+    np.testing.assert_array_equal(from_dev(ids, np.uint32), want_ids)
+    np.testing.assert_array_equal(from_dev(gw, np.uint16), want_w)
