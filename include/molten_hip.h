@@ -204,6 +204,94 @@ int mh_moe_route_batch(const float* logits, const float* bias, uint32_t* ids, ui
                        uint32_t m, uint32_t e, uint32_t topk, int mode, float eps,
                        mh_stream_t stream);
 
+/* ---------------------------------------------- prefill counting sort ---
+ * src/kernels/lfm.rs:557-624.  counts u32 [e] (zeroed by
+ * mh_moe_zero_counts, then accumulated); offsets = exclusive scan; the
+ * stable scatter in slot order (token-major, rank-major): ids_sorted[pos] =
+ * token, slotpos[t*topk + r] = pos.  e <= 256. */
+int mh_moe_zero_counts(uint32_t* counts, uint32_t e, mh_stream_t stream);
+int mh_moe_count_slots(const uint32_t* ids, uint32_t* counts, uint32_t s, uint32_t e,
+                       mh_stream_t stream);
+int mh_moe_offsets(const uint32_t* counts, uint32_t* offsets, uint32_t e, mh_stream_t stream);
+int mh_moe_sorted(const uint32_t* ids, const uint32_t* offsets, uint32_t* ids_sorted,
+                  uint32_t* slotpos, uint32_t m, uint32_t e, uint32_t topk, mh_stream_t stream);
+
+/* ------------------------------------------------ prefill block maps ---
+ * src/kernels/lfm.rs:626-697 with the column tile given per map (the
+ * reference uses one bn for both; its tiles have gu_bn == dn_bn == 64).
+ * Entry i of expert e is uint4(m0, e*N + n0, n0, m_end), in expert order;
+ * mh_moe_zero_blocks clears the maps first (unused tail entries stay zero
+ * and are skipped by the GEMMs). */
+int mh_moe_zero_blocks(uint32_t* gu, uint32_t* dn, uint32_t n_gu, uint32_t n_dn,
+                       mh_stream_t stream);
+int mh_moe_block_offsets(const uint32_t* counts, uint32_t* gu_off, uint32_t* dn_off, uint32_t e,
+                         uint32_t bm, uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n,
+                         uint32_t dn_n, mh_stream_t stream);
+int mh_moe_blocks(const uint32_t* counts, const uint32_t* offsets, const uint32_t* gu_off,
+                  const uint32_t* dn_off, uint32_t* gu, uint32_t max_gu, uint32_t* dn,
+                  uint32_t max_dn, uint32_t e, uint32_t bm, uint32_t gu_bn, uint32_t dn_bn,
+                  uint32_t gu_n, uint32_t dn_n, mh_stream_t stream);
+
+/* ----------------------------------------------------- elementwise ---
+ * src/kernels/elementwise.rs:59 gather_rows_bf16: out[i, :] = table[ids[i], :]
+ * (h % 8 == 0; ids clamped to n_table - 1).  :48 silu_mul_bf16:
+ * out = bf16(bf16(silu(g)) * u).  src/kernels/lfm.rs:701 moe_combine_rows:
+ * out[t, c] = bf16(sum_r bf16(w[t, r] * sorted[slotpos[t, r], c])). */
+int mh_gather_rows_bf16(const uint16_t* table, const uint32_t* ids, uint16_t* out, uint32_t m,
+                        uint32_t h, uint32_t n_table, mh_stream_t stream);
+int mh_silu_mul_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* out, size_t n,
+                     mh_stream_t stream);
+int mh_moe_combine_rows(const uint16_t* sorted, const uint32_t* slotpos, const uint16_t* weights,
+                        uint16_t* out, uint32_t m, uint32_t h, uint32_t topk, mh_stream_t stream);
+
+/* ------------------------------------------------- grouped Q4 GEMM ---
+ * src/kernels/quant.rs:223 gemm_q4_grouped_mlx: for every block-map entry
+ * (m0, e*N + n0, n0, m_end): C[m, n0 + j] = A[m, :] . dequant(W[e*N + n0 + j, :])
+ * (bf16 dequant, f32 MFMA accumulation, bf16 store), m in [m0, m_end).
+ * A bf16 [s_rows, K], C bf16 [s_rows, n], W 4-bit group 64 [E*n, K].
+ * Tiles (bm x bn): 32x64 and 128x64 (the reference's MoeTile shapes) and
+ * 128x256.  The map's column tile must equal bn. */
+int mh_gemm_q4_grouped(const uint16_t* a, const mh_quant_weights* w, uint16_t* c,
+                       const uint32_t* blocks, uint32_t n_blocks, uint32_t s_rows, uint32_t n,
+                       uint32_t bm, uint32_t bn, mh_stream_t stream);
+
+/* src/kernels/quant.rs:151 gemm_q4_grouped_mlx_gu: gate and up over the
+ * same map and A, stored separately.  Tiles 32x64, 128x64, 128x128. */
+int mh_gemm_q4_grouped_gu(const uint16_t* a, const mh_quant_weights* gate,
+                          const mh_quant_weights* up, uint16_t* gate_out, uint16_t* up_out,
+                          const uint32_t* blocks, uint32_t n_blocks, uint32_t s_rows, uint32_t n,
+                          uint32_t bm, uint32_t bn, mh_stream_t stream);
+
+/* gate/up + SwiGLU fused (gemm_q4_grouped_mlx_gu followed by silu_mul_bf16,
+ * src/lfm.rs:953-961), with the row gather of gather_rows_bf16 folded into
+ * the A load: tile row m reads x[ids_sorted[m]] (ids_sorted may be NULL: A =
+ * x [s_rows, K]).  act bf16 [s_rows, n]. */
+int mh_gemm_q4_grouped_gu_act(const uint16_t* x, const uint32_t* ids_sorted, uint32_t x_rows,
+                              const mh_quant_weights* gate, const mh_quant_weights* up,
+                              uint16_t* act, const uint32_t* blocks, uint32_t n_blocks,
+                              uint32_t s_rows, uint32_t n, uint32_t bm, uint32_t bn,
+                              mh_stream_t stream);
+
+/* ------------------------------------------------- prefill MoE step ---
+ * src/lfm.rs:847-965 moe_prefill for m tokens on a caller workspace
+ * (no allocation): router -> route -> sort -> maps -> gate/up+SwiGLU ->
+ * down -> combine.  out bf16 [m, d_model].  The workspace holds the
+ * intermediates below; mh_moe_prefill_workspace returns its size and (if
+ * offsets != NULL) each region's byte offset. */
+enum {
+    MH_PREFILL_WS_LOGITS = 0, MH_PREFILL_WS_IDS, MH_PREFILL_WS_GW, MH_PREFILL_WS_COUNTS,
+    MH_PREFILL_WS_OFFSETS, MH_PREFILL_WS_IDS_SORTED, MH_PREFILL_WS_SLOTPOS,
+    MH_PREFILL_WS_GU_OFF, MH_PREFILL_WS_DN_OFF, MH_PREFILL_WS_GU_MAP, MH_PREFILL_WS_DN_MAP,
+    MH_PREFILL_WS_ACT, MH_PREFILL_WS_ED, MH_PREFILL_WS_REGIONS
+};
+size_t mh_moe_prefill_workspace(uint32_t m, uint32_t n_experts, uint32_t topk, uint32_t d_model,
+                                uint32_t n_inter, size_t* offsets);
+int mh_moe_prefill(const void* router, int router_dtype, const float* bias, int mode, float eps,
+                   const mh_quant_weights* gate, const mh_quant_weights* up,
+                   const mh_quant_weights* down, uint32_t n_experts, uint32_t topk,
+                   const uint16_t* x, uint32_t m, uint16_t* out, void* workspace,
+                   size_t workspace_bytes, mh_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,302 @@
+// moe_prefill.hip -- the integer half of the prefill MoE (counting sort and
+// block maps) plus the row gather, SwiGLU and the weighted combine.
+//
+// Replaces lfm.metal:1604-1770 (moe_zero_counts, moe_count, moe_offsets,
+// moe_sorted_parallel, moe_zero_blocks, moe_block_offsets, moe_blocks),
+// lfm.metal:859-940 (combine) and elementwise.metal:7-52 (SwiGLU, gather).
+// Every integer output is a deterministic function of the ids: the sort is
+// stable in slot order (token-major, rank-major), like the reference's.
+#include "mh_device.hpp"
+#include "mh_host.hpp"
+
+namespace {
+
+__global__ void k_fill_u32(uint32_t* p, size_t n, uint32_t v) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        p[i] = v;
+    }
+}
+
+// Histogram: per-workgroup LDS counts, one atomic per (workgroup, expert).
+__global__ __launch_bounds__(256) void k_count(const uint32_t* ids, uint32_t* counts, uint32_t s,
+                                               uint32_t e) {
+    __shared__ uint32_t h[256];
+    for (uint32_t i = threadIdx.x; i < e; i += 256) h[i] = 0;
+    __syncthreads();
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < s; i += gridDim.x * 256) {
+        const uint32_t x = ids[i];
+        if (x < e) atomicAdd(&h[x], 1u);
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < e; i += 256) {
+        if (h[i]) atomicAdd(&counts[i], h[i]);
+    }
+}
+
+// Exclusive scan of counts (e <= 1024) by one workgroup.
+__global__ __launch_bounds__(1024) void k_offsets(const uint32_t* counts, uint32_t* offsets,
+                                                  uint32_t e) {
+    __shared__ uint32_t sh[1024];
+    const uint32_t t = threadIdx.x;
+    sh[t] = t < e ? counts[t] : 0u;
+    __syncthreads();
+    for (uint32_t d = 1; d < 1024; d <<= 1) {
+        const uint32_t v = t >= d ? sh[t - d] : 0u;
+        __syncthreads();
+        sh[t] += v;
+        __syncthreads();
+    }
+    if (t < e) offsets[t] = sh[t] - counts[t];
+}
+
+// Stable scatter: one workgroup per expert walks the slots in order, 256 at a
+// time; a slot routed to the expert goes to offsets[e] + (number of earlier
+// slots routed to it), found with a ballot prefix count.
+__global__ __launch_bounds__(256) void k_sorted(const uint32_t* ids, const uint32_t* offsets,
+                                                uint32_t* ids_sorted, uint32_t* slotpos,
+                                                uint32_t s, uint32_t topk) {
+    __shared__ uint32_t wave_tot[4];
+    const uint32_t e = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t base = offsets[e];
+    for (uint32_t t0 = 0; t0 < s; t0 += 256) {
+        const uint32_t i = t0 + threadIdx.x;
+        const bool hit = i < s && ids[i] == e;
+        const unsigned long long m = __ballot(hit);
+        const uint32_t before = __popcll(m & ((1ull << lane) - 1ull));
+        if (lane == 0) wave_tot[wave] = __popcll(m);
+        __syncthreads();
+        uint32_t wbase = 0;
+        for (int w = 0; w < wave; ++w) wbase += wave_tot[w];
+        const uint32_t tile_total = wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
+        if (hit) {
+            const uint32_t pos = base + wbase + before;
+            ids_sorted[pos] = i / topk;
+            slotpos[i] = pos;
+        }
+        base += tile_total;
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(64) void k_block_offsets(const uint32_t* counts, uint32_t* gu_off,
+                                                      uint32_t* dn_off, uint32_t e, uint32_t bm,
+                                                      uint32_t gu_tiles, uint32_t dn_tiles) {
+    if (threadIdx.x != 0) return;
+    uint32_t ag = 0, ad = 0;
+    for (uint32_t i = 0; i < e; ++i) {
+        gu_off[i] = ag;
+        dn_off[i] = ad;
+        const uint32_t rows = (counts[i] + bm - 1) / bm;
+        ag += rows * gu_tiles;
+        ad += rows * dn_tiles;
+    }
+}
+
+__device__ inline void write_map(uint4* map, uint32_t max_entries, uint32_t base, uint32_t n,
+                                 uint32_t off, uint32_t ex, uint32_t bm, uint32_t bn,
+                                 uint32_t n_cols) {
+    const uint32_t rows = (n + bm - 1) / bm;
+    const uint32_t tiles = n_cols / bn;
+    for (uint32_t i = threadIdx.x; i < rows * tiles; i += blockDim.x) {
+        if (base + i >= max_entries) break;
+        const uint32_t mt = i / tiles, nt = i % tiles;
+        const uint32_t m0 = off + mt * bm;
+        const uint32_t m_end = min(m0 + bm, off + n);
+        const uint32_t n0 = nt * bn;
+        map[base + i] = make_uint4(m0, ex * n_cols + n0, n0, m_end);
+    }
+}
+
+__global__ __launch_bounds__(128) void k_blocks(const uint32_t* counts, const uint32_t* offsets,
+                                                const uint32_t* gu_off, const uint32_t* dn_off,
+                                                uint4* gu, uint32_t max_gu, uint4* dn,
+                                                uint32_t max_dn, uint32_t bm, uint32_t gu_bn,
+                                                uint32_t dn_bn, uint32_t gu_n, uint32_t dn_n) {
+    const uint32_t ex = blockIdx.x;
+    const uint32_t n = counts[ex];
+    if (n == 0) return;
+    write_map(gu, max_gu, gu_off[ex], n, offsets[ex], ex, bm, gu_bn, gu_n);
+    write_map(dn, max_dn, dn_off[ex], n, offsets[ex], ex, bm, dn_bn, dn_n);
+}
+
+// out[i, :] = table[ids[i], :]; 16-byte vectors when h % 8 == 0.
+__global__ __launch_bounds__(256) void k_gather_rows(const uint16_t* table, const uint32_t* ids,
+                                                     uint16_t* out, uint32_t m, uint32_t h,
+                                                     uint32_t n_table) {
+    const uint32_t h8 = h / 8;
+    const size_t total = static_cast<size_t>(m) * h8;
+    for (size_t t = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+         t += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const uint32_t i = static_cast<uint32_t>(t / h8), c = static_cast<uint32_t>(t % h8);
+        const uint32_t r = min(ids[i], n_table - 1);
+        reinterpret_cast<uint4*>(out + static_cast<size_t>(i) * h)[c] =
+            reinterpret_cast<const uint4*>(table + static_cast<size_t>(r) * h)[c];
+    }
+}
+
+__global__ __launch_bounds__(256) void k_silu_mul(const uint16_t* gate, const uint16_t* up,
+                                                  uint16_t* out, size_t n) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const float g = mh::bf16_to_f32(gate[i]);
+        out[i] = mh::f32_to_bf16(mh::silu_bf16(g) * mh::bf16_to_f32(up[i]));
+    }
+}
+
+// out[t, c] = bf16( sum_r f32(bf16(w[t,r] * sorted[slotpos[t,r], c])) ), r
+// ascending from +0; eight columns per thread.
+__global__ __launch_bounds__(256) void k_combine(const uint16_t* sorted, const uint32_t* slotpos,
+                                                 const uint16_t* w, uint16_t* out, uint32_t m,
+                                                 uint32_t h, uint32_t topk, uint32_t n_sorted) {
+    const uint32_t h8 = h / 8;
+    const size_t total = static_cast<size_t>(m) * h8;
+    for (size_t t = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+         t += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const uint32_t tok = static_cast<uint32_t>(t / h8), c = static_cast<uint32_t>(t % h8);
+        float acc[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+        for (uint32_t r = 0; r < topk; ++r) {
+            const uint32_t p = min(slotpos[static_cast<size_t>(tok) * topk + r], n_sorted - 1);
+            const float wr = mh::bf16_to_f32(w[static_cast<size_t>(tok) * topk + r]);
+            const uint4 v = reinterpret_cast<const uint4*>(sorted + static_cast<size_t>(p) * h)[c];
+            const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[2 * j] = acc[2 * j] + mh::round_bf16(wr * mh::bf16lo(u[j]));
+                acc[2 * j + 1] = acc[2 * j + 1] + mh::round_bf16(wr * mh::bf16hi(u[j]));
+            }
+        }
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            o[j] = static_cast<uint32_t>(mh::f32_to_bf16(acc[2 * j])) |
+                   (static_cast<uint32_t>(mh::f32_to_bf16(acc[2 * j + 1])) << 16);
+        }
+        reinterpret_cast<uint4*>(out + static_cast<size_t>(tok) * h)[c] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+unsigned grid_for(size_t n, unsigned per = 256) {
+    const size_t want = (n + per - 1) / per;
+    const size_t cap = static_cast<size_t>(mh::cu_count()) * 16;
+    return static_cast<unsigned>(want == 0 ? 1 : (want < cap ? want : cap));
+}
+
+}  // namespace
+
+extern "C" {
+
+int mh_moe_zero_counts(uint32_t* counts, uint32_t e, mh_stream_t stream) {
+    MH_ENSURE(counts && e > 0, MH_ERR_INVALID, "mh_moe_zero_counts: bad arguments");
+    hipLaunchKernelGGL(k_fill_u32, dim3(1), dim3(256), 0, mh::as_stream(stream), counts,
+                       static_cast<size_t>(e), 0u);
+    return mh::launch_status("mh_moe_zero_counts");
+}
+
+int mh_moe_count_slots(const uint32_t* ids, uint32_t* counts, uint32_t s, uint32_t e,
+                       mh_stream_t stream) {
+    MH_ENSURE(ids && counts, MH_ERR_INVALID, "mh_moe_count_slots: NULL argument");
+    MH_ENSURE(e >= 1 && e <= 256, MH_ERR_UNSUPPORTED, "mh_moe_count_slots: %u experts", e);
+    if (s == 0) return MH_OK;
+    hipLaunchKernelGGL(k_count, dim3(grid_for(s, 4096)), dim3(256), 0, mh::as_stream(stream), ids,
+                       counts, s, e);
+    return mh::launch_status("mh_moe_count_slots");
+}
+
+int mh_moe_offsets(const uint32_t* counts, uint32_t* offsets, uint32_t e, mh_stream_t stream) {
+    MH_ENSURE(counts && offsets, MH_ERR_INVALID, "mh_moe_offsets: NULL argument");
+    MH_ENSURE(e >= 1 && e <= 1024, MH_ERR_UNSUPPORTED, "mh_moe_offsets: %u experts", e);
+    hipLaunchKernelGGL(k_offsets, dim3(1), dim3(1024), 0, mh::as_stream(stream), counts, offsets, e);
+    return mh::launch_status("mh_moe_offsets");
+}
+
+int mh_moe_sorted(const uint32_t* ids, const uint32_t* offsets, uint32_t* ids_sorted,
+                  uint32_t* slotpos, uint32_t m, uint32_t e, uint32_t topk, mh_stream_t stream) {
+    MH_ENSURE(ids && offsets && ids_sorted && slotpos, MH_ERR_INVALID, "mh_moe_sorted: NULL argument");
+    MH_ENSURE(e >= 1 && topk >= 1, MH_ERR_INVALID, "mh_moe_sorted: e=%u topk=%u", e, topk);
+    if (m == 0) return MH_OK;
+    hipLaunchKernelGGL(k_sorted, dim3(e), dim3(256), 0, mh::as_stream(stream), ids, offsets,
+                       ids_sorted, slotpos, m * topk, topk);
+    return mh::launch_status("mh_moe_sorted");
+}
+
+int mh_moe_zero_blocks(uint32_t* gu, uint32_t* dn, uint32_t n_gu, uint32_t n_dn,
+                       mh_stream_t stream) {
+    MH_ENSURE(gu && dn, MH_ERR_INVALID, "mh_moe_zero_blocks: NULL argument");
+    const hipStream_t s = mh::as_stream(stream);
+    hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(4ull * n_gu)), dim3(256), 0, s, gu,
+                       4ull * n_gu, 0u);
+    hipLaunchKernelGGL(k_fill_u32, dim3(grid_for(4ull * n_dn)), dim3(256), 0, s, dn,
+                       4ull * n_dn, 0u);
+    return mh::launch_status("mh_moe_zero_blocks");
+}
+
+int mh_moe_block_offsets(const uint32_t* counts, uint32_t* gu_off, uint32_t* dn_off, uint32_t e,
+                         uint32_t bm, uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n,
+                         uint32_t dn_n, mh_stream_t stream) {
+    MH_ENSURE(counts && gu_off && dn_off, MH_ERR_INVALID, "mh_moe_block_offsets: NULL argument");
+    MH_ENSURE(bm > 0 && gu_bn > 0 && dn_bn > 0 && gu_n % gu_bn == 0 && dn_n % dn_bn == 0,
+              MH_ERR_INVALID, "mh_moe_block_offsets: tiles bm=%u bn=%u/%u do not divide %u/%u",
+              bm, gu_bn, dn_bn, gu_n, dn_n);
+    hipLaunchKernelGGL(k_block_offsets, dim3(1), dim3(64), 0, mh::as_stream(stream), counts, gu_off,
+                       dn_off, e, bm, gu_n / gu_bn, dn_n / dn_bn);
+    return mh::launch_status("mh_moe_block_offsets");
+}
+
+int mh_moe_blocks(const uint32_t* counts, const uint32_t* offsets, const uint32_t* gu_off,
+                  const uint32_t* dn_off, uint32_t* gu, uint32_t max_gu, uint32_t* dn,
+                  uint32_t max_dn, uint32_t e, uint32_t bm, uint32_t gu_bn, uint32_t dn_bn,
+                  uint32_t gu_n, uint32_t dn_n, mh_stream_t stream) {
+    MH_ENSURE(counts && offsets && gu_off && dn_off && gu && dn, MH_ERR_INVALID,
+              "mh_moe_blocks: NULL argument");
+    MH_ENSURE(mh::aligned(gu, 16) && mh::aligned(dn, 16), MH_ERR_ALIGN,
+              "mh_moe_blocks: maps must be 16-byte aligned");
+    MH_ENSURE(bm > 0 && gu_bn > 0 && dn_bn > 0 && gu_n % gu_bn == 0 && dn_n % dn_bn == 0,
+              MH_ERR_INVALID, "mh_moe_blocks: tiles bm=%u bn=%u/%u do not divide %u/%u", bm,
+              gu_bn, dn_bn, gu_n, dn_n);
+    hipLaunchKernelGGL(k_blocks, dim3(e), dim3(128), 0, mh::as_stream(stream), counts, offsets,
+                       gu_off, dn_off, reinterpret_cast<uint4*>(gu), max_gu,
+                       reinterpret_cast<uint4*>(dn), max_dn, bm, gu_bn, dn_bn, gu_n, dn_n);
+    return mh::launch_status("mh_moe_blocks");
+}
+
+int mh_gather_rows_bf16(const uint16_t* table, const uint32_t* ids, uint16_t* out, uint32_t m,
+                        uint32_t h, uint32_t n_table, mh_stream_t stream) {
+    MH_ENSURE(table && ids && out, MH_ERR_INVALID, "mh_gather_rows_bf16: NULL argument");
+    MH_ENSURE(h % 8 == 0 && n_table > 0, MH_ERR_UNSUPPORTED,
+              "mh_gather_rows_bf16: row width %u not a multiple of 8", h);
+    MH_ENSURE(mh::aligned(table, 16) && mh::aligned(out, 16), MH_ERR_ALIGN,
+              "mh_gather_rows_bf16: rows must be 16-byte aligned");
+    if (m == 0) return MH_OK;
+    hipLaunchKernelGGL(k_gather_rows, dim3(grid_for(static_cast<size_t>(m) * h / 8)), dim3(256), 0,
+                       mh::as_stream(stream), table, ids, out, m, h, n_table);
+    return mh::launch_status("mh_gather_rows_bf16");
+}
+
+int mh_silu_mul_bf16(const uint16_t* gate, const uint16_t* up, uint16_t* out, size_t n,
+                     mh_stream_t stream) {
+    MH_ENSURE(gate && up && out, MH_ERR_INVALID, "mh_silu_mul_bf16: NULL argument");
+    if (n == 0) return MH_OK;
+    hipLaunchKernelGGL(k_silu_mul, dim3(grid_for(n)), dim3(256), 0, mh::as_stream(stream), gate, up,
+                       out, n);
+    return mh::launch_status("mh_silu_mul_bf16");
+}
+
+int mh_moe_combine_rows(const uint16_t* sorted, const uint32_t* slotpos, const uint16_t* weights,
+                        uint16_t* out, uint32_t m, uint32_t h, uint32_t topk, mh_stream_t stream) {
+    MH_ENSURE(sorted && slotpos && weights && out, MH_ERR_INVALID,
+              "mh_moe_combine_rows: NULL argument");
+    MH_ENSURE(h % 8 == 0, MH_ERR_UNSUPPORTED, "mh_moe_combine_rows: width %u not a multiple of 8", h);
+    MH_ENSURE(topk >= 1 && topk <= 8, MH_ERR_INVALID, "mh_moe_combine_rows: topk %u", topk);
+    MH_ENSURE(mh::aligned(sorted, 16) && mh::aligned(out, 16), MH_ERR_ALIGN,
+              "mh_moe_combine_rows: rows must be 16-byte aligned");
+    if (m == 0) return MH_OK;
+    hipLaunchKernelGGL(k_combine, dim3(grid_for(static_cast<size_t>(m) * h / 8)), dim3(256), 0,
+                       mh::as_stream(stream), sorted, slotpos, weights, out, m, h, topk, m * topk);
+    return mh::launch_status("mh_moe_combine_rows");
+}
+
+}  // extern "C"

@@ -1,0 +1,135 @@
+// moe_prefill_step.hip -- the whole prefill MoE block in one call
+// (src/lfm.rs:847-965 moe_prefill), on a caller-provided workspace.
+//
+// Sequence: router logits -> per-token top-k -> counting sort (counts,
+// offsets, stable scatter) -> block maps -> grouped gate/up GEMM with the
+// ids_sorted row gather and the SwiGLU epilogue fused -> grouped down GEMM ->
+// weighted combine.  Compared with the reference's sequence this drops the
+// materialised gathered rows and the separate gate/up outputs (two 4-byte
+// round trips per routed element); the values are the same.
+#include "mh_device.hpp"
+#include "mh_host.hpp"
+
+namespace {
+
+constexpr uint32_t kBM = 128;      // row tile of both grouped GEMMs
+constexpr uint32_t kGuBN = 128;    // gate/up tile width (fused SwiGLU)
+constexpr uint32_t kDnBN = 256;    // down tile width
+
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+struct Layout {
+    size_t off[MH_PREFILL_WS_REGIONS];
+    size_t total;
+    uint32_t max_gu, max_dn;
+};
+
+Layout layout_for(uint32_t m, uint32_t e, uint32_t topk, uint32_t d_model, uint32_t n_inter) {
+    const size_t s = static_cast<size_t>(m) * topk;
+    const uint32_t m_tiles = static_cast<uint32_t>((s + kBM - 1) / kBM) + e;
+    Layout l{};
+    l.max_gu = m_tiles * (n_inter / kGuBN);
+    l.max_dn = m_tiles * (d_model / kDnBN);
+    const size_t sizes[MH_PREFILL_WS_REGIONS] = {
+        static_cast<size_t>(m) * e * 4,  // logits f32 [m, e]
+        s * 4,                           // ids u32 [m, topk]
+        s * 2,                           // gw bf16 [m, topk]
+        static_cast<size_t>(e) * 4,      // counts
+        static_cast<size_t>(e) * 4,      // offsets
+        s * 4,                           // ids_sorted
+        s * 4,                           // slotpos
+        static_cast<size_t>(e) * 4,      // gate/up block offsets
+        static_cast<size_t>(e) * 4,      // down block offsets
+        static_cast<size_t>(l.max_gu) * 16,  // gate/up block map
+        static_cast<size_t>(l.max_dn) * 16,  // down block map
+        s * n_inter * 2,                 // act bf16 [s, n_inter]
+        s * d_model * 2,                 // ed bf16 [s, d_model]
+    };
+    size_t at = 0;
+    for (int i = 0; i < MH_PREFILL_WS_REGIONS; ++i) {
+        l.off[i] = at;
+        at = align256(at + sizes[i]);
+    }
+    l.total = at;
+    return l;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mh_moe_prefill_workspace(uint32_t m, uint32_t n_experts, uint32_t topk, uint32_t d_model,
+                                uint32_t n_inter, size_t* offsets) {
+    const Layout l = layout_for(m, n_experts, topk, d_model, n_inter);
+    if (offsets) {
+        for (int i = 0; i < MH_PREFILL_WS_REGIONS; ++i) offsets[i] = l.off[i];
+    }
+    return l.total;
+}
+
+int mh_moe_prefill(const void* router, int router_dtype, const float* bias, int mode, float eps,
+                   const mh_quant_weights* gate, const mh_quant_weights* up,
+                   const mh_quant_weights* down, uint32_t n_experts, uint32_t topk,
+                   const uint16_t* x, uint32_t m, uint16_t* out, void* workspace,
+                   size_t workspace_bytes, mh_stream_t stream) {
+    const char* op = "mh_moe_prefill";
+    MH_ENSURE(gate && up && down && x && out && workspace && router, MH_ERR_INVALID,
+              "%s: NULL argument", op);
+    MH_ENSURE(m > 0, MH_ERR_INVALID, "%s: no tokens", op);
+    MH_ENSURE(n_experts > 0 && n_experts <= 256 && gate->out_features % n_experts == 0 &&
+                  down->out_features % n_experts == 0,
+              MH_ERR_INVALID, "%s: stacked rows not divisible by %u experts", op, n_experts);
+    const uint32_t n_inter = gate->out_features / n_experts;
+    const uint32_t d_model = down->out_features / n_experts;
+    MH_ENSURE(gate->in_features == d_model && up->in_features == d_model &&
+                  up->out_features == gate->out_features && down->in_features == n_inter,
+              MH_ERR_INVALID, "%s: expert shapes do not chain", op);
+    MH_ENSURE(n_inter % kGuBN == 0 && d_model % kDnBN == 0, MH_ERR_UNSUPPORTED,
+              "%s: n_inter %% %u or d_model %% %u != 0", op, kGuBN, kDnBN);
+    MH_ENSURE(topk >= 1 && topk <= 8, MH_ERR_INVALID, "%s: topk %u", op, topk);
+    MH_ENSURE(mh::aligned(workspace, 256) && mh::aligned(x, 16) && mh::aligned(out, 16),
+              MH_ERR_ALIGN, "%s: workspace must be 256-byte aligned, x/out 16-byte aligned", op);
+    const Layout l = layout_for(m, n_experts, topk, d_model, n_inter);
+    MH_ENSURE(workspace_bytes >= l.total, MH_ERR_INVALID,
+              "%s: workspace holds %zu bytes, needs %zu", op, workspace_bytes, l.total);
+    for (const mh_quant_weights* w : {gate, up, down}) {
+        MH_TRY(mh::check_quant(w, op));
+        MH_ENSURE(w->bits == 4 && w->group_size == 64, MH_ERR_UNSUPPORTED,
+                  "%s: experts must be 4-bit group 64", op);
+    }
+
+    char* ws = static_cast<char*>(workspace);
+    auto at = [&](int region) { return ws + l.off[region]; };
+    float* logits = reinterpret_cast<float*>(at(MH_PREFILL_WS_LOGITS));
+    uint32_t* ids = reinterpret_cast<uint32_t*>(at(MH_PREFILL_WS_IDS));
+    uint16_t* gw = reinterpret_cast<uint16_t*>(at(MH_PREFILL_WS_GW));
+    uint32_t* counts = reinterpret_cast<uint32_t*>(at(MH_PREFILL_WS_COUNTS));
+    uint32_t* offsets = reinterpret_cast<uint32_t*>(at(MH_PREFILL_WS_OFFSETS));
+    uint32_t* ids_sorted = reinterpret_cast<uint32_t*>(at(MH_PREFILL_WS_IDS_SORTED));
+    uint32_t* slotpos = reinterpret_cast<uint32_t*>(at(MH_PREFILL_WS_SLOTPOS));
+    uint32_t* gu_off = reinterpret_cast<uint32_t*>(at(MH_PREFILL_WS_GU_OFF));
+    uint32_t* dn_off = reinterpret_cast<uint32_t*>(at(MH_PREFILL_WS_DN_OFF));
+    uint32_t* gu_map = reinterpret_cast<uint32_t*>(at(MH_PREFILL_WS_GU_MAP));
+    uint32_t* dn_map = reinterpret_cast<uint32_t*>(at(MH_PREFILL_WS_DN_MAP));
+    uint16_t* act = reinterpret_cast<uint16_t*>(at(MH_PREFILL_WS_ACT));
+    uint16_t* ed = reinterpret_cast<uint16_t*>(at(MH_PREFILL_WS_ED));
+    const uint32_t s = m * topk;
+
+    MH_TRY(mh_router_prefill(x, router, router_dtype, logits, m, d_model, n_experts, stream));
+    MH_TRY(mh_moe_route_batch(logits, bias, ids, gw, m, n_experts, topk, mode, eps, stream));
+    MH_TRY(mh_moe_zero_counts(counts, n_experts, stream));
+    MH_TRY(mh_moe_count_slots(ids, counts, s, n_experts, stream));
+    MH_TRY(mh_moe_offsets(counts, offsets, n_experts, stream));
+    MH_TRY(mh_moe_sorted(ids, offsets, ids_sorted, slotpos, m, n_experts, topk, stream));
+    MH_TRY(mh_moe_zero_blocks(gu_map, dn_map, l.max_gu, l.max_dn, stream));
+    MH_TRY(mh_moe_block_offsets(counts, gu_off, dn_off, n_experts, kBM, kGuBN, kDnBN, n_inter,
+                                d_model, stream));
+    MH_TRY(mh_moe_blocks(counts, offsets, gu_off, dn_off, gu_map, l.max_gu, dn_map, l.max_dn,
+                         n_experts, kBM, kGuBN, kDnBN, n_inter, d_model, stream));
+    MH_TRY(mh_gemm_q4_grouped_gu_act(x, ids_sorted, m, gate, up, act, gu_map, l.max_gu, s, n_inter,
+                                     kBM, kGuBN, stream));
+    MH_TRY(mh_gemm_q4_grouped(act, down, ed, dn_map, l.max_dn, s, d_model, kBM, kDnBN, stream));
+    return mh_moe_combine_rows(ed, slotpos, gw, out, m, d_model, topk, stream);
+}
+
+}  // extern "C"

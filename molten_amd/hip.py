@@ -95,8 +95,27 @@ _SIGNATURES = {
                       _vp, _vp, _vp, _vp],
     "mh_router_prefill": [_vp, _vp, _i32, _vp, _u32, _u32, _u32, _vp],
     "mh_moe_route_batch": [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _i32, _f32, _vp],
+    "mh_moe_zero_counts": [_vp, _u32, _vp],
+    "mh_moe_count_slots": [_vp, _vp, _u32, _u32, _vp],
+    "mh_moe_offsets": [_vp, _vp, _u32, _vp],
+    "mh_moe_sorted": [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp],
+    "mh_moe_zero_blocks": [_vp, _vp, _u32, _u32, _vp],
+    "mh_moe_block_offsets": [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _vp],
+    "mh_moe_blocks": [_vp, _vp, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _u32, _u32, _u32, _u32,
+                      _u32, _vp],
+    "mh_gather_rows_bf16": [_vp, _vp, _vp, _u32, _u32, _u32, _vp],
+    "mh_silu_mul_bf16": [_vp, _vp, _vp, _sz, _vp],
+    "mh_moe_combine_rows": [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp],
+    "mh_gemm_q4_grouped": [_vp, _qw, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp],
+    "mh_gemm_q4_grouped_gu": [_vp, _qw, _qw, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp],
+    "mh_gemm_q4_grouped_gu_act": [_vp, _vp, _u32, _qw, _qw, _vp, _vp, _u32, _u32, _u32, _u32,
+                                  _u32, _vp],
+    "mh_moe_prefill_workspace": [_u32, _u32, _u32, _u32, _u32, ctypes.POINTER(_sz)],
+    "mh_moe_prefill": [_vp, _i32, _vp, _i32, _f32, _qw, _qw, _qw, _u32, _u32, _vp, _u32, _vp,
+                       _vp, _sz, _vp],
 }
-_RESTYPES = {"mh_last_error": ctypes.c_char_p, "mh_version": ctypes.c_char_p}
+_RESTYPES = {"mh_last_error": ctypes.c_char_p, "mh_version": ctypes.c_char_p,
+             "mh_moe_prefill_workspace": ctypes.c_size_t}
 
 _lib: Optional[ctypes.CDLL] = None
 
@@ -304,3 +323,118 @@ def moe_route_batch(logits, bias, ids, gw, m: int, e: int, topk: int,
     """src/kernels/lfm.rs:536."""
     check(load().mh_moe_route_batch(_ptr(logits), _ptr(bias), _ptr(ids), _ptr(gw), m, e, topk,
                                     mode, eps, _stream(stream)), "moe_route_batch")
+
+
+# ------------------------------------------------------- prefill MoE ops --
+
+class MoeTile:
+    """Row x column tile of a grouped GEMM block map (src/kernels/quant.rs:19-40).
+    T32 / T128 are the reference's shapes; GU128 / DN128 are the MI355X tiles
+    the fused prefill uses for gate/up and down."""
+
+    T32 = (32, 64)
+    T128 = (128, 64)
+    GU128 = (128, 128)
+    DN128 = (128, 256)
+
+
+def moe_zero_counts(counts, e: int, stream=None) -> None:
+    check(load().mh_moe_zero_counts(_ptr(counts), e, _stream(stream)), "moe_zero_counts")
+
+
+def moe_count_slots(ids, counts, s: int, e: int, stream=None) -> None:
+    check(load().mh_moe_count_slots(_ptr(ids), _ptr(counts), s, e, _stream(stream)),
+          "moe_count_slots")
+
+
+def moe_offsets(counts, offsets, e: int, stream=None) -> None:
+    check(load().mh_moe_offsets(_ptr(counts), _ptr(offsets), e, _stream(stream)), "moe_offsets")
+
+
+def moe_sorted(ids, offsets, ids_sorted, slotpos, m: int, e: int, topk: int, stream=None) -> None:
+    check(load().mh_moe_sorted(_ptr(ids), _ptr(offsets), _ptr(ids_sorted), _ptr(slotpos), m, e,
+                               topk, _stream(stream)), "moe_sorted")
+
+
+def moe_zero_blocks(gu, dn, n_gu: int, n_dn: int, stream=None) -> None:
+    check(load().mh_moe_zero_blocks(_ptr(gu), _ptr(dn), n_gu, n_dn, _stream(stream)),
+          "moe_zero_blocks")
+
+
+def moe_block_offsets(counts, gu_off, dn_off, e: int, bm: int, gu_bn: int, dn_bn: int,
+                      gu_n: int, dn_n: int, stream=None) -> None:
+    check(load().mh_moe_block_offsets(_ptr(counts), _ptr(gu_off), _ptr(dn_off), e, bm, gu_bn,
+                                      dn_bn, gu_n, dn_n, _stream(stream)), "moe_block_offsets")
+
+
+def moe_blocks(counts, offsets, gu_off, dn_off, gu, max_gu: int, dn, max_dn: int, e: int, bm: int,
+               gu_bn: int, dn_bn: int, gu_n: int, dn_n: int, stream=None) -> None:
+    check(load().mh_moe_blocks(_ptr(counts), _ptr(offsets), _ptr(gu_off), _ptr(dn_off), _ptr(gu),
+                               max_gu, _ptr(dn), max_dn, e, bm, gu_bn, dn_bn, gu_n, dn_n,
+                               _stream(stream)), "moe_blocks")
+
+
+def gather_rows_bf16(table, ids, out, m: int, h: int, n_table: int, stream=None) -> None:
+    """src/kernels/elementwise.rs:59."""
+    check(load().mh_gather_rows_bf16(_ptr(table), _ptr(ids), _ptr(out), m, h, n_table,
+                                     _stream(stream)), "gather_rows_bf16")
+
+
+def silu_mul_bf16(gate, up, out, n: int, stream=None) -> None:
+    """src/kernels/elementwise.rs:48."""
+    check(load().mh_silu_mul_bf16(_ptr(gate), _ptr(up), _ptr(out), n, _stream(stream)),
+          "silu_mul_bf16")
+
+
+def moe_combine_rows(sorted_rows, slotpos, weights, out, m: int, h: int, topk: int,
+                     stream=None) -> None:
+    """src/kernels/lfm.rs:701."""
+    check(load().mh_moe_combine_rows(_ptr(sorted_rows), _ptr(slotpos), _ptr(weights), _ptr(out), m,
+                                     h, topk, _stream(stream)), "moe_combine_rows")
+
+
+def gemm_q4_grouped_mlx(a, w: QuantWeights, c, blocks, n_blocks: int, s_rows: int, n: int,
+                        tile=MoeTile.T128, stream=None) -> None:
+    """src/kernels/quant.rs:223."""
+    check(load().mh_gemm_q4_grouped(_ptr(a), _qref(w), _ptr(c), _ptr(blocks), n_blocks, s_rows, n,
+                                    tile[0], tile[1], _stream(stream)), "gemm_q4_grouped_mlx")
+
+
+def gemm_q4_grouped_mlx_gu(a, gate: QuantWeights, up: QuantWeights, gate_out, up_out, blocks,
+                           n_blocks: int, s_rows: int, n: int, tile=MoeTile.T32,
+                           stream=None) -> None:
+    """src/kernels/quant.rs:151."""
+    check(load().mh_gemm_q4_grouped_gu(_ptr(a), _qref(gate), _qref(up), _ptr(gate_out),
+                                       _ptr(up_out), _ptr(blocks), n_blocks, s_rows, n, tile[0],
+                                       tile[1], _stream(stream)), "gemm_q4_grouped_mlx_gu")
+
+
+def gemm_q4_grouped_gu_act(x, ids_sorted, x_rows: int, gate: QuantWeights, up: QuantWeights, act,
+                           blocks, n_blocks: int, s_rows: int, n: int, tile=MoeTile.GU128,
+                           stream=None) -> None:
+    """gate/up + SwiGLU with the row gather fused (no reference counterpart)."""
+    check(load().mh_gemm_q4_grouped_gu_act(_ptr(x), _ptr(ids_sorted), x_rows, _qref(gate),
+                                           _qref(up), _ptr(act), _ptr(blocks), n_blocks, s_rows,
+                                           n, tile[0], tile[1], _stream(stream)),
+          "gemm_q4_grouped_gu_act")
+
+
+PREFILL_WS_REGIONS = ["logits", "ids", "gw", "counts", "offsets", "ids_sorted", "slotpos",
+                      "gu_off", "dn_off", "gu_map", "dn_map", "act", "ed"]
+
+
+def moe_prefill_workspace(m: int, n_experts: int, topk: int, d_model: int, n_inter: int):
+    """(total bytes, {region: byte offset}) of mh_moe_prefill's workspace."""
+    offs = (ctypes.c_size_t * len(PREFILL_WS_REGIONS))()
+    total = load().mh_moe_prefill_workspace(m, n_experts, topk, d_model, n_inter, offs)
+    return int(total), dict(zip(PREFILL_WS_REGIONS, [int(o) for o in offs]))
+
+
+def moe_prefill(router, bias, gate: QuantWeights, up: QuantWeights, down: QuantWeights,
+                n_experts: int, topk: int, x, m: int, out, workspace, workspace_bytes: int,
+                mode: int = ROUTE_SIGMOID_BIAS, eps: float = 1e-6, stream=None) -> None:
+    """src/lfm.rs:847-965 moe_prefill as one call."""
+    check(load().mh_moe_prefill(_ptr(router), _dtype_of(router), _ptr(bias), mode, eps,
+                                _qref(gate), _qref(up), _qref(down), n_experts, topk, _ptr(x), m,
+                                _ptr(out), _ptr(workspace), workspace_bytes, _stream(stream)),
+          "moe_prefill")

@@ -155,14 +155,15 @@ void orc_moe_sorted(const uint32_t* ids, const uint32_t* offsets, uint32_t m,
 
 /* ---- a14: block maps (lfm.metal:1687-1770; src/lfm.rs:896-933) ------------
  * Entry i of expert e: uint4(m0, e*N + n0, n0, m_end), row tiles of bm,
- * column tiles of bn, expert order; the tail up to max_* is zero.
+ * column tiles of gu_bn / dn_bn (the reference uses one bn for both), expert
+ * order; the tail up to max_* is zero.
  * Pinned: brute-force enumeration from the definition in Python. */
 void orc_moe_block_offsets(const uint32_t* counts, uint32_t e, uint32_t bm,
-                           uint32_t bn, uint32_t gu_n, uint32_t dn_n,
+                           uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n, uint32_t dn_n,
                            uint32_t* gu_off, uint32_t* dn_off);
 void orc_moe_blocks(const uint32_t* counts, const uint32_t* offsets,
                     const uint32_t* gu_off, const uint32_t* dn_off, uint32_t e,
-                    uint32_t bm, uint32_t bn, uint32_t gu_n, uint32_t dn_n,
+                    uint32_t bm, uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n, uint32_t dn_n,
                     uint32_t* gu, uint32_t max_gu, uint32_t* dn, uint32_t max_dn);
 
 /* ---- a15 / a17 / a18: gather, SwiGLU, combine (elementwise.metal:7-52;
@@ -198,6 +199,18 @@ void orc_moe_prefill(const void* router, int router_is_f32, const float* bias,
                      uint16_t* gw, uint32_t* counts, uint32_t* offsets,
                      uint32_t* ids_sorted, uint32_t* slotpos, uint16_t* act,
                      uint16_t* ed);
+
+/* The same with the expert GEMMs computed only for tokens whose mask byte is
+ * non-zero (routing and sort still cover all m tokens); rows of masked-out
+ * tokens in act / ed / out are zero.  Used to check full-size prefill runs on
+ * a token sample. */
+void orc_moe_prefill_masked(const void* router, int router_is_f32, const float* bias, int mode,
+                            float eps, const orc_qw* gate, const orc_qw* up, const orc_qw* down,
+                            uint32_t n_experts, uint32_t topk, uint32_t d_model, uint32_t n_inter,
+                            uint32_t m, const uint16_t* x, const uint8_t* token_mask,
+                            uint16_t* out, uint32_t* ids_o, uint16_t* gw_o, uint32_t* counts_o,
+                            uint32_t* offsets_o, uint32_t* ids_sorted_o, uint32_t* slotpos_o,
+                            uint16_t* act_o, uint16_t* ed_o);
 
 /* OpenMP thread count used by the heavy loops (0 = library default). */
 void orc_set_threads(int n);

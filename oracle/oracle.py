@@ -230,24 +230,25 @@ def moe_sorted(ids: np.ndarray, offsets: np.ndarray, m: int, e: int, topk: int):
     return ids_sorted, slotpos
 
 
-def moe_block_offsets(counts, bm, bn, gu_n, dn_n):
+def moe_block_offsets(counts, bm, gu_bn, dn_bn, gu_n, dn_n):
     counts = np.ascontiguousarray(counts, np.uint32)
     gu_off = np.empty_like(counts)
     dn_off = np.empty_like(counts)
     lib().orc_moe_block_offsets(_p(counts), ctypes.c_uint32(counts.size), ctypes.c_uint32(bm),
-                                ctypes.c_uint32(bn), ctypes.c_uint32(gu_n), ctypes.c_uint32(dn_n),
-                                _p(gu_off), _p(dn_off))
+                                ctypes.c_uint32(gu_bn), ctypes.c_uint32(dn_bn),
+                                ctypes.c_uint32(gu_n), ctypes.c_uint32(dn_n), _p(gu_off),
+                                _p(dn_off))
     return gu_off, dn_off
 
 
-def moe_blocks(counts, offsets, gu_off, dn_off, bm, bn, gu_n, dn_n, max_gu, max_dn):
+def moe_blocks(counts, offsets, gu_off, dn_off, bm, gu_bn, dn_bn, gu_n, dn_n, max_gu, max_dn):
     c = [np.ascontiguousarray(a, np.uint32) for a in (counts, offsets, gu_off, dn_off)]
     gu = np.empty((max_gu, 4), np.uint32)
     dn = np.empty((max_dn, 4), np.uint32)
     lib().orc_moe_blocks(_p(c[0]), _p(c[1]), _p(c[2]), _p(c[3]), ctypes.c_uint32(c[0].size),
-                         ctypes.c_uint32(bm), ctypes.c_uint32(bn), ctypes.c_uint32(gu_n),
-                         ctypes.c_uint32(dn_n), _p(gu), ctypes.c_uint32(max_gu), _p(dn),
-                         ctypes.c_uint32(max_dn))
+                         ctypes.c_uint32(bm), ctypes.c_uint32(gu_bn), ctypes.c_uint32(dn_bn),
+                         ctypes.c_uint32(gu_n), ctypes.c_uint32(dn_n), _p(gu),
+                         ctypes.c_uint32(max_gu), _p(dn), ctypes.c_uint32(max_dn))
     return gu, dn
 
 
@@ -291,7 +292,7 @@ def gemm_q4_grouped(a: np.ndarray, h, blocks: np.ndarray, n_blocks: int, n: int,
 
 
 def moe_prefill(router, bias, mode, gate, up, down, n_experts, topk, d_model, n_inter, x,
-                eps: float = 1e-6):
+                eps: float = 1e-6, token_mask=None):
     router = np.ascontiguousarray(router)
     b = None if bias is None else np.ascontiguousarray(bias, np.float32)
     x = np.ascontiguousarray(x, np.uint16)
@@ -305,11 +306,13 @@ def moe_prefill(router, bias, mode, gate, up, down, n_experts, topk, d_model, n_
         ed=np.empty((s, d_model), np.uint16),
     )
     g, u, d = qw(gate), qw(up), qw(down)
-    lib().orc_moe_prefill(_p(router), ctypes.c_int(1 if router.dtype == np.float32 else 0), _p(b),
+    mask = None if token_mask is None else np.ascontiguousarray(token_mask, np.uint8)
+    lib().orc_moe_prefill_masked(_p(router), ctypes.c_int(1 if router.dtype == np.float32 else 0),
+                          _p(b),
                           ctypes.c_int(mode), ctypes.c_float(eps), ctypes.byref(g), ctypes.byref(u),
                           ctypes.byref(d), ctypes.c_uint32(n_experts), ctypes.c_uint32(topk),
                           ctypes.c_uint32(d_model), ctypes.c_uint32(n_inter), ctypes.c_uint32(m),
-                          _p(x), _p(r["out"]), _p(r["ids"]), _p(r["gw"]), _p(r["counts"]),
+                          _p(x), _p(mask), _p(r["out"]), _p(r["ids"]), _p(r["gw"]), _p(r["counts"]),
                           _p(r["offsets"]), _p(r["ids_sorted"]), _p(r["slotpos"]), _p(r["act"]),
                           _p(r["ed"]))
     return r

@@ -47,15 +47,16 @@ void orc_moe_sorted(const uint32_t* ids, const uint32_t* offsets, uint32_t m, ui
 
 /* ---------------------------------------------------------- block map --- */
 
-void orc_moe_block_offsets(const uint32_t* counts, uint32_t e, uint32_t bm, uint32_t bn,
-                           uint32_t gu_n, uint32_t dn_n, uint32_t* gu_off, uint32_t* dn_off) {
+void orc_moe_block_offsets(const uint32_t* counts, uint32_t e, uint32_t bm, uint32_t gu_bn,
+                           uint32_t dn_bn, uint32_t gu_n, uint32_t dn_n, uint32_t* gu_off,
+                           uint32_t* dn_off) {
     uint32_t ag = 0, ad = 0;
     for (uint32_t i = 0; i < e; ++i) {
         gu_off[i] = ag;
         dn_off[i] = ad;
         const uint32_t rows = (counts[i] + bm - 1) / bm;
-        ag += rows * (gu_n / bn);
-        ad += rows * (dn_n / bn);
+        ag += rows * (gu_n / gu_bn);
+        ad += rows * (dn_n / dn_bn);
     }
 }
 
@@ -80,8 +81,8 @@ static void fill_map(uint32_t count, uint32_t off, uint32_t base, uint32_t ex, u
 }
 
 void orc_moe_blocks(const uint32_t* counts, const uint32_t* offsets, const uint32_t* gu_off,
-                    const uint32_t* dn_off, uint32_t e, uint32_t bm, uint32_t bn,
-                    uint32_t gu_n, uint32_t dn_n, uint32_t* gu, uint32_t max_gu,
+                    const uint32_t* dn_off, uint32_t e, uint32_t bm, uint32_t gu_bn,
+                    uint32_t dn_bn, uint32_t gu_n, uint32_t dn_n, uint32_t* gu, uint32_t max_gu,
                     uint32_t* dn, uint32_t max_dn) {
     memset(gu, 0, (size_t)max_gu * 16);
     memset(dn, 0, (size_t)max_dn * 16);
@@ -89,8 +90,8 @@ void orc_moe_blocks(const uint32_t* counts, const uint32_t* offsets, const uint3
         if (counts[i] == 0) {
             continue;
         }
-        fill_map(counts[i], offsets[i], gu_off[i], i, bm, bn, gu_n, gu, max_gu);
-        fill_map(counts[i], offsets[i], dn_off[i], i, bm, bn, dn_n, dn, max_dn);
+        fill_map(counts[i], offsets[i], gu_off[i], i, bm, gu_bn, gu_n, gu, max_gu);
+        fill_map(counts[i], offsets[i], dn_off[i], i, bm, dn_bn, dn_n, dn, max_dn);
     }
 }
 
@@ -201,13 +202,13 @@ void orc_gemm_q4_grouped(const uint16_t* a, const orc_qw* w, uint16_t* c,
 
 /* --------------------------------------------------------- MoE prefill --- */
 
-void orc_moe_prefill(const void* router, int router_is_f32, const float* bias, int mode,
-                     float eps, const orc_qw* gate, const orc_qw* up, const orc_qw* down,
-                     uint32_t n_experts, uint32_t topk, uint32_t d_model, uint32_t n_inter,
-                     uint32_t m, const uint16_t* x, uint16_t* out, uint32_t* ids_o,
-                     uint16_t* gw_o, uint32_t* counts_o, uint32_t* offsets_o,
-                     uint32_t* ids_sorted_o, uint32_t* slotpos_o, uint16_t* act_o,
-                     uint16_t* ed_o) {
+void orc_moe_prefill_masked(const void* router, int router_is_f32, const float* bias, int mode,
+                            float eps, const orc_qw* gate, const orc_qw* up, const orc_qw* down,
+                            uint32_t n_experts, uint32_t topk, uint32_t d_model, uint32_t n_inter,
+                            uint32_t m, const uint16_t* x, const uint8_t* token_mask,
+                            uint16_t* out, uint32_t* ids_o, uint16_t* gw_o, uint32_t* counts_o,
+                            uint32_t* offsets_o, uint32_t* ids_sorted_o, uint32_t* slotpos_o,
+                            uint16_t* act_o, uint16_t* ed_o) {
     const uint32_t s = m * topk, E = n_experts, H = d_model, I = n_inter;
     float* logits = (float*)malloc((size_t)m * E * sizeof(float));
     uint32_t* ids = (uint32_t*)malloc((size_t)s * 4);
@@ -226,9 +227,22 @@ void orc_moe_prefill(const void* router, int router_is_f32, const float* bias, i
     orc_moe_sorted(ids, offsets, m, E, topk, ids_sorted, slotpos);
 
     enum { RB = 8 };
+    /* rows of each expert segment to compute (all, or those of masked-in tokens) */
+    uint32_t* live = (uint32_t*)malloc((size_t)s * 4);
+    uint32_t* n_live = (uint32_t*)calloc(E, 4);
+    for (uint32_t ex = 0; ex < E; ++ex) {
+        for (uint32_t i = 0; i < counts[ex]; ++i) {
+            const uint32_t row = offsets[ex] + i;
+            if (!token_mask || token_mask[ids_sorted[row]]) {
+                live[offsets[ex] + n_live[ex]++] = row;
+            }
+        }
+    }
+    memset(act, 0, (size_t)s * I * 2);
+    memset(ed, 0, (size_t)s * H * 2);
 #pragma omp parallel for schedule(dynamic) num_threads(ORC_THREADS)
     for (long ex = 0; ex < (long)E; ++ex) {
-        const uint32_t cnt = counts[ex], off = offsets[ex];
+        const uint32_t cnt = n_live[ex], off = offsets[ex];
         if (cnt == 0) {
             continue;
         }
@@ -246,7 +260,7 @@ void orc_moe_prefill(const void* router, int router_is_f32, const float* bias, i
         for (uint32_t i0 = 0; i0 < cnt; i0 += RB) {
             const uint32_t nr = (cnt - i0 < RB) ? cnt - i0 : RB;
             for (uint32_t i = 0; i < nr; ++i) {
-                const uint32_t t = ids_sorted[off + i0 + i];
+                const uint32_t t = ids_sorted[live[off + i0 + i]];
                 for (uint32_t kk = 0; kk < H; ++kk) {
                     xa[(size_t)i * H + kk] = orc_bf16_to_f32(x[(size_t)t * H + kk]);
                 }
@@ -259,14 +273,14 @@ void orc_moe_prefill(const void* router, int router_is_f32, const float* bias, i
                     const float u = bfr(ua[(size_t)i * I + j]);
                     const float sg = bfr(g / (1.0f + orc_expf(-g)));
                     const uint16_t av = orc_f32_to_bf16(sg * u);
-                    act[(size_t)(off + i0 + i) * I + j] = av;
+                    act[(size_t)live[off + i0 + i] * I + j] = av;
                     aa[(size_t)i * I + j] = orc_bf16_to_f32(av);
                 }
             }
             rows_times_wt(aa, nr, I, wd, H, da);
             for (uint32_t i = 0; i < nr; ++i) {
                 for (uint32_t h = 0; h < H; ++h) {
-                    ed[(size_t)(off + i0 + i) * H + h] = orc_f32_to_bf16(da[(size_t)i * H + h]);
+                    ed[(size_t)live[off + i0 + i] * H + h] = orc_f32_to_bf16(da[(size_t)i * H + h]);
                 }
             }
         }
@@ -279,6 +293,8 @@ void orc_moe_prefill(const void* router, int router_is_f32, const float* bias, i
         free(wu);
         free(wg);
     }
+    free(n_live);
+    free(live);
     orc_moe_combine_rows(ed, slotpos, gw, m, H, topk, out);
 
     if (ids_o) memcpy(ids_o, ids, (size_t)s * 4);
@@ -298,4 +314,16 @@ void orc_moe_prefill(const void* router, int router_is_f32, const float* bias, i
     free(gw);
     free(ids);
     free(logits);
+}
+
+void orc_moe_prefill(const void* router, int router_is_f32, const float* bias, int mode,
+                     float eps, const orc_qw* gate, const orc_qw* up, const orc_qw* down,
+                     uint32_t n_experts, uint32_t topk, uint32_t d_model, uint32_t n_inter,
+                     uint32_t m, const uint16_t* x, uint16_t* out, uint32_t* ids_o,
+                     uint16_t* gw_o, uint32_t* counts_o, uint32_t* offsets_o,
+                     uint32_t* ids_sorted_o, uint32_t* slotpos_o, uint16_t* act_o,
+                     uint16_t* ed_o) {
+    orc_moe_prefill_masked(router, router_is_f32, bias, mode, eps, gate, up, down, n_experts,
+                           topk, d_model, n_inter, m, x, NULL, out, ids_o, gw_o, counts_o,
+                           offsets_o, ids_sorted_o, slotpos_o, act_o, ed_o);
 }
