@@ -1,0 +1,310 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized-matmul hot path.
+
+One step = one pass of the hot path over one batch of synthetic input with
+all inputs resident in HBM.  The headline line is BASELINE config 2 (the Q4
+LM head 65536 x 2048 GEMV with fused argmax: logits stored and the token id
+written by the same launch), in GB/s of algorithmic bytes.  The other
+BASELINE configs are measured in the same run and reported under "others":
+
+  config 1  Q4 GEMV 2048 x 2048, batch 1                 GB/s (HBM)
+  config 3  MoE decode step (router, top-4 of 64, experts) GB/s (HBM)
+  config 4  prefill MoE, 4096 tokens x top-4 of 64        TFLOP/s (bf16 MFMA)
+  config 5  Q6 LM head 65536 x 2048 + argmax, b=1 / b=8   GB/s (HBM)
+
+Weights are synthetic (BASELINE distributions, random-init, generated on the
+GPU) and rotated over enough copies (>= 300 MB) that the 256 MB Infinity
+Cache cannot hold the working set; the MoE inputs vary per step so routing
+changes.  Kernel times come from HIP events recorded on the launch stream.
+The CPU baseline is the C oracle timed on the host cores on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+
+# Algorithmic bytes per step.
+BYTES = {
+    "config1": 2_367_488,
+    "config2": 75_632_644,
+    "config3": 21_504_000,
+    "config5_b1": 109_187_076,
+    "config5_b8": 110_133_280,
+}
+FLOPS_CONFIG4 = 309_237_645_312
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_quant(torch, n, k, bits, copies, dev, gen):
+    from molten_amd import hip
+
+    out = []
+    for _ in range(copies):
+        words = k * bits // 32
+        codes = torch.randint(-2**31, 2**31 - 1, (n, words), dtype=torch.int32, device=dev,
+                              generator=gen)
+        g = k // 64
+        scales = (torch.randn(n, g, device=dev, generator=gen).abs() * 0.02 + 1e-3)
+        biases = torch.randn(n, g, device=dev, generator=gen) * 0.02
+        scales = scales.to(torch.bfloat16).view(torch.int16)
+        biases = biases.to(torch.bfloat16).view(torch.int16)
+        out.append((hip.QuantWeights(codes, scales, biases, n, k, 64, bits), (codes, scales, biases)))
+    return out
+
+
+def bf16_randn(torch, shape, dev, gen, std=1.0):
+    return (torch.randn(shape, device=dev, generator=gen) * std).to(torch.bfloat16).view(torch.int16)
+
+
+def timed(torch, fn, steps, warmup):
+    """Average ms per call of fn(i) over `steps` calls after `warmup` calls,
+    bracketed by synchronizes; events on the current (launch) stream."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(warmup + i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def bench_lm_head(torch, hip, dev, gen, bits, batch, steps, warmup, copies):
+    n, k = 65536, 2048
+    ws = make_quant(torch, n, k, bits, copies, dev, gen)
+    x = bf16_randn(torch, (batch, k), dev, gen)
+    y = torch.empty((batch, n), dtype=torch.int16, device=dev)
+    scratch = torch.zeros(hip.argmax_scratch_words(batch), dtype=torch.int64, device=dev)
+    ids = torch.empty(batch, dtype=torch.int32, device=dev)
+
+    def step(i):
+        hip.gemv_quant_argmax(ws[i % copies][0], x, y, scratch, ids, batch)
+
+    ms = timed(torch, step, steps, warmup)
+    del ws
+    return ms
+
+
+def bench_config1(torch, hip, dev, gen, steps, warmup):
+    copies = 128  # 128 x 2.36 MB = 302 MB
+    ws = make_quant(torch, 2048, 2048, 4, copies, dev, gen)
+    x = bf16_randn(torch, (1, 2048), dev, gen)
+    y = torch.empty((1, 2048), dtype=torch.int16, device=dev)
+    ms = timed(torch, lambda i: hip.gemv_quant(ws[i % copies][0], x, y, 1), steps, warmup)
+    del ws
+    return ms
+
+
+def moe_set(torch, dev, gen, E=64, H=2048, I=1536):
+    gate = make_quant(torch, E * I, H, 4, 1, dev, gen)[0]
+    up = make_quant(torch, E * I, H, 4, 1, dev, gen)[0]
+    down = make_quant(torch, E * H, I, 4, 1, dev, gen)[0]
+    router = bf16_randn(torch, (E, H), dev, gen, std=0.02)
+    return gate, up, down, router
+
+
+def bench_config3(torch, hip, dev, gen, steps, warmup):
+    E, H, I, topk = 64, 2048, 1536, 4
+    sets = [moe_set(torch, dev, gen) for _ in range(4)]  # 4 x 340 MB of experts
+    xs = [bf16_randn(torch, (H,), dev, gen) for _ in range(16)]
+    out = torch.empty(H, dtype=torch.int16, device=dev)
+    logits = torch.empty(E, dtype=torch.float32, device=dev)
+    ids = torch.empty(topk, dtype=torch.int32, device=dev)
+    wt = torch.empty(topk, dtype=torch.int16, device=dev)
+    act = torch.empty((topk, I), dtype=torch.int16, device=dev)
+    counter = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def step(i):
+        g, u, d, r = sets[i % len(sets)]
+        hip.moe_decode(r, None, g[0], u[0], d[0], E, topk, xs[i % len(xs)], out, logits, ids, wt,
+                       act, counter, mode=hip.ROUTE_SOFTMAX)
+
+    ms = timed(torch, step, steps, warmup)
+    del sets
+    return ms
+
+
+def bench_config4(torch, hip, dev, gen, steps, warmup):
+    E, H, I, topk, m = 64, 2048, 1536, 4, 4096
+    sets = [moe_set(torch, dev, gen) for _ in range(2)]
+    x = bf16_randn(torch, (m, H), dev, gen)
+    out = torch.empty((m, H), dtype=torch.int16, device=dev)
+    total, offs = hip.moe_prefill_workspace(m, E, topk, H, I)
+    ws = torch.zeros(total, dtype=torch.uint8, device=dev)
+
+    def step(i):
+        g, u, d, r = sets[i % len(sets)]
+        hip.moe_prefill(r, None, g[0], u[0], d[0], E, topk, x, m, out, ws, total,
+                        mode=hip.ROUTE_SOFTMAX)
+
+    ms_step = timed(torch, step, max(2, steps // 4), max(1, warmup // 4))
+    # the two grouped GEMMs alone, replayed on the workspace of the last step
+    g, u, d, r = sets[(max(2, steps // 4) + max(1, warmup // 4) - 1) % len(sets)]
+    base = ws.data_ptr()
+    s = m * topk
+    gu_bn, dn_bn, bm = 128, 256, 128
+    m_tiles = -(-s // bm) + E
+    max_gu, max_dn = m_tiles * I // gu_bn, m_tiles * H // dn_bn
+
+    def gemms(i):
+        hip.gemm_q4_grouped_gu_act(x, base + offs["ids_sorted"], m, g[0], u[0], base + offs["act"],
+                                   base + offs["gu_map"], max_gu, s, I, hip.MoeTile.GU128)
+        hip.gemm_q4_grouped_mlx(base + offs["act"], d[0], base + offs["ed"], base + offs["dn_map"],
+                                max_dn, s, H, hip.MoeTile.DN128)
+
+    ms_gemm = timed(torch, gemms, max(2, steps // 4), 1)
+    del sets, ws
+    return ms_step, ms_gemm
+
+
+def cpu_baseline_config2(budget_s: float):
+    """The C oracle's Q4 LM-head GEMV (65536 x 2048, batch 1) + argmax on the
+    host cores, repeated for about `budget_s` seconds."""
+    import numpy as np
+
+    from molten_amd import layout
+    from oracle import oracle as orc
+
+    rng = np.random.default_rng(0)
+    h = layout.synth_quant(rng, 65536, 2048, 4)
+    x = layout.synth_bf16(rng, (1, 2048))
+    orc.gemv_quant(h, x, 1)  # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        y = orc.gemv_quant(h, x, 1)
+        orc.argmax_bf16(y[0])
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 1000:
+            break
+    per = el / reps
+    return dict(value=round(BYTES["config2"] / per / 1e9, 3), unit="GB/s", cores=orc.get_threads(),
+                kind="port",
+                sample=f"full config 2 workload (65536x2048 Q4 GEMV + argmax) x {reps} reps, "
+                       f"{el:.1f} s, {per * 1e3:.1f} ms per step")
+
+
+def read_traffic():
+    """HBM bytes per launch of the headline kernel from the committed rocprof
+    PMC summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), if present."""
+    p = os.path.join(ROOT, "profiles", "gemv_q4_lm_head_traffic.json")
+    try:
+        with open(p) as f:
+            return json.load(f).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="time budget of the CPU baseline sample (0 = skip)")
+    ap.add_argument("--only-headline", action="store_true", help="skip configs 1, 3, 4, 5")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="also run a plain device copy of this many MiB (PMC byte calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(--gpus must be 1).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from molten_amd import hip
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    hip.load()
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    steps, warmup = args.steps, args.warmup
+
+    log("config 2: Q4 LM head + argmax")
+    ms2 = bench_lm_head(torch, hip, dev, gen, 4, 1, steps, warmup, copies=5)
+    gbs2 = BYTES["config2"] / (ms2 * 1e-3) / 1e9
+    if args.calibrate_copy_mib > 0:
+        src = torch.ones(args.calibrate_copy_mib << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    others = {}
+    if not args.only_headline:
+        log("config 1: Q4 GEMV 2048x2048")
+        ms1 = bench_config1(torch, hip, dev, gen, steps, warmup)
+        others["config1_q4_gemv_2048"] = dict(
+            value=round(BYTES["config1"] / (ms1 * 1e-3) / 1e9, 1), unit="GB/s",
+            ms_per_step=round(ms1, 5), frac_of_hbm_peak=round(BYTES["config1"] / (ms1 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+        log("config 3: MoE decode step")
+        ms3 = bench_config3(torch, hip, dev, gen, steps, warmup)
+        v3 = BYTES["config3"] / (ms3 * 1e-3) / 1e9
+        others["config3_moe_decode_step"] = dict(value=round(v3, 1), unit="GB/s",
+                                                 ms_per_step=round(ms3, 5),
+                                                 frac_of_hbm_peak=round(v3 / HBM_PEAK_GBS, 4))
+        log("config 5: Q6 LM head + argmax, b=1 and b=8")
+        for b, key in ((1, "config5_b1"), (8, "config5_b8")):
+            ms5 = bench_lm_head(torch, hip, dev, gen, 6, b, steps, warmup, copies=3)
+            v5 = BYTES[key] / (ms5 * 1e-3) / 1e9
+            others[f"{key}_q6_lm_head_argmax"] = dict(value=round(v5, 1), unit="GB/s",
+                                                      ms_per_step=round(ms5, 5),
+                                                      frac_of_hbm_peak=round(v5 / HBM_PEAK_GBS, 4))
+        log("config 4: prefill MoE (4096 tokens)")
+        ms4, ms4g = bench_config4(torch, hip, dev, gen, steps, warmup)
+        others["config4_prefill_moe"] = dict(
+            value=round(FLOPS_CONFIG4 / (ms4 * 1e-3) / 1e12, 2), unit="TFLOP/s",
+            ms_per_step=round(ms4, 4),
+            grouped_gemm_only_tflops=round(FLOPS_CONFIG4 / (ms4g * 1e-3) / 1e12, 2),
+            grouped_gemm_only_ms=round(ms4g, 4),
+            frac_of_bf16_peak=round(FLOPS_CONFIG4 / (ms4g * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        log("CPU baseline (oracle, config 2)")
+        cpu = cpu_baseline_config2(args.cpu_seconds)
+
+    line = {
+        "metric": "Q4 LM-head GEMV + argmax HBM GB/s (config 2; MoE decode / prefill under others)",
+        "value": round(gbs2, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms2, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (BASELINE distributions, random init, 5 rotated weight copies)",
+        "config": {"workload": "config2_q4_lm_head_argmax", "n": 65536, "k": 2048, "bits": 4,
+                   "group_size": 64, "batch": 1, "outputs": "bf16 logits + argmax id"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs2, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs2 / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic()},
+        "cpu_baseline": cpu,
+        "others": others,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

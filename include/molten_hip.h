@@ -119,14 +119,18 @@ int mh_gemv_quant(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uin
 int mh_gemv_head_argmax(const mh_quant_weights* w, const uint16_t* x, uint64_t* best,
                         uint32_t batch, mh_stream_t stream);
 
-/* Head GEMV that stores the bf16 logits (y, may be NULL) AND folds the
- * argmax keys into best[batch] (zero on entry).  With done != NULL (one u32,
- * zero on entry) the last workgroup to finish writes ids[b] = argmax token of
- * row b and leaves best and done zero again: one launch, no tail kernel.
- * No reference counterpart for the stored-logits form: BASELINE configs 2/5. */
+/* Head GEMV that stores the bf16 logits (y, may be NULL) and writes
+ * ids[b] = argmax token of row b in the same launch: the last workgroup to
+ * finish converts the keys (no tail kernel).  scratch: u64 words, at least
+ * MH_ARGMAX_SCRATCH_WORDS(batch), zero on entry and left zero; calls that
+ * overlap on one scratch buffer race.  The keys are folded through a
+ * two-level tree of MH_ARGMAX_GROUPS groups so few workgroups contend on any
+ * one atomic.  No reference counterpart (BASELINE configs 2 and 5 store the
+ * logits; molten's head stores none). */
+#define MH_ARGMAX_GROUPS 32u
+#define MH_ARGMAX_SCRATCH_WORDS(batch) ((MH_ARGMAX_GROUPS + 1u) * (batch) + MH_ARGMAX_GROUPS + 1u)
 int mh_gemv_quant_argmax(const mh_quant_weights* w, const uint16_t* x, uint16_t* y,
-                         uint64_t* best, uint32_t* done, uint32_t* ids, uint32_t batch,
-                         mh_stream_t stream);
+                         uint64_t* scratch, uint32_t* ids, uint32_t batch, mh_stream_t stream);
 
 /* src/kernels/lfm.rs:850 token_tail without `next`: out_tok[b] = token of
  * key best[b]; best[b] is cleared. */

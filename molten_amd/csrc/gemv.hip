@@ -25,8 +25,8 @@ struct GemvArgs {
     const uint16_t* biases;
     const uint16_t* x;        // bf16 [batch, k]
     uint16_t* y;              // bf16 [batch, n] or null
-    unsigned long long* best; // [batch] argmax keys or null
-    uint32_t* done;           // finisher counter or null
+    unsigned long long* best; // [batch] keys, or the finisher scratch
+    const void* done;         // non-null: finisher mode (best is the scratch)
     uint32_t* ids;            // [batch] tokens written by the finisher
     uint32_t n, k, gs, row_words, groups;
 };
@@ -40,17 +40,36 @@ __device__ __forceinline__ void load_row_chunk(const GemvArgs& a, uint32_t row, 
     b = mh::bf16_to_f32(a.biases[static_cast<size_t>(row) * a.groups + g]);
 }
 
-// Per-wave argmax state folded into the workgroup, then into best[b].
-// bv/bi are wave-uniform.  All cross-workgroup traffic is atomic: every
-// workgroup's atomicMax has returned (been performed) before its thread 0
-// increments the counter, and the finisher reads the keys with atomic swaps,
-// so no cache write-back fence is needed.
+// Per-wave argmax state folded into the workgroup, then into the keys.
+// bv/bi are wave-uniform.  Cross-workgroup traffic is atomic only: an
+// atomic's returned value is consumed before the workgroup signals, so it has
+// been performed at the coherence point and no cache write-back is needed.
+//
+// Without a finisher (a.done == null: the reference's gemv_head_argmax) every
+// workgroup folds its key into best[b].  With the finisher, contention is a
+// two-level tree: workgroup w folds into group key (w % G), the last
+// workgroup of each group folds that into the final key, and the last group
+// writes the token ids and re-zeroes the scratch (layout in molten_hip.h:
+// group keys [G][B] | final keys [B] | group counters [G] | top counter).
+constexpr uint32_t kArgGroups = MH_ARGMAX_GROUPS;
+
+__device__ __forceinline__ unsigned long long amax(unsigned long long* p, unsigned long long v) {
+    return __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long axchg(unsigned long long* p, unsigned long long v) {
+    return __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long aadd(unsigned long long* p, unsigned long long v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int B>
 __device__ void fold_argmax(const GemvArgs& a, const float (&bv)[B], const uint32_t (&bi)[B],
                             int lane, int wave) {
     __shared__ float sv[kWaves][B];
     __shared__ uint32_t si[kWaves][B];
-    __shared__ uint32_t last;
+    __shared__ uint32_t flag;
+    __shared__ unsigned long long sink;
     if (lane == 0) {
 #pragma unroll
         for (int b = 0; b < B; ++b) {
@@ -59,6 +78,7 @@ __device__ void fold_argmax(const GemvArgs& a, const float (&bv)[B], const uint3
         }
     }
     __syncthreads();
+    unsigned long long key = 0;
     if (threadIdx.x < B) {
         const int b = threadIdx.x;
         float v = sv[0][b];
@@ -66,31 +86,51 @@ __device__ void fold_argmax(const GemvArgs& a, const float (&bv)[B], const uint3
         for (int w = 1; w < kWaves; ++w) {
             mh::argmax_merge(v, i, sv[w][b], si[w][b]);
         }
-        const unsigned long long old = __hip_atomic_fetch_max(
-            a.best + b, mh::argmax_key(v, i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // consume the returned value so the atomic has completed before the barrier
-        if (old == 0x0123456789abcdefull) {
-            sv[0][0] = 0.0f;
-        }
+        key = mh::argmax_key(v, i);
     }
     if (a.done == nullptr) {
+        if (threadIdx.x < B) {
+            amax(a.best + threadIdx.x, key);
+        }
         return;
+    }
+    const uint32_t groups = min(gridDim.x, kArgGroups);
+    const uint32_t g = blockIdx.x % groups;
+    const uint32_t members = (gridDim.x - g + groups - 1) / groups;
+    unsigned long long* gkeys = a.best;                      // [G][B]
+    unsigned long long* fkeys = a.best + kArgGroups * B;     // [B]
+    unsigned long long* gcnt = fkeys + B;                    // [G]
+    unsigned long long* top = gcnt + kArgGroups;             // [1]
+    if (threadIdx.x < B) {
+        sink = amax(gkeys + g * B + threadIdx.x, key);  // performed before the barrier
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        const uint32_t prev =
-            __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last = (prev == gridDim.x - 1) ? 1u : 0u;
+        flag = aadd(gcnt + g, 1ull) == members - 1 ? 1u : 0u;
     }
     __syncthreads();
-    if (last && threadIdx.x < B) {
-        const int b = threadIdx.x;
-        const unsigned long long key =
-            __hip_atomic_exchange(a.best + b, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        a.ids[b] = ~static_cast<uint32_t>(key & 0xffffffffull);
-        if (b == 0) {
-            __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+    if (!flag) {
+        return;
+    }
+    if (threadIdx.x < B) {
+        const unsigned long long k = axchg(gkeys + g * B + threadIdx.x, 0ull);
+        sink = amax(fkeys + threadIdx.x, k);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        axchg(gcnt + g, 0ull);
+        flag = aadd(top, 1ull) == groups - 1 ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!flag) {
+        return;
+    }
+    if (threadIdx.x < B) {
+        const unsigned long long k = axchg(fkeys + threadIdx.x, 0ull);
+        a.ids[threadIdx.x] = ~static_cast<uint32_t>(k & 0xffffffffull);
+    }
+    if (threadIdx.x == 0) {
+        axchg(top, 0ull);
     }
 }
 
@@ -123,42 +163,29 @@ __device__ __forceinline__ void emit_rows(const GemvArgs& a, uint32_t rg, const 
 // Batch 1, K <= 2048: each lane owns chunk `lane` of every row, with its x in
 // registers for the whole kernel.  Waves are persistent over row groups and
 // keep the next group's loads in flight during the current group's math.
+// Row addresses are wave-uniform (scalar base + the lane's fixed offset), so
+// the loads cost no vector ALU work.
 template <int BITS, int R>
 __global__ __launch_bounds__(kThreads) void k_gemv_b1(GemvArgs a) {
     const int lane = threadIdx.x & (mh::kWave - 1);
-    const int wave = threadIdx.x / mh::kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / mh::kWave);
     const uint32_t C = a.k / 32u;
     const uint32_t N = a.n;
     const bool live = lane < static_cast<int>(C);
+    const uint32_t c = live ? lane : 0u;
 
     float xr[32];
-    float xs = 0.0f;
-    {
-        const uint32_t c = live ? lane : 0u;
-        const uint16_t* xp = a.x + 32u * c;
-        uint32_t xw[16];
-        if ((reinterpret_cast<uintptr_t>(a.x) & 15u) == 0) {
-            const uint4* xv = reinterpret_cast<const uint4*>(xp);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint4 v = xv[q];
-                xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
-            }
-        } else {
-#pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                xw[q] = static_cast<uint32_t>(xp[2 * q]) | (static_cast<uint32_t>(xp[2 * q + 1]) << 16);
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const float lo = mh::bf16lo(xw[q]), hi = mh::bf16hi(xw[q]);
-            xs = xs + lo;
-            xs = xs + hi;
-            xr[2 * q] = mh::prep_x<BITS>(lo, 2 * q);
-            xr[2 * q + 1] = mh::prep_x<BITS>(hi, 2 * q + 1);
-        }
-    }
+    float xs;
+    mh::load_x_chunk<BITS>(a.x + 32u * c, xr, xs);
+
+    // lane-invariant byte offsets; row bases are scalar
+    const uint32_t code_off = c * BITS * 4u;
+    const uint32_t sb_off = ((32u * c) / a.gs) * 2u;
+    const size_t row_bytes = static_cast<size_t>(a.row_words) * 4u;
+    const size_t sb_row_bytes = static_cast<size_t>(a.groups) * 2u;
+    const char* codes = reinterpret_cast<const char*>(a.codes);
+    const char* scales = reinterpret_cast<const char*>(a.scales);
+    const char* biases = reinterpret_cast<const char*>(a.biases);
 
     float bv[1] = {-__builtin_inff()};
     uint32_t bi[1] = {0u};
@@ -172,13 +199,9 @@ __global__ __launch_bounds__(kThreads) void k_gemv_b1(GemvArgs a) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint32_t row = min(g * R + r, N - 1);
-            if (live) {
-                load_row_chunk<BITS>(a, row, lane, ch[r], s[r], b[r]);
-            } else {
-                ch[r].zero();
-                s[r] = 0.0f;
-                b[r] = 0.0f;
-            }
+            ch[r].load(mh::uniform_ptr(codes + row * row_bytes), code_off);
+            s[r] = mh::bf16_to_f32(mh::gload<uint16_t>(mh::uniform_ptr(scales + row * sb_row_bytes), sb_off));
+            b[r] = mh::bf16_to_f32(mh::gload<uint16_t>(mh::uniform_ptr(biases + row * sb_row_bytes), sb_off));
         }
     };
     if (rg < n_rg) {
@@ -226,12 +249,12 @@ __global__ __launch_bounds__(kThreads) void k_gemv_staged(GemvArgs a) {
 
     for (uint32_t t = threadIdx.x; t < B * C; t += kThreads) {
         const uint32_t b = t / C, c = t % C;
-        const uint16_t* xp = a.x + static_cast<size_t>(b) * a.k + 32u * c;
-        float s = 0.0f;
-        for (int i = 0; i < 32; ++i) {
-            const float v = mh::bf16_to_f32(xp[i]);
-            s = s + v;
-            xl[static_cast<size_t>(t) * kXPitch + i] = mh::prep_x<BITS>(v, i);
+        float xc[32], s;
+        mh::load_x_chunk<BITS>(a.x + static_cast<size_t>(b) * a.k + 32u * c, xc, s);
+        float4* dst = reinterpret_cast<float4*>(xl + static_cast<size_t>(t) * kXPitch);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            dst[q] = make_float4(xc[4 * q], xc[4 * q + 1], xc[4 * q + 2], xc[4 * q + 3]);
         }
         xsl[t] = s;
     }
@@ -349,7 +372,7 @@ int dispatch_gemv(const GemvArgs& a, uint32_t batch, hipStream_t stream) {
 constexpr size_t kMaxLds = 160u * 1024u;
 
 int gemv_common(const char* op, const mh_quant_weights* w, const uint16_t* x, uint16_t* y,
-                uint64_t* best, uint32_t* done, uint32_t* ids, uint32_t batch,
+                uint64_t* best, bool finisher, uint32_t* ids, uint32_t batch,
                 mh_stream_t stream) {
     MH_TRY(mh::check_quant(w, op));
     MH_ENSURE(x != nullptr, MH_ERR_INVALID, "%s: x is NULL", op);
@@ -358,10 +381,8 @@ int gemv_common(const char* op, const mh_quant_weights* w, const uint16_t* x, ui
               "%s: x/y not 2-byte aligned", op);
     MH_ENSURE(best == nullptr || mh::aligned(best, 8), MH_ERR_ALIGN,
               "%s: argmax key not 8-byte aligned", op);
-    MH_ENSURE((done == nullptr) == (ids == nullptr), MH_ERR_INVALID,
-              "%s: done and ids are given together", op);
-    MH_ENSURE(done == nullptr || best != nullptr, MH_ERR_INVALID,
-              "%s: the finisher needs the key scratch", op);
+    MH_ENSURE(!finisher || (best != nullptr && ids != nullptr), MH_ERR_INVALID,
+              "%s: the argmax finisher needs the scratch and ids", op);
     const uint32_t C = w->in_features / 32u;
     const bool xreg = batch == 1 && w->in_features <= 2048u;
     MH_ENSURE(xreg || static_cast<size_t>(batch) * C * (kXPitch + 1) * 4 <= kMaxLds,
@@ -374,7 +395,7 @@ int gemv_common(const char* op, const mh_quant_weights* w, const uint16_t* x, ui
     a.x = x;
     a.y = y;
     a.best = reinterpret_cast<unsigned long long*>(best);
-    a.done = done;
+    a.done = finisher ? static_cast<const void*>(best) : nullptr;
     a.ids = ids;
     a.n = w->out_features;
     a.k = w->in_features;
@@ -526,21 +547,21 @@ extern "C" {
 int mh_gemv_quant(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint32_t batch,
                   mh_stream_t stream) {
     MH_ENSURE(y != nullptr, MH_ERR_INVALID, "mh_gemv_quant: y is NULL");
-    return gemv_common("mh_gemv_quant", w, x, y, nullptr, nullptr, nullptr, batch, stream);
+    return gemv_common("mh_gemv_quant", w, x, y, nullptr, false, nullptr, batch, stream);
 }
 
 int mh_gemv_head_argmax(const mh_quant_weights* w, const uint16_t* x, uint64_t* best,
                         uint32_t batch, mh_stream_t stream) {
     MH_ENSURE(best != nullptr, MH_ERR_INVALID, "mh_gemv_head_argmax: best is NULL");
-    return gemv_common("mh_gemv_head_argmax", w, x, nullptr, best, nullptr, nullptr, batch,
+    return gemv_common("mh_gemv_head_argmax", w, x, nullptr, best, false, nullptr, batch,
                        stream);
 }
 
 int mh_gemv_quant_argmax(const mh_quant_weights* w, const uint16_t* x, uint16_t* y,
-                         uint64_t* best, uint32_t* done, uint32_t* ids, uint32_t batch,
-                         mh_stream_t stream) {
-    MH_ENSURE(best != nullptr, MH_ERR_INVALID, "mh_gemv_quant_argmax: best is NULL");
-    return gemv_common("mh_gemv_quant_argmax", w, x, y, best, done, ids, batch, stream);
+                         uint64_t* scratch, uint32_t* ids, uint32_t batch, mh_stream_t stream) {
+    MH_ENSURE(scratch != nullptr && ids != nullptr, MH_ERR_INVALID,
+              "mh_gemv_quant_argmax: scratch/ids is NULL");
+    return gemv_common("mh_gemv_quant_argmax", w, x, y, scratch, true, ids, batch, stream);
 }
 
 int mh_token_tail(uint64_t* best, uint32_t* out_tok, uint32_t batch, mh_stream_t stream) {

@@ -21,6 +21,28 @@ namespace mh {
 
 constexpr int kWave = 64;
 
+// Global-memory (address space 1) byte pointer.
+typedef const __attribute__((address_space(1))) char* gbytes;
+
+// A wave-uniform pointer pinned to scalar registers as a global pointer, so
+// that adding a 32-bit per-lane offset selects the scalar-base +
+// vector-offset global load form (no per-lane 64-bit address arithmetic).
+__device__ __forceinline__ gbytes uniform_ptr(const void* p) {
+    const uint64_t u = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+    return reinterpret_cast<gbytes>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Load from a scalar base plus a 32-bit per-lane byte offset.
+template <typename T>
+__device__ __forceinline__ T gload(gbytes base, uint32_t off) {
+    return *reinterpret_cast<const __attribute__((address_space(1))) T*>(base + off);
+}
+
 // ------------------------------------------------------------------ bf16 ---
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
@@ -199,6 +221,42 @@ __device__ __forceinline__ float q6_chunk_dot(const uint32_t (&w)[6], const floa
     return p;
 }
 
+// A lane's 32-element bf16 chunk of x as f32 (odd positions pre-scaled for
+// Q4) plus its ascending sum; 16-byte loads when the chunk is aligned.
+template <int BITS>
+__device__ __forceinline__ void load_x_chunk(const uint16_t* xp, float (&xr)[32], float& xs) {
+    uint32_t xw[16];
+    if ((reinterpret_cast<uintptr_t>(xp) & 15u) == 0) {
+        const uint4* xv = reinterpret_cast<const uint4*>(xp);
+        const uint4 v0 = xv[0], v1 = xv[1], v2 = xv[2], v3 = xv[3];
+        const uint4 v[4] = {v0, v1, v2, v3};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            xw[4 * q] = v[q].x; xw[4 * q + 1] = v[q].y; xw[4 * q + 2] = v[q].z; xw[4 * q + 3] = v[q].w;
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            xw[q] = static_cast<uint32_t>(xp[2 * q]) | (static_cast<uint32_t>(xp[2 * q + 1]) << 16);
+        }
+    }
+    xs = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const float lo = bf16lo(xw[q]), hi = bf16hi(xw[q]);
+        xs = xs + lo;
+        xs = xs + hi;
+        xr[2 * q] = lo;
+        xr[2 * q + 1] = hi;
+    }
+    if (BITS == 4) {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            xr[2 * q + 1] = xr[2 * q + 1] * 0.0625f;
+        }
+    }
+}
+
 // ---------------------------------------------------------- chunk loads ---
 template <int BITS>
 struct Chunk;
@@ -208,6 +266,10 @@ struct Chunk<4> {
     uint32_t w[4];
     __device__ __forceinline__ void load(const uint32_t* p) {  // 16-byte aligned
         const uint4 v = *reinterpret_cast<const uint4*>(p);
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    }
+    __device__ __forceinline__ void load(gbytes base, uint32_t off) {  // 16-byte aligned
+        const u32x4 v = gload<u32x4>(base, off);
         w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
     }
     __device__ __forceinline__ void zero() { w[0] = w[1] = w[2] = w[3] = 0u; }
@@ -220,6 +282,11 @@ struct Chunk<6> {
     __device__ __forceinline__ void load(const uint32_t* p) {  // 8-byte aligned
         const uint2* q = reinterpret_cast<const uint2*>(p);
         const uint2 a = q[0], b = q[1], c = q[2];
+        w[0] = a.x; w[1] = a.y; w[2] = b.x; w[3] = b.y; w[4] = c.x; w[5] = c.y;
+    }
+    __device__ __forceinline__ void load(gbytes base, uint32_t off) {  // 8-byte aligned
+        const u32x2 a = gload<u32x2>(base, off), b = gload<u32x2>(base, off + 8),
+                    c = gload<u32x2>(base, off + 16);
         w[0] = a.x; w[1] = a.y; w[2] = b.x; w[3] = b.y; w[4] = c.x; w[5] = c.y;
     }
     __device__ __forceinline__ void zero() { w[0] = w[1] = w[2] = w[3] = w[4] = w[5] = 0u; }

@@ -6,7 +6,7 @@
 // mode 1 (softmax): rank on z; weights bf16(e_r / (e_0 + ... + e_{k-1})),
 //        e_r = exp(z_r - z_top1) (softmax over all experts restricted to the
 //        chosen ones and renormalised).
-// Selection is the serial scan of lfm_moe_route_batch: for each slot, the
+// Selection equals the serial scan of lfm_moe_route_batch: for each slot, the
 // greatest unused candidate, an exact tie to the lower expert id, starting
 // from (-inf, id 0).  exp is mh::expf_fixed, so CPU and GPU agree bit for bit.
 #pragma once
@@ -29,29 +29,51 @@ __device__ __forceinline__ void route_score(float z, float bias, int mode, float
     }
 }
 
-// Serial selection over LDS-resident scores (one thread).  used[] is scratch.
-__device__ inline void route_select(const float* s, const float* cand, unsigned char* used,
-                                    uint32_t e, uint32_t topk, int mode, float eps,
-                                    uint32_t* ids_out, uint16_t* w_out) {
+// Selection over LDS-resident scores by one full wave.  For each slot every
+// lane takes the best eligible candidate among its experts (lane, lane + 64,
+// ...), then the wave reduces with the same rule.  "value desc, id asc" is a
+// strict total order on eligible candidates (ids are distinct), so the winner
+// does not depend on the reduction order and equals the serial scan's: that
+// scan starts from (-inf, id 0) and only replaces on v > best or (v == best and
+// a lower id), so used experts, NaN and -inf never win, and with no eligible
+// candidate it returns expert 0.  Lane 0 writes ids and weights.
+__device__ inline void route_select(const float* s, const float* cand, uint32_t e, uint32_t topk,
+                                    int mode, float eps, uint32_t* ids_out, uint16_t* w_out) {
+    const uint32_t lane = threadIdx.x & 63u;
+    constexpr int kPerLane = kMaxExperts / 64;
+    uint32_t used = 0;  // bit j: expert lane + 64 j already chosen
     uint32_t chosen[kMaxTopk];
-    for (uint32_t i = 0; i < e; ++i) {
-        used[i] = 0;
-    }
     for (uint32_t r = 0; r < topk; ++r) {
-        float best = -__builtin_inff();
-        uint32_t best_e = 0;
-        for (uint32_t i = 0; i < e; ++i) {
-            if (used[i]) {
-                continue;
-            }
-            const float v = cand[i];
-            if (v > best || (v == best && i < best_e)) {
-                best = v;
-                best_e = i;
+        float bv = -__builtin_inff();
+        uint32_t bi = 0xffffffffu;
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+            const uint32_t i = lane + 64u * j;
+            if (i < e && !((used >> j) & 1u)) {
+                const float v = cand[i];
+                if (v > -__builtin_inff() && (v > bv || (v == bv && i < bi))) {
+                    bv = v;
+                    bi = i;
+                }
             }
         }
-        chosen[r] = best_e;
-        used[best_e] = 1;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const uint32_t oi = __shfl_xor(bi, off);
+            if (oi != 0xffffffffu && (bi == 0xffffffffu || ov > bv || (ov == bv && oi < bi))) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        const uint32_t pick = bi == 0xffffffffu ? 0u : bi;
+        chosen[r] = pick;
+        if ((pick & 63u) == lane) {
+            used |= 1u << (pick >> 6);
+        }
+    }
+    if (lane != 0) {
+        return;
     }
     if (mode == 0) {
         float denom = eps;

@@ -66,21 +66,21 @@ struct DenseArgs {
     float eps;
 };
 
-// Stage x rows [t0, t0 + nt) into LDS as padded f32 chunks.
+// Stage x rows [t0, t0 + nt) into LDS as padded f32 chunks, one 32-element
+// chunk per thread per step with 16-byte loads (k % 32 == 0 keeps each
+// chunk 64-byte aligned when x is 16-byte aligned).
 __device__ inline void stage_x(const uint16_t* x, uint32_t t0, uint32_t nt, uint32_t k,
                                float* xl, int tt) {
     const uint32_t C = k / 32u;
-    for (uint32_t i = threadIdx.x; i < static_cast<uint32_t>(tt) * C * 16u; i += kThreads) {
-        const uint32_t t = i / (C * 16u), rem = i % (C * 16u);
-        const uint32_t c = rem / 16u, q = rem % 16u;
-        uint32_t u = 0;
-        if (t < nt) {
-            const uint16_t* xp = x + static_cast<size_t>(t0 + t) * k + 32u * c + 2u * q;
-            u = static_cast<uint32_t>(xp[0]) | (static_cast<uint32_t>(xp[1]) << 16);
+    for (uint32_t i = threadIdx.x; i < static_cast<uint32_t>(tt) * C; i += kThreads) {
+        const uint32_t t = i / C, c = i % C;
+        float xc[32], s;
+        mh::load_x_chunk<0>(x + static_cast<size_t>(t0 + (t < nt ? t : 0)) * k + 32u * c, xc, s);
+        float4* d = reinterpret_cast<float4*>(xl + (static_cast<size_t>(t) * C + c) * kXPitch);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            d[q] = make_float4(xc[4 * q], xc[4 * q + 1], xc[4 * q + 2], xc[4 * q + 3]);
         }
-        float* d = xl + (static_cast<size_t>(t) * C + c) * kXPitch + 2u * q;
-        d[0] = mh::bf16lo(u);
-        d[1] = mh::bf16hi(u);
     }
 }
 
@@ -160,7 +160,6 @@ __global__ __launch_bounds__(kThreads) void k_dense_gemv(DenseArgs a) {
         return;
     }
     __shared__ float s[mh::kMaxExperts], cand[mh::kMaxExperts];
-    __shared__ unsigned char used[mh::kMaxExperts];
     for (uint32_t i = threadIdx.x; i < a.n; i += kThreads) {
         const float z = __uint_as_float(__hip_atomic_fetch_or(reinterpret_cast<uint32_t*>(a.y) + i,
                                                               0u, __ATOMIC_RELAXED,
@@ -168,8 +167,10 @@ __global__ __launch_bounds__(kThreads) void k_dense_gemv(DenseArgs a) {
         mh::route_score(z, a.bias ? a.bias[i] : 0.0f, a.mode, s[i], cand[i]);
     }
     __syncthreads();
+    if (threadIdx.x < 64) {
+        mh::route_select(s, cand, a.n, a.topk, a.mode, a.eps, a.ids, a.weights);
+    }
     if (threadIdx.x == 0) {
-        mh::route_select(s, cand, used, a.n, a.topk, a.mode, a.eps, a.ids, a.weights);
         __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
@@ -226,17 +227,14 @@ __global__ __launch_bounds__(64) void k_route(const float* logits, const float* 
                                               uint32_t* ids, uint16_t* w, uint32_t e,
                                               uint32_t topk, int mode, float eps) {
     __shared__ float s[mh::kMaxExperts], cand[mh::kMaxExperts];
-    __shared__ unsigned char used[mh::kMaxExperts];
     const uint32_t t = blockIdx.x;
     for (uint32_t i = threadIdx.x; i < e; i += 64) {
         mh::route_score(logits[static_cast<size_t>(t) * e + i], bias ? bias[i] : 0.0f, mode, s[i],
                         cand[i]);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        mh::route_select(s, cand, used, e, topk, mode, eps, ids + static_cast<size_t>(t) * topk,
-                         w + static_cast<size_t>(t) * topk);
-    }
+    mh::route_select(s, cand, e, topk, mode, eps, ids + static_cast<size_t>(t) * topk,
+                     w + static_cast<size_t>(t) * topk);
 }
 
 int route_checks(const char* op, const float* logits, uint32_t* ids, uint16_t* w, uint32_t m,
@@ -298,19 +296,8 @@ __global__ __launch_bounds__(kThreads) void k_gather_act(ActArgs a) {
     const uint32_t C = a.k / 32u;
     const bool live = lane < static_cast<int>(C);
     float xr[32];
-    float xs = 0.0f;
-    {
-        const uint16_t* xp = a.x + 32u * (live ? lane : 0);
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const uint32_t u = static_cast<uint32_t>(xp[2 * q]) | (static_cast<uint32_t>(xp[2 * q + 1]) << 16);
-            const float lo = mh::bf16lo(u), hi = mh::bf16hi(u);
-            xs = xs + lo;
-            xs = xs + hi;
-            xr[2 * q] = mh::prep_x<4>(lo, 2 * q);
-            xr[2 * q + 1] = mh::prep_x<4>(hi, 2 * q + 1);
-        }
-    }
+    float xs;
+    mh::load_x_chunk<4>(a.x + 32u * (live ? lane : 0), xr, xs);
     const uint32_t rows = a.slots * a.n_inter;
     const uint32_t n_rg = (rows + R - 1) / R;
     const uint32_t stride = gridDim.x * kWaves;
@@ -417,18 +404,7 @@ __global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
     float wt[TK];
 #pragma unroll
     for (int r = 0; r < TK; ++r) {
-        const uint16_t* xp = a.act + static_cast<size_t>(r) * a.k + 32u * (live ? lane : 0);
-        float s = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const uint32_t u = static_cast<uint32_t>(xp[2 * q]) | (static_cast<uint32_t>(xp[2 * q + 1]) << 16);
-            const float lo = mh::bf16lo(u), hi = mh::bf16hi(u);
-            s = s + lo;
-            s = s + hi;
-            xr[r][2 * q] = mh::prep_x<4>(lo, 2 * q);
-            xr[r][2 * q + 1] = mh::prep_x<4>(hi, 2 * q + 1);
-        }
-        xs[r] = s;
+        mh::load_x_chunk<4>(a.act + static_cast<size_t>(r) * a.k + 32u * (live ? lane : 0), xr[r], xs[r]);
         const uint32_t id = a.ids[r];
         e[r] = id < a.n_experts ? id : 0u;
         wt[r] = mh::bf16_to_f32(a.weights[r]);

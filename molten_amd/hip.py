@@ -80,7 +80,7 @@ _SIGNATURES = {
     "mh_dequant_q4_bf16_bulk": [_qw, _vp, _vp],
     "mh_gemv_quant": [_qw, _vp, _vp, _u32, _vp],
     "mh_gemv_head_argmax": [_qw, _vp, _vp, _u32, _vp],
-    "mh_gemv_quant_argmax": [_qw, _vp, _vp, _vp, _vp, _vp, _u32, _vp],
+    "mh_gemv_quant_argmax": [_qw, _vp, _vp, _vp, _vp, _u32, _vp],
     "mh_token_tail": [_vp, _vp, _u32, _vp],
     "mh_argmax_bf16": [_vp, _u32, _vp, _vp, _vp],
     "mh_gemv_f32": [_vp, _vp, _vp, _u32, _u32, _vp],
@@ -226,11 +226,19 @@ def gemv_head_argmax(w: QuantWeights, x, best, batch: int = 1, stream=None) -> N
           "gemv_head_argmax")
 
 
-def gemv_quant_argmax(w: QuantWeights, x, y, best, done=None, ids=None, batch: int = 1,
-                      stream=None) -> None:
-    """Stored logits + argmax (BASELINE configs 2 and 5)."""
-    check(load().mh_gemv_quant_argmax(_qref(w), _ptr(x), _ptr(y), _ptr(best), _ptr(done),
-                                      _ptr(ids), batch, _stream(stream)), "gemv_quant_argmax")
+ARGMAX_GROUPS = 32
+
+
+def argmax_scratch_words(batch: int) -> int:
+    """MH_ARGMAX_SCRATCH_WORDS(batch): u64 words of gemv_quant_argmax scratch."""
+    return (ARGMAX_GROUPS + 1) * batch + ARGMAX_GROUPS + 1
+
+
+def gemv_quant_argmax(w: QuantWeights, x, y, scratch, ids, batch: int = 1, stream=None) -> None:
+    """Stored logits (y may be None) + argmax ids in one launch (BASELINE
+    configs 2 and 5).  scratch: zeroed u64 [argmax_scratch_words(batch)]."""
+    check(load().mh_gemv_quant_argmax(_qref(w), _ptr(x), _ptr(y), _ptr(scratch), _ptr(ids), batch,
+                                      _stream(stream)), "gemv_quant_argmax")
 
 
 def token_tail(best, out_tok, batch: int = 1, stream=None) -> None:

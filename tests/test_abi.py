@@ -64,10 +64,10 @@ def test_argmax_arguments():
     with pytest.raises(hip.MoltenError):
         hip.gemv_head_argmax(_qw(), 0x4000, None, stream=0)
     with pytest.raises(hip.MoltenError) as ei:
-        hip.gemv_quant_argmax(_qw(), 0x4000, 0x5000, 0x6004, stream=0)
+        hip.gemv_quant_argmax(_qw(), 0x4000, 0x5000, 0x6004, 0x7000, stream=0)
     assert ei.value.code == hip.MH_ERR_ALIGN
-    with pytest.raises(hip.MoltenError):  # done without ids
-        hip.gemv_quant_argmax(_qw(), 0x4000, 0x5000, 0x6000, done=0x7000, stream=0)
+    with pytest.raises(hip.MoltenError):  # scratch without ids
+        hip.gemv_quant_argmax(_qw(), 0x4000, 0x5000, 0x6000, None, stream=0)
     with pytest.raises(hip.MoltenError):
         hip.token_tail(0x6000, 0x7000, batch=0, stream=0)
     with pytest.raises(hip.MoltenError):

@@ -65,16 +65,15 @@ def test_argmax_paths_agree_with_oracle(dev, orc, bits, batch):
     xd = to_dev(x)
     # (1) stored logits + finisher ids, run twice to check the scratch is re-zeroed
     y = empty_dev((batch, n), np.uint16)
-    best = zeros_dev((batch,), np.uint64)
-    done = zeros_dev((1,), np.uint32)
+    scratch = zeros_dev((hip.argmax_scratch_words(batch),), np.uint64)
     ids = empty_dev((batch,), np.uint32)
-    for _ in range(2):
-        hip.gemv_quant_argmax(w, xd, y, best, done, ids, batch)
+    for _ in range(3):
+        hip.gemv_quant_argmax(w, xd, y, scratch, ids, batch)
         assert from_dev(ids, np.uint32).tolist() == want
-        assert from_dev(best, np.uint64).tolist() == [0] * batch
-        assert from_dev(done, np.uint32).tolist() == [0]
+        assert not from_dev(scratch, np.uint64).any()
     np.testing.assert_array_equal(from_dev(y, np.uint16), logits)
     # (2) reference pair: head argmax (no logits) + token tail
+    best = zeros_dev((batch,), np.uint64)
     tok = empty_dev((batch,), np.uint32)
     hip.gemv_head_argmax(w, xd, best, batch)
     hip.token_tail(best, tok, batch)
@@ -95,10 +94,9 @@ def test_argmax_ties_take_lowest_index(dev, orc):
     logits = orc.gemv_quant(hb, x, 1)[0]
     want = orc.argmax_bf16(logits)
     w, keep = dev_quant(hb)
-    best = zeros_dev((1,), np.uint64)
-    done = zeros_dev((1,), np.uint32)
+    scratch = zeros_dev((hip.argmax_scratch_words(1),), np.uint64)
     ids = empty_dev((1,), np.uint32)
-    hip.gemv_quant_argmax(w, to_dev(x), None, best, done, ids, 1)
+    hip.gemv_quant_argmax(w, to_dev(x), None, scratch, ids, 1)
     assert from_dev(ids, np.uint32)[0] == want
 
 
@@ -139,10 +137,9 @@ def test_lm_head_full_size(dev, orc, bits, batch):
     x = layout.synth_bf16(rng, (batch, k))
     w, keep = dev_quant(h)
     y = empty_dev((batch, n), np.uint16)
-    best = zeros_dev((batch,), np.uint64)
-    done = zeros_dev((1,), np.uint32)
+    scratch = zeros_dev((hip.argmax_scratch_words(batch),), np.uint64)
     ids = empty_dev((batch,), np.uint32)
-    hip.gemv_quant_argmax(w, to_dev(x), y, best, done, ids, batch)
+    hip.gemv_quant_argmax(w, to_dev(x), y, scratch, ids, batch)
     got = from_dev(y, np.uint16)
     got_ids = from_dev(ids, np.uint32)
     want = orc.gemv_quant(h, x, batch)

@@ -166,3 +166,36 @@ def test_prefill_router_and_route_batch(dev, orc):
     want_ids, want_w = orc.route(want, None, TOPK, 1)
     np.testing.assert_array_equal(from_dev(ids, np.uint32), want_ids)
     np.testing.assert_array_equal(from_dev(gw, np.uint16), want_w)
+
+
+@pytest.mark.parametrize("e", [64, 100, 256])
+def test_route_special_values_match_serial_scan(dev, orc, e):
+    """NaN and -inf candidates never win, exact ties go to the lower id, and a
+    token with fewer eligible experts than slots falls back to expert 0, as
+    the serial scan of the reference does."""
+    rng = np.random.default_rng(e)
+    topk = 4
+    cases = []
+    z = rng.normal(0, 1, e).astype(np.float32)
+    z[[3, 9]] = np.nan
+    z[[5, 6]] = -np.inf
+    cases.append(z)
+    z = np.full(e, -np.inf, np.float32)
+    z[e - 1] = 2.0
+    z[7] = 2.0
+    cases.append(z)                       # two eligible, both tied
+    cases.append(np.full(e, np.nan, np.float32))  # none eligible
+    z = np.zeros(e, np.float32)
+    z[e // 2] = np.inf
+    cases.append(z)
+    m = len(cases)
+    logits = np.stack(cases)
+    for mode in (0, 1):
+        bias = rng.normal(0, 0.1, e).astype(np.float32) if mode == 0 else None
+        ids = empty_dev((m, topk), np.uint32)
+        w = empty_dev((m, topk), np.uint16)
+        hip.moe_route_batch(to_dev(logits), None if bias is None else to_dev(bias), ids, w, m, e,
+                            topk, mode=mode)
+        want_ids, want_w = orc.route(logits, bias, topk, mode)
+        np.testing.assert_array_equal(from_dev(ids, np.uint32), want_ids)
+        np.testing.assert_array_equal(from_dev(w, np.uint16), want_w)
