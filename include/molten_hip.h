@@ -120,15 +120,16 @@ int mh_gemv_head_argmax(const mh_quant_weights* w, const uint16_t* x, uint64_t* 
                         uint32_t batch, mh_stream_t stream);
 
 /* Head GEMV that stores the bf16 logits (y, may be NULL) and writes
- * ids[b] = argmax token of row b in the same launch: the last workgroup to
- * finish converts the keys (no tail kernel).  scratch: u64 words, at least
- * MH_ARGMAX_SCRATCH_WORDS(batch), zero on entry and left zero; calls that
- * overlap on one scratch buffer race.  The keys are folded through a
- * two-level tree of MH_ARGMAX_GROUPS groups so few workgroups contend on any
- * one atomic.  No reference counterpart (BASELINE configs 2 and 5 store the
+ * ids[b] = argmax token of row b in the same launch.  Every workgroup but
+ * the last publishes its key for each batch row into its own scratch slot;
+ * the last-dispatched workgroup (every other one has started by then) collects
+ * the slots, writes the token ids and re-zeroes the slots, so no two
+ * workgroups contend on one atomic.  scratch: MH_ARGMAX_SCRATCH_WORDS(batch)
+ * u64 words, zero on entry and left zero; calls that overlap on one scratch
+ * buffer race.  No reference counterpart (BASELINE configs 2 and 5 store the
  * logits; molten's head stores none). */
-#define MH_ARGMAX_GROUPS 32u
-#define MH_ARGMAX_SCRATCH_WORDS(batch) ((MH_ARGMAX_GROUPS + 1u) * (batch) + MH_ARGMAX_GROUPS + 1u)
+#define MH_ARGMAX_SLOTS 2048u
+#define MH_ARGMAX_SCRATCH_WORDS(batch) (MH_ARGMAX_SLOTS * (batch))
 int mh_gemv_quant_argmax(const mh_quant_weights* w, const uint16_t* x, uint16_t* y,
                          uint64_t* scratch, uint32_t* ids, uint32_t batch, mh_stream_t stream);
 

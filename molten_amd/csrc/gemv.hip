@@ -18,58 +18,112 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / mh::kWave;
 constexpr int kXPitch = 36;  // LDS floats per staged x chunk (32 + 4: no bank conflicts)
+constexpr uint32_t kArgSlots = MH_ARGMAX_SLOTS;
+constexpr uint32_t kSpinLimit = 1u << 24;  // bound of the collector's wait for one slot
 
 struct GemvArgs {
     const uint32_t* codes;
     const uint16_t* scales;
     const uint16_t* biases;
-    const uint16_t* x;        // bf16 [batch, k]
-    uint16_t* y;              // bf16 [batch, n] or null
-    unsigned long long* best; // [batch] keys, or the finisher scratch
-    const void* done;         // non-null: finisher mode (best is the scratch)
-    uint32_t* ids;            // [batch] tokens written by the finisher
+    const uint16_t* x;          // bf16 [batch, k]
+    uint16_t* y;                // bf16 [batch, n] or null
+    unsigned long long* best;   // [batch] keys (reference head argmax), or null
+    unsigned long long* slots;  // [batch][kArgSlots] finisher scratch, or null
+    uint32_t* ids;              // [batch] tokens written by the finisher
     uint32_t n, k, gs, row_words, groups;
 };
-
-template <int BITS>
-__device__ __forceinline__ void load_row_chunk(const GemvArgs& a, uint32_t row, uint32_t c,
-                                               mh::Chunk<BITS>& ch, float& s, float& b) {
-    ch.load(a.codes + static_cast<size_t>(row) * a.row_words + static_cast<size_t>(c) * BITS);
-    const uint32_t g = (32u * c) / a.gs;
-    s = mh::bf16_to_f32(a.scales[static_cast<size_t>(row) * a.groups + g]);
-    b = mh::bf16_to_f32(a.biases[static_cast<size_t>(row) * a.groups + g]);
-}
-
-// Per-wave argmax state folded into the workgroup, then into the keys.
-// bv/bi are wave-uniform.  Cross-workgroup traffic is atomic only: an
-// atomic's returned value is consumed before the workgroup signals, so it has
-// been performed at the coherence point and no cache write-back is needed.
-//
-// Without a finisher (a.done == null: the reference's gemv_head_argmax) every
-// workgroup folds its key into best[b].  With the finisher, contention is a
-// two-level tree: workgroup w folds into group key (w % G), the last
-// workgroup of each group folds that into the final key, and the last group
-// writes the token ids and re-zeroes the scratch (layout in molten_hip.h:
-// group keys [G][B] | final keys [B] | group counters [G] | top counter).
-constexpr uint32_t kArgGroups = MH_ARGMAX_GROUPS;
 
 __device__ __forceinline__ unsigned long long amax(unsigned long long* p, unsigned long long v) {
     return __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ unsigned long long axchg(unsigned long long* p, unsigned long long v) {
-    return __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned long long aadd(unsigned long long* p, unsigned long long v) {
-    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+// Argmax epilogue with the finisher.  Keys are published by "units" (waves
+// of the batch-1 kernel, workgroups of the staged kernel) into their own
+// slots, so no two units contend on one address.  The last workgroup of the
+// grid is dispatched after all others have started, so its wait for their
+// slots ends; it reduces the slots with its own units' keys, writes the token
+// ids and re-zeroes the slots.  Keys are never zero (the orderable value of
+// any non-NaN float, -inf included, is nonzero), so zero marks an empty slot.
+__device__ __forceinline__ void publish_key(const GemvArgs& a, uint32_t b, uint32_t unit,
+                                            unsigned long long key) {
+    __hip_atomic_store(a.slots + static_cast<size_t>(b) * kArgSlots + unit, key, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Run by the whole collector workgroup.  own[b]: the collector's own key.
+// Each thread reads its slots together; the ones still empty (their unit has
+// not published yet) are read again together until they fill.
 template <int B>
-__device__ void fold_argmax(const GemvArgs& a, const float (&bv)[B], const uint32_t (&bi)[B],
-                            int lane, int wave) {
+__device__ void collect_keys(const GemvArgs& a, uint32_t n_units, const unsigned long long* own) {
+    __shared__ unsigned long long sk[kWaves];
+    constexpr int kPer = kArgSlots / kThreads;  // slots per collector thread
+    static_assert(kPer <= 32, "pending mask is 32 bits");
+    const int lane = threadIdx.x & (mh::kWave - 1), wave = threadIdx.x / mh::kWave;
+    for (int b = 0; b < B; ++b) {
+        unsigned long long* sl = a.slots + static_cast<size_t>(b) * kArgSlots + threadIdx.x;
+        unsigned long long v[kPer];
+        uint32_t pend = 0;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const bool mine = threadIdx.x + j * kThreads < n_units;
+            v[j] = mine ? __hip_atomic_load(sl + j * kThreads, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1ull;
+            pend |= (v[j] == 0ull ? 1u : 0u) << j;
+        }
+        uint32_t spins = 0;
+        while (pend != 0u && ++spins < kSpinLimit) {
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int j = 0; j < kPer; ++j) {
+                if ((pend >> j) & 1u) {
+                    v[j] = __hip_atomic_load(sl + j * kThreads, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < kPer; ++j) {
+                if (v[j] != 0ull) {
+                    pend &= ~(1u << j);
+                }
+            }
+        }
+        const bool lost = pend != 0u;
+        unsigned long long m = 0;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            if (threadIdx.x + j * kThreads < n_units) {
+                m = v[j] > m ? v[j] : m;
+                __hip_atomic_store(sl + j * kThreads, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const unsigned long long o = __shfl_xor(m, off);
+            m = o > m ? o : m;
+        }
+        const bool any_lost = __syncthreads_or(lost) != 0;
+        if (lane == 0) {
+            sk[wave] = m;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned long long t = own[b];
+            for (int w = 0; w < kWaves; ++w) {
+                t = sk[w] > t ? sk[w] : t;
+            }
+            a.ids[b] = any_lost ? 0xffffffffu : ~static_cast<uint32_t>(t & 0xffffffffull);
+        }
+        __syncthreads();
+    }
+}
+
+// Workgroup argmax of the staged kernel: waves' (bv, bi) per batch row merged
+// in LDS; then one atomic max per workgroup into best[b] (the reference's
+// gemv_head_argmax) or the finisher's slots.
+template <int B>
+__device__ void finish_argmax(const GemvArgs& a, const float (&bv)[B], const uint32_t (&bi)[B],
+                              int lane, int wave) {
     __shared__ float sv[kWaves][B];
     __shared__ uint32_t si[kWaves][B];
-    __shared__ uint32_t flag;
-    __shared__ unsigned long long sink;
+    __shared__ unsigned long long own[B];
     if (lane == 0) {
 #pragma unroll
         for (int b = 0; b < B; ++b) {
@@ -88,53 +142,239 @@ __device__ void fold_argmax(const GemvArgs& a, const float (&bv)[B], const uint3
         }
         key = mh::argmax_key(v, i);
     }
-    if (a.done == nullptr) {
+    if (a.slots == nullptr) {
         if (threadIdx.x < B) {
             amax(a.best + threadIdx.x, key);
         }
         return;
     }
-    const uint32_t groups = min(gridDim.x, kArgGroups);
-    const uint32_t g = blockIdx.x % groups;
-    const uint32_t members = (gridDim.x - g + groups - 1) / groups;
-    unsigned long long* gkeys = a.best;                      // [G][B]
-    unsigned long long* fkeys = a.best + kArgGroups * B;     // [B]
-    unsigned long long* gcnt = fkeys + B;                    // [G]
-    unsigned long long* top = gcnt + kArgGroups;             // [1]
-    if (threadIdx.x < B) {
-        sink = amax(gkeys + g * B + threadIdx.x, key);  // performed before the barrier
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        flag = aadd(gcnt + g, 1ull) == members - 1 ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!flag) {
+    const uint32_t last = gridDim.x - 1;
+    if (blockIdx.x != last) {
+        if (threadIdx.x < B) {
+            publish_key(a, threadIdx.x, blockIdx.x, key);
+        }
         return;
     }
     if (threadIdx.x < B) {
-        const unsigned long long k = axchg(gkeys + g * B + threadIdx.x, 0ull);
-        sink = amax(fkeys + threadIdx.x, k);
+        own[threadIdx.x] = key;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        axchg(gcnt + g, 0ull);
-        flag = aadd(top, 1ull) == groups - 1 ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!flag) {
-        return;
-    }
-    if (threadIdx.x < B) {
-        const unsigned long long k = axchg(fkeys + threadIdx.x, 0ull);
-        a.ids[threadIdx.x] = ~static_cast<uint32_t>(k & 0xffffffffull);
-    }
-    if (threadIdx.x == 0) {
-        axchg(top, 0ull);
-    }
+    collect_keys<B>(a, last, own);
 }
 
-// Row values (wave-uniform) of one row group: store and argmax.
+// Wave max / min with the DPP tree of wave_sum_lane63 (valid in lane 63).
+__device__ __forceinline__ float wave_max_f32(float v) {
+    v = fmaxf(v, mh::dpp_move<0x111, 0xf>(v));
+    v = fmaxf(v, mh::dpp_move<0x112, 0xf>(v));
+    v = fmaxf(v, mh::dpp_move<0x114, 0xf>(v));
+    v = fmaxf(v, mh::dpp_move<0x118, 0xf>(v));
+    v = fmaxf(v, mh::dpp_move<0x142, 0xa>(v));
+    v = fmaxf(v, mh::dpp_move<0x143, 0xc>(v));
+    return mh::lane63(v);
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(-1, static_cast<int>(v), CTRL, ROW_MASK, 0xf, false));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    v = min(v, dpp_u32<0x111, 0xf>(v));
+    v = min(v, dpp_u32<0x112, 0xf>(v));
+    v = min(v, dpp_u32<0x114, 0xf>(v));
+    v = min(v, dpp_u32<0x118, 0xf>(v));
+    v = min(v, dpp_u32<0x142, 0xa>(v));
+    v = min(v, dpp_u32<0x143, 0xc>(v));
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
+// Key of the wave's argmax over per-lane bests (bv, bi) kept by argmax_merge:
+// the greatest value (NaN never wins, -0 == +0), ties to the lowest index;
+// with no non-NaN candidate the serial scan's (-inf, 0).
+__device__ __forceinline__ unsigned long long wave_argmax_key(float bv, uint32_t bi) {
+    const float m = wave_max_f32(bv);
+    if (m != m) {
+        return mh::argmax_key(-__builtin_inff(), 0u);
+    }
+    const uint32_t i = wave_min_u32(bv == m ? bi : 0xffffffffu);
+    return mh::argmax_key(m, i);
+}
+
+// Rows of the batch-1 kernel: each wave owns blocks of kBlockRows consecutive
+// rows; x is held in registers (lane c owns chunk c, K <= 2048).
+constexpr int kBlockRows = 8;
+constexpr int kGroupRows = 4;
+constexpr int kMaxGroups = 64;  // K / group size <= 2048 / 32
+
+// Four row values h[0..3] per lane reduced with the chunk order's xor
+// butterfly, four rows in one register: levels 1 and 2 (xor 1, xor 2) pair
+// lanes holding the same row, after which lane l carries row (l & 3); levels
+// 3..6 use row_shr:4 (correct where bit 2 of the lane is set), row_ror:8
+// (xor 8) and the permlane16/32 swaps (xor 16, xor 32).  Every addition is
+// a_l + a_{l^m} of the single-row butterfly (addition is commutative), so
+// lane 60 + j ends with row j's butterfly value.
+template <int CTRL>
+__device__ __forceinline__ float qmove(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float reduce_rows4(const float (&h)[4], int lane) {
+    const bool b0 = lane & 1, b1 = (lane >> 1) & 1;
+    const float s01 = (b0 ? h[1] : h[0]) + qmove<0xB1>(b0 ? h[0] : h[1]);  // quad_perm 1,0,3,2
+    const float s23 = (b0 ? h[3] : h[2]) + qmove<0xB1>(b0 ? h[2] : h[3]);
+    float v = (b1 ? s23 : s01) + qmove<0x4E>(b1 ? s01 : s23);              // quad_perm 2,3,0,1
+    v = v + mh::dpp_move<0x114, 0xf>(v);  // row_shr:4
+    v = v + mh::dpp_move<0x128, 0xf>(v);  // row_ror:8
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    return v;
+}
+
+// Batch 1, K <= 2048, even K / group size.  Each wave owns blocks of
+// kBlockRows consecutive rows (one block per wave up to kArgSlots
+// workgroups).  A block's scales and biases are read with a few wide loads
+// and staged in LDS as (scale | bias << 16) words; the codes of the block's
+// two row groups are loaded non-temporally (each byte is read once), group
+// 1 while group 0 is computed; each group's four row values are reduced
+// together, and the block's outputs are stored by lanes 0..7 at once.
+// FAST: K == 2048, group size 64 and N a multiple of kBlockRows (every lane
+// owns a chunk, 32 groups per row, no partial block).  ARGMAX: per-lane
+// bests, a DPP wave argmax, then the finisher (or the reference's atomic
+// max).
+template <int BITS, bool FAST, bool ARGMAX>
+__global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
+    constexpr int BR = kBlockRows, R = kGroupRows;
+    __shared__ uint32_t sbl[kWaves][BR * kMaxGroups];
+    const int lane = threadIdx.x & (mh::kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / mh::kWave);
+    const uint32_t C = a.k / 32u;
+    const uint32_t N = a.n;
+    const uint32_t G = FAST ? 32u : a.groups;
+    const bool live = FAST || lane < static_cast<int>(C);
+    const uint32_t c = live ? lane : 0u;
+
+    // x is converted after the first block's loads are issued
+    uint32_t xw[16];
+    mh::load_x_words(a.x + 32u * c, xw);
+    float xr[32];
+    float xs = 0.0f;
+    bool x_ready = false;
+    const uint32_t code_off = c * BITS * 4u;
+    const uint32_t gc = FAST ? static_cast<uint32_t>(lane) / 2u : (32u * c) / a.gs;
+    const uint32_t row_bytes = FAST ? 2048u * BITS / 8u : a.row_words * 4u;
+    uint32_t* sb = sbl[wave];
+
+    float lbv = -__builtin_inff();  // per-lane best of the rows this lane stored
+    uint32_t lbi = 0u;
+    const uint32_t n_blocks = (N + BR - 1) / BR;
+    for (uint32_t blk = blockIdx.x * kWaves + wave; blk < n_blocks; blk += gridDim.x * kWaves) {
+        const uint32_t row0 = blk * BR;
+        const uint32_t nrows = FAST ? static_cast<uint32_t>(BR) : min(static_cast<uint32_t>(BR), N - row0);
+        // scale/bias words of the block's rows (contiguous, dword aligned)
+        const uint32_t nd = nrows * G / 2u;
+        const uint32_t* s2 = reinterpret_cast<const uint32_t*>(a.scales + static_cast<size_t>(row0) * G);
+        const uint32_t* b2 = reinterpret_cast<const uint32_t*>(a.biases + static_cast<size_t>(row0) * G);
+        constexpr int NSB = BR * (FAST ? 32 : kMaxGroups) / 128;
+#pragma unroll
+        for (int j = 0; j < NSB; ++j) {
+            const uint32_t i = lane + mh::kWave * j;
+            if (FAST || i < nd) {
+                const uint32_t sw = s2[i], bw = b2[i];
+                *reinterpret_cast<uint2*>(sb + 2u * i) =
+                    make_uint2(__builtin_amdgcn_perm(bw, sw, 0x05040100u),   // s.lo | b.lo << 16
+                               __builtin_amdgcn_perm(bw, sw, 0x07060302u));  // s.hi | b.hi << 16
+            }
+        }
+        const char* codes = reinterpret_cast<const char*>(a.codes) + static_cast<size_t>(row0) * row_bytes;
+        auto load = [&](int grp, mh::Chunk<BITS>(&ch)[R]) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t rr = FAST ? grp * R + r : min(static_cast<uint32_t>(grp * R + r), nrows - 1u);
+                ch[r].load_nt(mh::uniform_ptr(codes + rr * row_bytes), code_off);
+            }
+        };
+        float yv = 0.0f;
+        auto compute = [&](int grp, const mh::Chunk<BITS>(&ch)[R]) {
+            float h[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t rr = FAST ? grp * R + r : min(static_cast<uint32_t>(grp * R + r), nrows - 1u);
+                const uint32_t w = sb[rr * G + gc];
+                const float p = ch[r].dot(xr);
+                const float hv = __builtin_fmaf(__uint_as_float(w << 16), p,
+                                                __uint_as_float(w & 0xffff0000u) * xs);
+                h[r] = live ? 0.0f + hv : 0.0f;
+            }
+            const float v = reduce_rows4(h, lane);
+            const float mv = __int_as_float(__builtin_amdgcn_ds_bpermute((60 + (lane & 3)) * 4, __float_as_int(v)));
+            if ((lane >> 2) == grp) {
+                yv = mv;
+            }
+        };
+        mh::Chunk<BITS> A[R], Bc[R];
+        load(0, A);
+        if (!x_ready) {
+            mh::x_words_fence(xw);
+            mh::x_words_to_f32(xw, xr, xs);
+            if (BITS == 4) {
+                mh::q4_scale_x(xr);
+            }
+            x_ready = true;
+        }
+        load(1, Bc);
+        compute(0, A);
+        compute(1, Bc);
+        const uint16_t yb = mh::f32_to_bf16(yv);
+        if (lane < static_cast<int>(nrows)) {
+            if (a.y != nullptr) {
+                a.y[row0 + lane] = yb;
+            }
+            if (ARGMAX) {
+                mh::argmax_merge(lbv, lbi, mh::bf16_to_f32(yb), row0 + lane);
+            }
+        }
+    }
+    if (!ARGMAX) {
+        return;
+    }
+    const unsigned long long key = wave_argmax_key(lbv, lbi);
+    if (a.slots == nullptr) {
+        if (lane == 0) {
+            amax(a.best, key);
+        }
+        return;
+    }
+    // workgroup key (one slot per workgroup), then publish or collect
+    __shared__ unsigned long long wk[kWaves];
+    __shared__ unsigned long long own[1];
+    if (lane == 0) {
+        wk[wave] = key;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long t = wk[0];
+        for (int w = 1; w < kWaves; ++w) {
+            t = wk[w] > t ? wk[w] : t;
+        }
+        own[0] = t;
+    }
+    const uint32_t last = gridDim.x - 1;
+    if (blockIdx.x != last) {
+        if (threadIdx.x == 0) {
+            publish_key(a, 0, blockIdx.x, own[0]);
+        }
+        return;
+    }
+    __syncthreads();
+    collect_keys<1>(a, last, own);
+}
+
+// Row values (wave-uniform) of one row group of the staged kernel: store and
+// argmax.
 template <int B, int R>
 __device__ __forceinline__ void emit_rows(const GemvArgs& a, uint32_t rg, const float (&v)[R][B],
                                           float (&bv)[B], uint32_t (&bi)[B], int lane) {
@@ -149,7 +389,7 @@ __device__ __forceinline__ void emit_rows(const GemvArgs& a, uint32_t rg, const 
             if (lane == r) {
                 mine = vb;
             }
-            if (a.best != nullptr && row < N) {
+            if (row < N) {
                 mh::argmax_merge(bv[b], bi[b], mh::bf16_to_f32(vb), row);
             }
         }
@@ -160,79 +400,13 @@ __device__ __forceinline__ void emit_rows(const GemvArgs& a, uint32_t rg, const 
     }
 }
 
-// Batch 1, K <= 2048: each lane owns chunk `lane` of every row, with its x in
-// registers for the whole kernel.  Waves are persistent over row groups and
-// keep the next group's loads in flight during the current group's math.
-// Row addresses are wave-uniform (scalar base + the lane's fixed offset), so
-// the loads cost no vector ALU work.
-template <int BITS, int R>
-__global__ __launch_bounds__(kThreads) void k_gemv_b1(GemvArgs a) {
-    const int lane = threadIdx.x & (mh::kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / mh::kWave);
-    const uint32_t C = a.k / 32u;
-    const uint32_t N = a.n;
-    const bool live = lane < static_cast<int>(C);
-    const uint32_t c = live ? lane : 0u;
-
-    float xr[32];
-    float xs;
-    mh::load_x_chunk<BITS>(a.x + 32u * c, xr, xs);
-
-    // lane-invariant byte offsets; row bases are scalar
-    const uint32_t code_off = c * BITS * 4u;
-    const uint32_t sb_off = ((32u * c) / a.gs) * 2u;
-    const size_t row_bytes = static_cast<size_t>(a.row_words) * 4u;
-    const size_t sb_row_bytes = static_cast<size_t>(a.groups) * 2u;
-    const char* codes = reinterpret_cast<const char*>(a.codes);
-    const char* scales = reinterpret_cast<const char*>(a.scales);
-    const char* biases = reinterpret_cast<const char*>(a.biases);
-
-    float bv[1] = {-__builtin_inff()};
-    uint32_t bi[1] = {0u};
-    const uint32_t n_rg = (N + R - 1) / R;
-    const uint32_t stride = gridDim.x * kWaves;
-    uint32_t rg = blockIdx.x * kWaves + wave;
-
-    mh::Chunk<BITS> cur[R];
-    float cs[R], cb[R];
-    auto load_group = [&](uint32_t g, mh::Chunk<BITS>(&ch)[R], float(&s)[R], float(&b)[R]) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const uint32_t row = min(g * R + r, N - 1);
-            ch[r].load(mh::uniform_ptr(codes + row * row_bytes), code_off);
-            s[r] = mh::bf16_to_f32(mh::gload<uint16_t>(mh::uniform_ptr(scales + row * sb_row_bytes), sb_off));
-            b[r] = mh::bf16_to_f32(mh::gload<uint16_t>(mh::uniform_ptr(biases + row * sb_row_bytes), sb_off));
-        }
-    };
-    if (rg < n_rg) {
-        load_group(rg, cur, cs, cb);
-    }
-    while (rg < n_rg) {
-        const uint32_t next = rg + stride;
-        mh::Chunk<BITS> nxt[R];
-        float ns[R], nb[R];
-        if (next < n_rg) {
-            load_group(next, nxt, ns, nb);
-        }
-        float v[R][1];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const float p = cur[r].dot(xr);
-            const float h = __builtin_fmaf(cs[r], p, cb[r] * xs);
-            v[r][0] = mh::lane63(mh::wave_sum_lane63(live ? 0.0f + h : 0.0f));
-        }
-        emit_rows<1, R>(a, rg, v, bv, bi, lane);
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            cur[r] = nxt[r];
-            cs[r] = ns[r];
-            cb[r] = nb[r];
-        }
-        rg = next;
-    }
-    if (a.best != nullptr) {
-        fold_argmax<1>(a, bv, bi, lane, wave);
-    }
+template <int BITS>
+__device__ __forceinline__ void load_row_chunk(const GemvArgs& a, uint32_t row, uint32_t c,
+                                               mh::Chunk<BITS>& ch, float& s, float& b) {
+    ch.load(a.codes + static_cast<size_t>(row) * a.row_words + static_cast<size_t>(c) * BITS);
+    const uint32_t g = (32u * c) / a.gs;
+    s = mh::bf16_to_f32(a.scales[static_cast<size_t>(row) * a.groups + g]);
+    b = mh::bf16_to_f32(a.biases[static_cast<size_t>(row) * a.groups + g]);
 }
 
 // General form: any K, batch 1..8.  x is staged in LDS, one padded 32-float
@@ -250,7 +424,10 @@ __global__ __launch_bounds__(kThreads) void k_gemv_staged(GemvArgs a) {
     for (uint32_t t = threadIdx.x; t < B * C; t += kThreads) {
         const uint32_t b = t / C, c = t % C;
         float xc[32], s;
-        mh::load_x_chunk<BITS>(a.x + static_cast<size_t>(b) * a.k + 32u * c, xc, s);
+        mh::load_x_chunk(a.x + static_cast<size_t>(b) * a.k + 32u * c, xc, s);
+        if (BITS == 4) {
+            mh::q4_scale_x(xc);
+        }
         float4* dst = reinterpret_cast<float4*>(xl + static_cast<size_t>(t) * kXPitch);
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
@@ -317,20 +494,16 @@ __global__ __launch_bounds__(kThreads) void k_gemv_staged(GemvArgs a) {
         }
         emit_rows<B, R>(a, rg, v, bv, bi, lane);
     }
-    if (a.best != nullptr) {
-        fold_argmax<B>(a, bv, bi, lane, wave);
+    if (a.best != nullptr || a.slots != nullptr) {
+        finish_argmax<B>(a, bv, bi, lane, wave);
     }
 }
 
 constexpr int kWgPerCu = 4;
 
 template <typename K>
-int launch_grid(K kernel, const GemvArgs& a, uint32_t rows_per_wave, size_t lds, hipStream_t stream,
-                const char* name) {
-    const uint32_t n_rg = (a.n + rows_per_wave - 1) / rows_per_wave;
-    const uint32_t want = (n_rg + kWaves - 1) / kWaves;
-    const uint32_t cap = static_cast<uint32_t>(mh::cu_count()) * kWgPerCu;
-    const uint32_t grid = want < cap ? want : cap;
+int launch(K kernel, const GemvArgs& a, uint32_t grid, size_t lds, hipStream_t stream,
+           const char* name) {
     if (lds > 64u * 1024u) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -343,18 +516,40 @@ int launch_grid(K kernel, const GemvArgs& a, uint32_t rows_per_wave, size_t lds,
     return mh::launch_status(name);
 }
 
+// Workgroups for `units` wave-sized work items, capped by `cap`.
+uint32_t grid_for(uint32_t units, uint32_t cap) {
+    const uint32_t want = (units + kWaves - 1) / kWaves;
+    return want < cap ? want : cap;
+}
+
 template <int BITS, int B, int R>
 int launch_staged(const GemvArgs& a, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(B) * (a.k / 32u) * (kXPitch + 1) * sizeof(float);
-    return launch_grid(k_gemv_staged<BITS, B, R>, a, R, lds, stream, "k_gemv_staged");
+    uint32_t cap = static_cast<uint32_t>(mh::cu_count()) * kWgPerCu;
+    cap = cap < kArgSlots ? cap : kArgSlots;
+    return launch(k_gemv_staged<BITS, B, R>, a, grid_for((a.n + R - 1) / R, cap), lds, stream,
+                  "k_gemv_staged");
+}
+
+template <int BITS, bool ARGMAX>
+int launch_rows(const GemvArgs& a, hipStream_t stream) {
+    // one block per wave while the finisher has a slot for every workgroup
+    // (the hardware keeps as many workgroups resident as registers allow);
+    // beyond that the waves loop over blocks
+    const uint32_t grid = grid_for((a.n + kBlockRows - 1) / kBlockRows, kArgSlots);
+    if (a.k == 2048u && a.gs == 64u && a.n % kBlockRows == 0u) {
+        return launch(k_gemv_rows<BITS, true, ARGMAX>, a, grid, 0, stream, "k_gemv_rows");
+    }
+    return launch(k_gemv_rows<BITS, false, ARGMAX>, a, grid, 0, stream, "k_gemv_rows");
 }
 
 template <int BITS>
 int dispatch_gemv(const GemvArgs& a, uint32_t batch, hipStream_t stream) {
     switch (batch) {
         case 1:
-            if (a.k <= 2048u) {
-                return launch_grid(k_gemv_b1<BITS, 4>, a, 4, 0, stream, "k_gemv_b1");
+            if (a.k <= 2048u && a.groups <= static_cast<uint32_t>(kMaxGroups) && (a.groups & 1u) == 0u) {
+                return (a.best != nullptr || a.slots != nullptr) ? launch_rows<BITS, true>(a, stream)
+                                                                 : launch_rows<BITS, false>(a, stream);
             }
             return launch_staged<BITS, 1, 4>(a, stream);
         case 2: return launch_staged<BITS, 2, 2>(a, stream);
@@ -383,6 +578,7 @@ int gemv_common(const char* op, const mh_quant_weights* w, const uint16_t* x, ui
               "%s: argmax key not 8-byte aligned", op);
     MH_ENSURE(!finisher || (best != nullptr && ids != nullptr), MH_ERR_INVALID,
               "%s: the argmax finisher needs the scratch and ids", op);
+    MH_ENSURE(ids == nullptr || mh::aligned(ids, 4), MH_ERR_ALIGN, "%s: ids not 4-byte aligned", op);
     const uint32_t C = w->in_features / 32u;
     const bool xreg = batch == 1 && w->in_features <= 2048u;
     MH_ENSURE(xreg || static_cast<size_t>(batch) * C * (kXPitch + 1) * 4 <= kMaxLds,
@@ -394,8 +590,8 @@ int gemv_common(const char* op, const mh_quant_weights* w, const uint16_t* x, ui
     a.biases = w->biases;
     a.x = x;
     a.y = y;
-    a.best = reinterpret_cast<unsigned long long*>(best);
-    a.done = finisher ? static_cast<const void*>(best) : nullptr;
+    a.best = finisher ? nullptr : reinterpret_cast<unsigned long long*>(best);
+    a.slots = finisher ? reinterpret_cast<unsigned long long*>(best) : nullptr;
     a.ids = ids;
     a.n = w->out_features;
     a.k = w->in_features;

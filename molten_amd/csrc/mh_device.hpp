@@ -43,6 +43,12 @@ __device__ __forceinline__ T gload(gbytes base, uint32_t off) {
     return *reinterpret_cast<const __attribute__((address_space(1))) T*>(base + off);
 }
 
+// Makes the wave wait for v: used on a returning atomic's old value, so the
+// atomic has been performed at the coherence point before any later
+// instruction (a barrier, another workgroup's signal) of this wave.
+__device__ __forceinline__ void consume(unsigned long long v) { asm volatile("" ::"v"(v)); }
+__device__ __forceinline__ void consume(uint32_t v) { asm volatile("" ::"v"(v)); }
+
 // ------------------------------------------------------------------ bf16 ---
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
@@ -182,11 +188,15 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
     return v;
 }
 
-// Q4 chunk: 32 nibble codes in four words, low nibble first.  xr holds the
-// chunk's x with odd positions pre-multiplied by 1/16: the high nibble of a
-// byte is converted as 16*q and multiplied by x/16.  Both are exact (a bf16
-// times 2^-4 is an f32, denormals kept), so every fma sees the exact product
-// q*x and the chain equals fma(q_k, x_k, p) in ascending k.
+// Q4 chunk: 32 nibble codes in four words, low nibble first (code 8d+n at
+// bits 4n of word d).  xr holds the chunk's x with odd positions
+// pre-multiplied by 1/16 (q4_scale_x): the high nibble of a byte is converted
+// as 16 q (v_cvt_f32_ubyte on the word masked once) and multiplied by x/16.
+// Both are exact (a bf16 times 2^-4 is an f32, denormals kept), so every fma
+// sees the exact product q*x and the chain equals fma(q_k, x_k, p) in
+// ascending k.  (Measured on gfx950: the f16-denormal v_fma_mix_f32 form and
+// the fp8-conversion form of the same dot are both exact but not faster:
+// v_fma_mix_f32 and v_cvt_pk_f32_fp8 issue at a fraction of v_fmac_f32's rate.)
 __device__ __forceinline__ float q4_chunk_dot(const uint32_t (&w)[4], const float* xr) {
     float p = 0.0f;
 #pragma unroll
@@ -221,11 +231,10 @@ __device__ __forceinline__ float q6_chunk_dot(const uint32_t (&w)[6], const floa
     return p;
 }
 
-// A lane's 32-element bf16 chunk of x as f32 (odd positions pre-scaled for
-// Q4) plus its ascending sum; 16-byte loads when the chunk is aligned.
-template <int BITS>
-__device__ __forceinline__ void load_x_chunk(const uint16_t* xp, float (&xr)[32], float& xs) {
-    uint32_t xw[16];
+// A lane's 32-element bf16 chunk of x: the raw words (16-byte loads when the
+// chunk is aligned), then as f32 plus the ascending sum.  Split so a kernel
+// can issue its weight loads before it waits for x.
+__device__ __forceinline__ void load_x_words(const uint16_t* xp, uint32_t (&xw)[16]) {
     if ((reinterpret_cast<uintptr_t>(xp) & 15u) == 0) {
         const uint4* xv = reinterpret_cast<const uint4*>(xp);
         const uint4 v0 = xv[0], v1 = xv[1], v2 = xv[2], v3 = xv[3];
@@ -240,6 +249,9 @@ __device__ __forceinline__ void load_x_chunk(const uint16_t* xp, float (&xr)[32]
             xw[q] = static_cast<uint32_t>(xp[2 * q]) | (static_cast<uint32_t>(xp[2 * q + 1]) << 16);
         }
     }
+}
+
+__device__ __forceinline__ void x_words_to_f32(const uint32_t (&xw)[16], float (&xr)[32], float& xs) {
     xs = 0.0f;
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
@@ -249,11 +261,30 @@ __device__ __forceinline__ void load_x_chunk(const uint16_t* xp, float (&xr)[32]
         xr[2 * q] = lo;
         xr[2 * q + 1] = hi;
     }
-    if (BITS == 4) {
+}
+
+// Pins x's words after the memory operations issued so far: the compiler can
+// neither hoist their conversion above those loads nor sink the loads below it.
+__device__ __forceinline__ void x_words_fence(uint32_t (&xw)[16]) {
+    asm volatile(""
+                 : "+v"(xw[0]), "+v"(xw[1]), "+v"(xw[2]), "+v"(xw[3]), "+v"(xw[4]), "+v"(xw[5]),
+                   "+v"(xw[6]), "+v"(xw[7]), "+v"(xw[8]), "+v"(xw[9]), "+v"(xw[10]), "+v"(xw[11]),
+                   "+v"(xw[12]), "+v"(xw[13]), "+v"(xw[14]), "+v"(xw[15])
+                 :
+                 : "memory");
+}
+
+__device__ __forceinline__ void load_x_chunk(const uint16_t* xp, float (&xr)[32], float& xs) {
+    uint32_t xw[16];
+    load_x_words(xp, xw);
+    x_words_to_f32(xw, xr, xs);
+}
+
+// Scale a raw x chunk for q4_chunk_dot: odd positions times 1/16 (exact).
+__device__ __forceinline__ void q4_scale_x(float (&xr)[32]) {
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            xr[2 * q + 1] = xr[2 * q + 1] * 0.0625f;
-        }
+    for (int i = 1; i < 32; i += 2) {
+        xr[i] = xr[i] * 0.0625f;
     }
 }
 
@@ -273,6 +304,11 @@ struct Chunk<4> {
         w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
     }
     __device__ __forceinline__ void zero() { w[0] = w[1] = w[2] = w[3] = 0u; }
+    __device__ __forceinline__ void load_nt(gbytes base, uint32_t off) {  // streamed once
+        const u32x4 v = __builtin_nontemporal_load(
+            reinterpret_cast<const __attribute__((address_space(1))) u32x4*>(base + off));
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    }
     __device__ __forceinline__ float dot(const float* xr) const { return q4_chunk_dot(w, xr); }
 };
 
@@ -290,16 +326,14 @@ struct Chunk<6> {
         w[0] = a.x; w[1] = a.y; w[2] = b.x; w[3] = b.y; w[4] = c.x; w[5] = c.y;
     }
     __device__ __forceinline__ void zero() { w[0] = w[1] = w[2] = w[3] = w[4] = w[5] = 0u; }
+    __device__ __forceinline__ void load_nt(gbytes base, uint32_t off) {  // streamed once
+        typedef const __attribute__((address_space(1))) u32x2* p2;
+        const u32x2 a = __builtin_nontemporal_load(reinterpret_cast<p2>(base + off));
+        const u32x2 b = __builtin_nontemporal_load(reinterpret_cast<p2>(base + off + 8));
+        const u32x2 c = __builtin_nontemporal_load(reinterpret_cast<p2>(base + off + 16));
+        w[0] = a.x; w[1] = a.y; w[2] = b.x; w[3] = b.y; w[4] = c.x; w[5] = c.y;
+    }
     __device__ __forceinline__ float dot(const float* xr) const { return q6_chunk_dot(w, xr); }
 };
-
-// x prepared for a chunk dot: Q4 scales odd positions by 1/16.
-template <int BITS>
-__device__ __forceinline__ float prep_x(float x, int pos_in_chunk) {
-    if (BITS == 4 && (pos_in_chunk & 1)) {
-        return x * 0.0625f;
-    }
-    return x;
-}
 
 }  // namespace mh

@@ -75,7 +75,7 @@ __device__ inline void stage_x(const uint16_t* x, uint32_t t0, uint32_t nt, uint
     for (uint32_t i = threadIdx.x; i < static_cast<uint32_t>(tt) * C; i += kThreads) {
         const uint32_t t = i / C, c = i % C;
         float xc[32], s;
-        mh::load_x_chunk<0>(x + static_cast<size_t>(t0 + (t < nt ? t : 0)) * k + 32u * c, xc, s);
+        mh::load_x_chunk(x + static_cast<size_t>(t0 + (t < nt ? t : 0)) * k + 32u * c, xc, s);
         float4* d = reinterpret_cast<float4*>(xl + (static_cast<size_t>(t) * C + c) * kXPitch);
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
@@ -291,13 +291,8 @@ __device__ __forceinline__ void load_act_row(const ActArgs& a, uint32_t v, int l
 // x (K <= 2048) in registers; each wave takes R virtual rows (slot, j) at a
 // time, both matrices, with the next group's loads in flight.
 template <int R>
-__global__ __launch_bounds__(kThreads) void k_gather_act(ActArgs a) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t C = a.k / 32u;
-    const bool live = lane < static_cast<int>(C);
-    float xr[32];
-    float xs;
-    mh::load_x_chunk<4>(a.x + 32u * (live ? lane : 0), xr, xs);
+__device__ __forceinline__ void gather_act_rows(const ActArgs& a, const float (&xr)[32], float xs,
+                                                int lane, int wave, bool live) {
     const uint32_t rows = a.slots * a.n_inter;
     const uint32_t n_rg = (rows + R - 1) / R;
     const uint32_t stride = gridDim.x * kWaves;
@@ -338,6 +333,18 @@ __global__ __launch_bounds__(kThreads) void k_gather_act(ActArgs a) {
         for (int r = 0; r < R; ++r) cur[r] = nxt[r];
         rg = next;
     }
+}
+
+template <int R>
+__global__ __launch_bounds__(kThreads) void k_gather_act(ActArgs a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t C = a.k / 32u;
+    const bool live = lane < static_cast<int>(C);
+    float xr[32];
+    float xs;
+    mh::load_x_chunk(a.x + 32u * (live ? lane : 0), xr, xs);
+    mh::q4_scale_x(xr);
+    gather_act_rows<R>(a, xr, xs, lane, wave, live);
 }
 
 int launch_gather_act(const ActArgs& a, hipStream_t stream) {
@@ -394,21 +401,9 @@ struct DownArgs {
 };
 
 template <int TK>
-__global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t C = a.k / 32u;
-    const bool live = lane < static_cast<int>(C);
-    float xr[TK][32];
-    float xs[TK];
-    uint32_t e[TK];
-    float wt[TK];
-#pragma unroll
-    for (int r = 0; r < TK; ++r) {
-        mh::load_x_chunk<4>(a.act + static_cast<size_t>(r) * a.k + 32u * (live ? lane : 0), xr[r], xs[r]);
-        const uint32_t id = a.ids[r];
-        e[r] = id < a.n_experts ? id : 0u;
-        wt[r] = mh::bf16_to_f32(a.weights[r]);
-    }
+__device__ __forceinline__ void down_rows(const DownArgs& a, const float (&xr)[TK][32],
+                                          const float (&xs)[TK], const uint32_t (&e)[TK],
+                                          const float (&wt)[TK], int lane, int wave, bool live) {
     auto load = [&](uint32_t i, mh::Chunk<4>(&ch)[TK], float(&s)[TK], float(&b)[TK]) {
 #pragma unroll
         for (int r = 0; r < TK; ++r) {
@@ -453,6 +448,26 @@ __global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
         }
         i = next;
     }
+}
+
+template <int TK>
+__global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t C = a.k / 32u;
+    const bool live = lane < static_cast<int>(C);
+    float xr[TK][32];
+    float xs[TK];
+    uint32_t e[TK];
+    float wt[TK];
+#pragma unroll
+    for (int r = 0; r < TK; ++r) {
+        mh::load_x_chunk(a.act + static_cast<size_t>(r) * a.k + 32u * (live ? lane : 0), xr[r], xs[r]);
+        mh::q4_scale_x(xr[r]);
+        const uint32_t id = a.ids[r];
+        e[r] = id < a.n_experts ? id : 0u;
+        wt[r] = mh::bf16_to_f32(a.weights[r]);
+    }
+    down_rows<TK>(a, xr, xs, e, wt, lane, wave, live);
 }
 
 int launch_down(const DownArgs& a, uint32_t topk, hipStream_t stream) {

@@ -226,12 +226,12 @@ def gemv_head_argmax(w: QuantWeights, x, best, batch: int = 1, stream=None) -> N
           "gemv_head_argmax")
 
 
-ARGMAX_GROUPS = 32
+ARGMAX_SLOTS = 2048
 
 
 def argmax_scratch_words(batch: int) -> int:
     """MH_ARGMAX_SCRATCH_WORDS(batch): u64 words of gemv_quant_argmax scratch."""
-    return (ARGMAX_GROUPS + 1) * batch + ARGMAX_GROUPS + 1
+    return ARGMAX_SLOTS * batch
 
 
 def gemv_quant_argmax(w: QuantWeights, x, y, scratch, ids, batch: int = 1, stream=None) -> None:

@@ -40,6 +40,37 @@ def test_gemv_bit_exact(dev, orc, bits, n, k, batch):
     np.testing.assert_array_equal(got, want)
 
 
+def _extreme_x(rng, batch, k, huge):
+    """N(0,1) activations with f32-denormal, zero and -0 entries, and (huge)
+    a few finite entries of magnitude 2^110."""
+    x = rng.normal(0, 1, (batch, k)).astype(np.float32)
+    idx = rng.choice(k, 64, replace=False)
+    x[:, idx[:16]] = np.float32(2.0 ** -130) * np.sign(rng.normal(size=16)).astype(np.float32)
+    x[:, idx[16:24]] = 0.0
+    x[:, idx[24:32]] = -0.0
+    if huge:
+        x[:, idx[32:36]] = np.float32(2.0 ** 110) * np.array([1, -1, 1, -1], np.float32)
+    return layout.f32_to_bf16(x)
+
+
+@pytest.mark.parametrize("huge", [False, True])
+@pytest.mark.parametrize("n,k,batch", [(512, 2048, 1), (96, 11776, 1), (256, 2048, 4)])
+def test_q4_extreme_activations(dev, orc, huge, n, k, batch):
+    """Denormal, signed-zero and (huge) 2^110 activations: the mix form of
+    the Q4 dot is exact for the first three, and the kernels switch to the
+    convert form when x * 2^24 would overflow; both stay bit-exact."""
+    _log(f"q4 extreme x huge={huge} n={n} k={k} batch={batch}")
+    rng = np.random.default_rng(5 + huge + k + batch)
+    h = layout.synth_quant(rng, n, k, 4)
+    x = _extreme_x(rng, batch, k, huge)
+    want = orc.gemv_quant(h, x, batch)
+    assert np.isfinite(layout.bf16_to_f32(want)).all()
+    w, keep = dev_quant(h)
+    y = empty_dev((batch, n), np.uint16)
+    hip.gemv_quant(w, to_dev(x), y, batch)
+    np.testing.assert_array_equal(from_dev(y, np.uint16), want)
+
+
 @pytest.mark.parametrize("bits", [4, 6])
 @pytest.mark.parametrize("gs", [32, 128])
 def test_gemv_other_group_sizes(dev, orc, bits, gs):

@@ -116,6 +116,38 @@ def test_down_combine_bit_exact(dev, orc, experts, topk):
     np.testing.assert_array_equal(from_dev(out, np.uint16), orc.down_combine(down, H, act, ids, w))
 
 
+@pytest.mark.parametrize("huge", [False, True])
+def test_expert_kernels_extreme_activations(dev, orc, experts, huge):
+    """gather_act and down_combine with denormal / signed-zero / 2^100-scale
+    inputs (the latter forces the convert form of the Q4 dot)."""
+    gate, up, down = experts["h"]
+    dg, du, dd = experts["d"]
+    rng = np.random.default_rng(20 + huge)
+
+    def extreme(shape, scale):
+        v = rng.normal(0, 1, shape).astype(np.float32)
+        flat = v.reshape(-1)
+        idx = rng.choice(flat.size, 48, replace=False)
+        flat[idx[:16]] = np.float32(2.0 ** -130)
+        flat[idx[16:24]] = -0.0
+        if huge:
+            flat[idx[24:28]] = np.float32(scale)
+        return layout.f32_to_bf16(v)
+
+    x = extreme((H,), 2.0 ** 106)
+    ids = rng.choice(E, TOPK, replace=False).astype(np.uint32)
+    act = empty_dev((TOPK, I), np.uint16)
+    hip.gemv_gather_act(dg, du, to_dev(x), to_dev(ids), act, TOPK, I)
+    np.testing.assert_array_equal(from_dev(act, np.uint16), orc.gather_act(gate, up, I, x, ids))
+    a = extreme((TOPK, I), 2.0 ** 105)
+    w = layout.f32_to_bf16(np.full(TOPK, 0.25, np.float32))
+    out = empty_dev((H,), np.uint16)
+    hip.gemv_gather_down_combine4(dd, to_dev(a), to_dev(ids), to_dev(w), out, TOPK, H)
+    want = orc.down_combine(down, H, a, ids, w)
+    assert np.isfinite(layout.bf16_to_f32(want)).all()
+    np.testing.assert_array_equal(from_dev(out, np.uint16), want)
+
+
 @pytest.mark.parametrize("mode,f32", [(1, False), (0, True)])
 def test_moe_decode_step_bit_exact(dev, orc, experts, mode, f32):
     """Config 3: router -> top-4 -> gate/up/SwiGLU -> down -> combine, all
