@@ -15,7 +15,8 @@ BASELINE configs are measured in the same run and reported under "others":
 Weights are synthetic (BASELINE distributions, random-init, generated on the
 GPU) and rotated over enough copies (>= 300 MB) that the 256 MB Infinity
 Cache cannot hold the working set; the MoE inputs vary per step so routing
-changes.  Kernel times come from HIP events recorded on the launch stream.
+changes.  The timed steps are captured in one HIP graph and replayed between
+HIP events on the launch stream (no host launch overhead in the timing).
 The CPU baseline is the C oracle timed on the host cores on a bounded sample.
 """
 from __future__ import annotations
@@ -69,19 +70,32 @@ def bf16_randn(torch, shape, dev, gen, std=1.0):
 
 
 def timed(torch, fn, steps, warmup):
-    """Average ms per call of fn(i) over `steps` calls after `warmup` calls,
-    bracketed by synchronizes; events on the current (launch) stream."""
+    """Average ms per call of fn(i) over `steps` calls after `warmup` eager
+    calls.  The `steps` calls are captured once in a HIP graph and the graph
+    is replayed between two events on the launch stream, bracketed by
+    synchronizes, so host launch overhead (ctypes, Python) is not timed: the
+    GPU runs the kernels back to back, as a decode loop captured in a graph
+    would."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(steps):
-        fn(warmup + i)
-    end.record()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            fn(warmup + i)
+    graph.replay()  # untimed first replay
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    times = []
+    for _ in range(5):  # median of five timed replays
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end) / steps)
+    del graph
+    return sorted(times)[len(times) // 2]
 
 
 def bench_lm_head(torch, hip, dev, gen, bits, batch, steps, warmup, copies):

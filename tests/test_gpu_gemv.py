@@ -112,6 +112,47 @@ def test_argmax_paths_agree_with_oracle(dev, orc, bits, batch):
     assert from_dev(best, np.uint64).tolist() == [0] * batch
 
 
+def test_lm_head_argmax_graph_replays(dev, orc):
+    """The GEMV + argmax finisher captured in a HIP graph (three weight sets
+    sharing one scratch) and replayed several times, with eager launches on
+    the same scratch and cleared outputs between replays: every replay
+    reproduces the eager logits and ids."""
+    _log("graph replay gemv_quant_argmax")
+    rng = np.random.default_rng(606)
+    n, k = 8192, 2048
+    hs = [layout.synth_quant(rng, n, k, 4) for _ in range(3)]
+    x = layout.synth_bf16(rng, (1, k))
+    devw = [dev_quant(h) for h in hs]
+    xd = to_dev(x)
+    want = [orc.gemv_quant(h, x, 1) for h in hs]
+    want_ids = [orc.argmax_bf16(w[0]) for w in want]
+    scratch = zeros_dev((hip.argmax_scratch_words(1),), np.uint64)
+    ys = [empty_dev((1, n), np.uint16) for _ in hs]
+    ids = [empty_dev((1,), np.uint32) for _ in hs]
+    for (w, _), y, i in zip(devw, ys, ids):  # eager warm-up
+        hip.gemv_quant_argmax(w, xd, y, scratch, i, 1)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for (w, _), y, i in zip(devw, ys, ids):
+            hip.gemv_quant_argmax(w, xd, y, scratch, i, 1)
+    other_y = empty_dev((1, n), np.uint16)
+    other_id = empty_dev((1,), np.uint32)
+    for rep in range(4):
+        for y, i in zip(ys, ids):
+            y.zero_()
+            i.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        for c in range(3):
+            np.testing.assert_array_equal(from_dev(ys[c], np.uint16), want[c])
+            assert int(from_dev(ids[c], np.uint32)[0]) == want_ids[c]
+        assert not from_dev(scratch, np.uint64).any()
+        hip.gemv_quant_argmax(devw[rep % 3][0], xd, other_y, scratch, other_id, 1)  # eager, same scratch
+        torch.cuda.synchronize()
+        assert int(from_dev(other_id, np.uint32)[0]) == want_ids[rep % 3]
+
+
 def test_argmax_ties_take_lowest_index(dev, orc):
     # identical rows -> identical logits: the lowest row must win
     rng = np.random.default_rng(5)
