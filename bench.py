@@ -71,11 +71,11 @@ def bf16_randn(torch, shape, dev, gen, std=1.0):
 
 def timed(torch, fn, steps, warmup):
     """Average ms per call of fn(i) over `steps` calls after `warmup` eager
-    calls.  The `steps` calls are captured once in a HIP graph and the graph
-    is replayed between two events on the launch stream, bracketed by
-    synchronizes, so host launch overhead (ctypes, Python) is not timed: the
-    GPU runs the kernels back to back, as a decode loop captured in a graph
-    would."""
+    calls.  The `steps` calls are captured once in a HIP graph; the graph is
+    replayed five times, each replay between two events on the launch stream
+    and bracketed by synchronizes, and the median replay is returned.  Host
+    launch overhead (ctypes, Python) is not timed: the GPU runs the kernels
+    back to back, as a decode loop captured in a graph would."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
