@@ -68,85 +68,141 @@ __device__ __forceinline__ bf16x8_t deq_word(uint32_t w, float s, float s16, flo
     return __builtin_bit_cast(bf16x8_t, u);
 }
 
-template <int BM, int NBW, int WAVES, bool GATHER, int EPI>
-__global__ __launch_bounds__(WAVES * 64) void k_grouped(GemmArgs a) {
-    constexpr int kThr = WAVES * 64;
+typedef __attribute__((address_space(3))) void* lds_ptr;
+typedef const __attribute__((address_space(1))) void* glb_ptr;
+
+constexpr int kStages = 3;  // LDS ring depth: two K-blocks in flight while one is consumed
+
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// 16-byte LDS read issued without a wait: the caller waits with lds_wait.
+// (Written as asm so the compiler does not wait for every outstanding
+// direct-to-LDS load before it.)
+__device__ __forceinline__ uint4 lds_read16(uint32_t addr) {
+    uint4 v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+
+// Direct-to-LDS 16-byte load: lane l's data lands at lds_base + 16 l.
+__device__ __forceinline__ void dma16(mh::gbytes src, uint32_t lds_base) {
+    __builtin_amdgcn_global_load_lds((glb_ptr)src, (lds_ptr)(uintptr_t)lds_base, 16, 0, 0);
+}
+// Direct-to-LDS 4-byte load: lane l's dword lands at lds_base + 4 l.
+__device__ __forceinline__ void dma4(mh::gbytes src, uint32_t lds_base) {
+    __builtin_amdgcn_global_load_lds((glb_ptr)src, (lds_ptr)(uintptr_t)lds_base, 4, 0, 0);
+}
+__device__ __forceinline__ uint32_t lds_read4(uint32_t addr) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+
+// Tile of BM rows x (NW * NBW * 32) columns per matrix; NW waves, wave w owns
+// column blocks [w * NBW, (w + 1) * NBW) of every matrix and all BM rows.
+// K advances 64 at a time through a kStages-deep LDS ring:
+//   A (the BM x 64 activation block, rows gathered) arrives by direct-to-LDS
+//     loads shared by the workgroup, 16-byte chunks XOR-swizzled by row so the
+//     MFMA operand reads are bank-conflict free;
+//   B codes (16 bytes per lane: a column's 32 codes of one k-half) arrive by
+//     direct-to-LDS loads into the owning wave's region;
+//   scales and biases are register loads.
+// Each wave waits for its own loads of a stage (vmcnt), one barrier then
+// publishes the A block and frees the slot the next stage overwrites.
+// Row blocks of 32 past the expert's segment are skipped.  Block-map entries
+// are taken XCD by XCD: workgroup i runs entry (i % 8) * L + i / 8, so the
+// entries that share A rows (one expert's row tile across its column tiles)
+// run on one XCD and hit its L2.
+template <int BM, int NBW, int NW, bool GATHER, int EPI>
+__global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void k_grouped(GemmArgs a, uint32_t n_entries) {
+    constexpr int kThr = NW * 64;
     constexpr int RB = BM / 32;
     constexpr int NMAT = (EPI == EPI_STORE) ? 1 : 2;
-    constexpr int SEGS = (BM * 8 + kThr - 1) / kThr;  // 16-byte A segments per thread per block
-    __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kAPitch];
+    constexpr int QA = BM / (8 * NW);             // A loads (8 rows each) per wave per stage
+    constexpr int NB = NMAT * NBW;                // B column blocks per wave
+    constexpr int A_BYTES = BM * 128;
+    constexpr int B_BYTES = NW * NB * 1024;
+    constexpr int SB_BYTES = NW * NB * 256;
+    constexpr int STAGE = A_BYTES + B_BYTES + SB_BYTES;
+    constexpr int STAGE_OPS = QA + 2 * NB;        // vector memory ops per wave per stage
+    static_assert(BM % (8 * NW) == 0, "A rows per wave");
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    (void)kThr;
 
-    const uint4 blk = a.blocks[blockIdx.x];
+    const uint32_t per_xcd = (n_entries + 7u) / 8u;
+    const uint32_t ent = (blockIdx.x % 8u) * per_xcd + blockIdx.x / 8u;
+    if (ent >= n_entries) {
+        return;
+    }
+    const uint4 blk = a.blocks[ent];
     const uint32_t m0 = blk.x, brow = blk.y, n0 = blk.z, m_end = blk.w;
     if (m0 >= m_end) {
         return;
     }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int i32 = lane & 31, h = lane >> 5;
     const uint32_t K = a.k, nkb = K / kBK;
-    const uint32_t words = K / 8u, groups = K / 64u;
+    const uint32_t groups = K / 64u;
+    const uint32_t live_rb = min(static_cast<uint32_t>(RB), (m_end - m0 + 31u) / 32u);
+    const uint32_t lds0 = static_cast<uint32_t>((uintptr_t)((lds_ptr)lds));
 
-    // ---- A staging
-    uint4 ra[SEGS];
-    size_t arow[SEGS];
-    int lrow[SEGS], lseg[SEGS];
-    bool lval[SEGS];
-#pragma unroll
-    for (int i = 0; i < SEGS; ++i) {
-        const int idx = threadIdx.x + i * kThr;
-        lval[i] = idx < BM * 8;
-        lrow[i] = idx / 8;
-        lseg[i] = idx % 8;
-        const uint32_t m = min(m0 + static_cast<uint32_t>(lrow[i]), m_end - 1);
-        uint32_t src = m;
-        if (GATHER) {
-            src = a.gather[m];
-        }
-        src = min(src, a.a_rows - 1);
-        arow[i] = static_cast<size_t>(src) * K;
+    // 32-bit byte offsets from wave-uniform bases (the host checks that the
+    // operands fit in 4 GiB), so each load is scalar base + vector offset.
+    const mh::gbytes abase = mh::uniform_ptr(a.a);
+    mh::gbytes cbase[NMAT], sbase[NMAT], bbase[NMAT];
+    cbase[0] = mh::uniform_ptr(a.c0);
+    sbase[0] = mh::uniform_ptr(a.s0);
+    bbase[0] = mh::uniform_ptr(a.b0);
+    if (NMAT == 2) {
+        cbase[NMAT - 1] = mh::uniform_ptr(a.c1);
+        sbase[NMAT - 1] = mh::uniform_ptr(a.s1);
+        bbase[NMAT - 1] = mh::uniform_ptr(a.b1);
     }
-    auto load_a = [&](uint32_t kb) {
+    // A: this lane's source row for each of its QA loads (clamped into the segment)
+    uint32_t aoffs[QA];
 #pragma unroll
-        for (int i = 0; i < SEGS; ++i) {
-            if (lval[i]) {
-                ra[i] = *reinterpret_cast<const uint4*>(a.a + arow[i] + kb * kBK + 8 * lseg[i]);
-            }
-        }
-    };
-    auto store_a = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < SEGS; ++i) {
-            if (lval[i]) {
-                *reinterpret_cast<uint4*>(&As[buf][lrow[i] * kAPitch + 8 * lseg[i]]) = ra[i];
-            }
-        }
-    };
-
-    // ---- B: this lane's weight rows (one per column block and matrix)
-    size_t wrow[NMAT][NBW];
+    for (int q = 0; q < QA; ++q) {
+        const uint32_t r = 8u * (wave * QA + q) + static_cast<uint32_t>(lane >> 3);
+        const uint32_t m = min(m0 + r, m_end - 1u);
+        uint32_t src = GATHER ? a.gather[m] : m;
+        src = min(src, a.a_rows - 1u);
+        const uint32_t chunk = static_cast<uint32_t>(lane & 7) ^ (r & 7u);
+        aoffs[q] = src * K * 2u + chunk * 16u;
+    }
+    // B: this lane's weight row (column) per column block and matrix.  The
+    // scale/bias load is one dword per lane: lanes 0-31 the column's scale
+    // pair (groups kb & ~1, kb | 1), lanes 32-63 its bias pair.
+    uint32_t boffs[NB], sboffs[NB];
 #pragma unroll
     for (int cb = 0; cb < NBW; ++cb) {
-        const uint32_t r = min(brow + static_cast<uint32_t>(wave * 32 * NBW + cb * 32 + i32), a.w_rows - 1);
+        const uint32_t col = static_cast<uint32_t>((wave * NBW + cb) * 32 + i32);
+        const uint32_t r = min(brow + col, a.w_rows - 1u);
 #pragma unroll
         for (int mat = 0; mat < NMAT; ++mat) {
-            wrow[mat][cb] = r;
+            boffs[mat * NBW + cb] = r * (K / 2u) + 16u * h;
+            sboffs[mat * NBW + cb] = r * groups * 2u;
         }
     }
-    uint4 bc[NMAT][NBW];
-    float bs[NMAT][NBW], bb[NMAT][NBW];
-    auto load_b = [&](uint32_t kb, uint4(&c)[NMAT][NBW], float(&s)[NMAT][NBW], float(&b)[NMAT][NBW]) {
+
+    auto issue = [&](uint32_t kb, int slot) {
+        const uint32_t base = lds0 + slot * STAGE;
 #pragma unroll
-        for (int mat = 0; mat < NMAT; ++mat) {
-            const uint32_t* cp = mat == 0 ? a.c0 : a.c1;
-            const uint16_t* sp = mat == 0 ? a.s0 : a.s1;
-            const uint16_t* bp = mat == 0 ? a.b0 : a.b1;
+        for (int q = 0; q < QA; ++q) {
+            dma16(abase + aoffs[q] + kb * 128u, base + (wave * QA + q) * 1024u);
+        }
 #pragma unroll
-            for (int cb = 0; cb < NBW; ++cb) {
-                const size_t r = wrow[mat][cb];
-                c[mat][cb] = *reinterpret_cast<const uint4*>(cp + r * words + 8u * kb + 4u * h);
-                s[mat][cb] = mh::bf16_to_f32(sp[r * groups + kb]);
-                b[mat][cb] = mh::bf16_to_f32(bp[r * groups + kb]);
-            }
+        for (int t = 0; t < NB; ++t) {
+            dma16(cbase[t / NBW] + boffs[t] + kb * 32u, base + A_BYTES + (wave * NB + t) * 1024u);
+        }
+#pragma unroll
+        for (int t = 0; t < NB; ++t) {
+            const mh::gbytes sb = h ? bbase[t / NBW] : sbase[t / NBW];
+            dma4(sb + sboffs[t] + (kb & ~1u) * 2u, base + A_BYTES + B_BYTES + (wave * NB + t) * 256u);
         }
     };
 
@@ -160,57 +216,85 @@ __global__ __launch_bounds__(WAVES * 64) void k_grouped(GemmArgs a) {
 #pragma unroll
                 for (int q = 0; q < 16; ++q) acc[mat][rb][cb][q] = 0.0f;
 
-    load_a(0);
-    load_b(0, bc, bs, bb);
-    store_a(0);
-    __syncthreads();
+    // A operand addresses: row rb*32 + i32, logical chunk 4h + j, swizzled
+    uint32_t aoff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        aoff[j] = static_cast<uint32_t>(i32) * 128u + ((static_cast<uint32_t>(4 * h + j) ^ static_cast<uint32_t>(i32 & 7)) * 16u);
+    }
 
-    for (uint32_t kb = 0; kb < nkb; ++kb) {
-        const int buf = kb & 1;
-        const bool more = kb + 1 < nkb;
-        uint4 nc[NMAT][NBW];
-        float ns[NMAT][NBW], nb[NMAT][NBW];
-        if (more) {
-            load_a(kb + 1);
-            load_b(kb + 1, nc, ns, nb);
+#pragma unroll
+    for (int d = 0; d < kStages - 1; ++d) {
+        if (static_cast<uint32_t>(d) < nkb) {
+            issue(d, d);
         }
-        bf16x8_t bf[NMAT][NBW][4];
+    }
+    for (uint32_t kb0 = 0; kb0 < nkb; kb0 += kStages) {
 #pragma unroll
-        for (int mat = 0; mat < NMAT; ++mat)
-#pragma unroll
-            for (int cb = 0; cb < NBW; ++cb) {
-                const float s = bs[mat][cb], s16 = s * 0.0625f, b = bb[mat][cb];
-                const uint32_t wv[4] = {bc[mat][cb].x, bc[mat][cb].y, bc[mat][cb].z, bc[mat][cb].w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) bf[mat][cb][j] = deq_word(wv[j], s, s16, b);
+        for (int u = 0; u < kStages; ++u) {
+            const uint32_t kb = kb0 + u;
+            if (kb >= nkb) {
+                break;
             }
-        const uint16_t* at = As[buf];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb) {
-                const uint4 av = *reinterpret_cast<const uint4*>(at + (rb * 32 + i32) * kAPitch + 32 * h + 8 * j);
-                const bf16x8_t af = __builtin_bit_cast(bf16x8_t, av);
-#pragma unroll
-                for (int mat = 0; mat < NMAT; ++mat)
-#pragma unroll
-                    for (int cb = 0; cb < NBW; ++cb)
-                        acc[mat][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                            af, bf[mat][cb][j], acc[mat][rb][cb], 0, 0, 0);
+            // own loads of stage kb done (later stages may stay in flight)
+            if (kb + 1 < nkb) {
+                wait_vmcnt<STAGE_OPS>();
+            } else {
+                wait_vmcnt<0>();
             }
-        }
-        if (more) {
-            store_a(buf ^ 1);
+            __builtin_amdgcn_s_barrier();  // no fence: later stages stay in flight
+            if (kb + kStages - 1 < nkb) {
+                issue(kb + kStages - 1, (u + kStages - 1) % kStages);
+            }
+            const uint32_t base = lds0 + u * STAGE;
+            uint4 bcode[NB];
+            uint32_t sw[NB], bw[NB];
 #pragma unroll
-            for (int mat = 0; mat < NMAT; ++mat)
+            for (int t = 0; t < NB; ++t) {
+                bcode[t] = lds_read16(base + A_BYTES + (wave * NB + t) * 1024u + lane * 16u);
+                const uint32_t sbl = base + A_BYTES + B_BYTES + (wave * NB + t) * 256u + i32 * 4u;
+                sw[t] = lds_read4(sbl);
+                bw[t] = lds_read4(sbl + 128u);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            const uint32_t half = (kb & 1u) ? 0u : 16u;  // bf16 of group kb in the high half
+            float sf[NB], s16[NB], bf[NB];
 #pragma unroll
-                for (int cb = 0; cb < NBW; ++cb) {
-                    bc[mat][cb] = nc[mat][cb];
-                    bs[mat][cb] = ns[mat][cb];
-                    bb[mat][cb] = nb[mat][cb];
+            for (int t = 0; t < NB; ++t) {
+                sf[t] = __uint_as_float((sw[t] << half) & 0xffff0000u);
+                s16[t] = sf[t] * 0.0625f;
+                bf[t] = __uint_as_float((bw[t] << half) & 0xffff0000u);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                bf16x8_t bfr[NB];
+#pragma unroll
+                for (int t = 0; t < NB; ++t) {
+                    const uint32_t wv = j == 0 ? bcode[t].x : j == 1 ? bcode[t].y : j == 2 ? bcode[t].z : bcode[t].w;
+                    bfr[t] = deq_word(wv, sf[t], s16[t], bf[t]);
                 }
+                uint4 av[RB];
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) {
+                    if (static_cast<uint32_t>(rb) < live_rb) {
+                        av[rb] = lds_read16(base + rb * 4096u + aoff[j]);
+                    }
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) {
+                    if (static_cast<uint32_t>(rb) < live_rb) {
+                        const bf16x8_t af = __builtin_bit_cast(bf16x8_t, av[rb]);
+#pragma unroll
+                        for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+                            for (int cb = 0; cb < NBW; ++cb)
+                                acc[mat][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                    af, bfr[mat * NBW + cb], acc[mat][rb][cb], 0, 0, 0);
+                    }
+                }
+            }
         }
-        __syncthreads();
     }
 
     // ---- epilogue: D lane layout row = 8*(q/4) + 4*h + q%4, col = i32
@@ -222,7 +306,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_grouped(GemmArgs a) {
             for (int q = 0; q < 16; ++q) {
                 const uint32_t row = m0 + rb * 32 + 8 * (q / 4) + 4 * h + (q % 4);
                 if (row >= m_end) continue;
-                const size_t o = static_cast<size_t>(row) * a.n + n0 + wave * 32 * NBW + cb * 32 + i32;
+                const size_t o = static_cast<size_t>(row) * a.n + n0 + (wave * NBW + cb) * 32 + i32;
                 if constexpr (EPI == EPI_STORE) {
                     a.out0[o] = mh::f32_to_bf16(acc[0][rb][cb][q]);
                 } else if constexpr (EPI == EPI_GATE_UP) {
@@ -236,10 +320,21 @@ __global__ __launch_bounds__(WAVES * 64) void k_grouped(GemmArgs a) {
             }
 }
 
-template <int BM, int NBW, int WAVES, bool GATHER, int EPI>
+template <int BM, int NBW, int NW, bool GATHER, int EPI>
 int launch_t(const GemmArgs& a, uint32_t n_blocks, hipStream_t s) {
-    hipLaunchKernelGGL((k_grouped<BM, NBW, WAVES, GATHER, EPI>), dim3(n_blocks), dim3(WAVES * 64), 0,
-                       s, a);
+    constexpr int NMAT = (EPI == EPI_STORE) ? 1 : 2;
+    constexpr size_t lds = static_cast<size_t>(kStages) * (BM * 128 + NW * NMAT * NBW * (1024 + 256));
+    auto kern = k_grouped<BM, NBW, NW, GATHER, EPI>;
+    if (lds > 64u * 1024u) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 static_cast<int>(lds));
+        if (e != hipSuccess) {
+            return mh::hip_error(e, "k_grouped");
+        }
+    }
+    const uint32_t grid = (n_blocks + 7u) / 8u * 8u;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), lds, s, a, n_blocks);
     return mh::launch_status("k_grouped");
 }
 
