@@ -204,36 +204,6 @@ constexpr int kBlockRows = 8;
 constexpr int kGroupRows = 4;
 constexpr int kMaxGroups = 64;  // K / group size <= 2048 / 32
 
-// Four row values h[0..3] per lane reduced with the chunk order's xor
-// butterfly, four rows in one register: levels 1 and 2 (xor 1, xor 2) pair
-// lanes holding the same row, after which lane l carries row (l & 3); levels
-// 3..6 use row_shr:4 (correct where bit 2 of the lane is set), row_ror:8
-// (xor 8) and the permlane16/32 swaps (xor 16, xor 32).  Every addition is
-// a_l + a_{l^m} of the single-row butterfly (addition is commutative), so
-// lane 60 + j ends with row j's butterfly value.
-template <int CTRL>
-__device__ __forceinline__ float qmove(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-
-__device__ __forceinline__ float reduce_rows4(const float (&h)[4], int lane) {
-    const bool b0 = lane & 1, b1 = (lane >> 1) & 1;
-    const float s01 = (b0 ? h[1] : h[0]) + qmove<0xB1>(b0 ? h[0] : h[1]);  // quad_perm 1,0,3,2
-    const float s23 = (b0 ? h[3] : h[2]) + qmove<0xB1>(b0 ? h[2] : h[3]);
-    float v = (b1 ? s23 : s01) + qmove<0x4E>(b1 ? s01 : s23);              // quad_perm 2,3,0,1
-    v = v + mh::dpp_move<0x114, 0xf>(v);  // row_shr:4
-    v = v + mh::dpp_move<0x128, 0xf>(v);  // row_ror:8
-    {
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-    {
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-    return v;
-}
-
 // Batch 1, K <= 2048, even K / group size.  Each wave owns blocks of
 // kBlockRows consecutive rows (one block per wave up to kArgSlots
 // workgroups).  A block's scales and biases are read with a few wide loads
@@ -309,7 +279,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
                                                 __uint_as_float(w & 0xffff0000u) * xs);
                 h[r] = live ? 0.0f + hv : 0.0f;
             }
-            const float v = reduce_rows4(h, lane);
+            const float v = mh::reduce_rows4(h, lane);
             const float mv = __int_as_float(__builtin_amdgcn_ds_bpermute((60 + (lane & 3)) * 4, __float_as_int(v)));
             if ((lane >> 2) == grp) {
                 yv = mv;

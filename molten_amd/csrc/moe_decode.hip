@@ -175,6 +175,126 @@ __global__ __launch_bounds__(kThreads) void k_dense_gemv(DenseArgs a) {
     }
 }
 
+// Many tokens, K <= 2048 (the prefill router): a workgroup owns 4 tokens,
+// each wave a quarter of the experts.  A wave keeps the tokens' x chunks in
+// registers (lane c holds chunk c), streams its experts' rows (the next row's
+// loads in flight during the current row's fmas), reduces the four tokens'
+// chunk sums in one 4-row butterfly and gathers expert e's logits into lane
+// e % 64 of a per-token register; the logits are stored with one coalesced
+// store per token.  Same chunk order as k_dense_gemv.
+template <typename WT>
+struct RowWords;
+template <>
+struct RowWords<uint16_t> {  // 32 bf16 = 16 words
+    uint4 v[4];
+    __device__ __forceinline__ void load(const uint16_t* p) {
+        const uint4* q = reinterpret_cast<const uint4*>(p);
+        v[0] = q[0]; v[1] = q[1]; v[2] = q[2]; v[3] = q[3];
+    }
+    __device__ __forceinline__ void to_f32(float (&w)[32]) const {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t u[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                w[8 * i + 2 * j] = mh::bf16lo(u[j]);
+                w[8 * i + 2 * j + 1] = mh::bf16hi(u[j]);
+            }
+        }
+    }
+};
+template <>
+struct RowWords<float> {  // 32 f32
+    float4 v[8];
+    __device__ __forceinline__ void load(const float* p) {
+        const float4* q = reinterpret_cast<const float4*>(p);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = q[i];
+    }
+    __device__ __forceinline__ void to_f32(float (&w)[32]) const {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            w[4 * i] = v[i].x; w[4 * i + 1] = v[i].y; w[4 * i + 2] = v[i].z; w[4 * i + 3] = v[i].w;
+        }
+    }
+};
+
+constexpr int kRowTokens = 4;
+constexpr int kMaxExpertGroups = mh::kMaxExperts / 64;
+
+template <typename WT>
+__global__ __launch_bounds__(kThreads) void k_dense_rows(DenseArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t C = a.k / 32u;
+    const bool live = lane < static_cast<int>(C);
+    const uint32_t c = live ? lane : 0u;
+    const uint32_t t0 = blockIdx.x * kRowTokens;
+    const uint32_t per_wave = (a.n + kWaves - 1) / kWaves;
+    const uint32_t e_begin = wave * per_wave;
+    const uint32_t e_end = min(a.n, e_begin + per_wave);
+    if (e_begin >= e_end) {
+        return;
+    }
+    float xr[kRowTokens][32];
+#pragma unroll
+    for (int t = 0; t < kRowTokens; ++t) {
+        const uint32_t tok = min(t0 + t, a.m - 1u);
+        float xs;
+        mh::load_x_chunk(a.x + static_cast<size_t>(tok) * a.k + 32u * c, xr[t], xs);
+    }
+    const WT* w = static_cast<const WT*>(a.w) + 32u * c;
+    float out[kMaxExpertGroups][kRowTokens];
+#pragma unroll
+    for (int g = 0; g < kMaxExpertGroups; ++g)
+#pragma unroll
+        for (int t = 0; t < kRowTokens; ++t) out[g][t] = 0.0f;
+    RowWords<WT> cur, nxt;
+    cur.load(w + static_cast<size_t>(e_begin) * a.k);
+    for (uint32_t e = e_begin; e < e_end; ++e) {
+        if (e + 1 < e_end) {
+            nxt.load(w + static_cast<size_t>(e + 1) * a.k);
+        }
+        float wr[32];
+        cur.to_f32(wr);
+        float h[kRowTokens];
+#pragma unroll
+        for (int t = 0; t < kRowTokens; ++t) {
+            float p = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                p = __builtin_fmaf(wr[i], xr[t][i], p);
+            }
+            h[t] = live ? 0.0f + p : 0.0f;
+        }
+        const float v = mh::reduce_rows4(h, lane);
+        const uint32_t g = e >> 6, le = e & 63u;
+#pragma unroll
+        for (int t = 0; t < kRowTokens; ++t) {
+            const float vt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 60 + t));
+#pragma unroll
+            for (int gg = 0; gg < kMaxExpertGroups; ++gg) {
+                if (gg == static_cast<int>(g) && static_cast<uint32_t>(lane) == le) {
+                    out[gg][t] = vt;
+                }
+            }
+        }
+        cur = nxt;
+    }
+#pragma unroll
+    for (int t = 0; t < kRowTokens; ++t) {
+        if (t0 + t < a.m) {
+#pragma unroll
+            for (int g = 0; g < kMaxExpertGroups; ++g) {
+                const uint32_t e = g * 64u + lane;
+                if (e >= e_begin && e < e_end) {
+                    a.y[static_cast<size_t>(t0 + t) * a.n + e] = out[g][t];
+                }
+            }
+        }
+    }
+}
+
 template <typename WT, int TT, int EPW>
 int launch_dense(const DenseArgs& a, hipStream_t stream) {
     const uint32_t C = a.k / 32u;
@@ -197,6 +317,11 @@ template <typename WT>
 int dispatch_dense(const DenseArgs& a, hipStream_t stream) {
     if (a.m == 1) {
         return launch_dense<WT, 1, 1>(a, stream);
+    }
+    if (a.k <= 2048u && a.n <= static_cast<uint32_t>(mh::kMaxExperts) && a.done == nullptr) {
+        hipLaunchKernelGGL(k_dense_rows<WT>, dim3((a.m + kRowTokens - 1) / kRowTokens), dim3(kThreads), 0,
+                           stream, a);
+        return mh::launch_status("k_dense_rows");
     }
     return launch_dense<WT, 8, 4>(a, stream);
 }
