@@ -37,6 +37,16 @@ inline bool aligned(const void* p, uintptr_t a) {
 int check_quant(const mh_quant_weights* w, const char* op);
 
 // Launch status after hipLaunchKernelGGL.
+// Internal launches of the prefill MoE step (moe_prefill.hip, moe_decode.hip).
+int moe_sort_maps(const uint32_t* ids, uint32_t s, uint32_t e, uint32_t topk, uint32_t* counts,
+                  uint32_t* offsets, uint32_t* gu_off, uint32_t* dn_off, uint32_t* ids_sorted,
+                  uint32_t* slotpos, uint32_t* gu, uint32_t max_gu, uint32_t* dn, uint32_t max_dn,
+                  uint32_t bm, uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n, uint32_t dn_n,
+                  mh_stream_t stream);
+int router_prefill_route(const uint16_t* x, const void* w, int w_dtype, float* logits,
+                         const float* bias, uint32_t* ids, uint16_t* gw, uint32_t m, uint32_t k,
+                         uint32_t e, uint32_t topk, int mode, float eps, mh_stream_t stream);
+
 inline int launch_status(const char* what) {
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? MH_OK : hip_error(e, what);

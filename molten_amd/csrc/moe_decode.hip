@@ -64,6 +64,7 @@ struct DenseArgs {
     uint32_t topk;
     int mode;
     float eps;
+    uint32_t route_rows;  // k_dense_rows: also route each token (ids/weights [m, topk])
 };
 
 // Stage x rows [t0, t0 + nt) into LDS as padded f32 chunks, one 32-element
@@ -233,65 +234,89 @@ __global__ __launch_bounds__(kThreads) void k_dense_rows(DenseArgs a) {
     const uint32_t per_wave = (a.n + kWaves - 1) / kWaves;
     const uint32_t e_begin = wave * per_wave;
     const uint32_t e_end = min(a.n, e_begin + per_wave);
-    if (e_begin >= e_end) {
-        return;
-    }
-    float xr[kRowTokens][32];
-#pragma unroll
-    for (int t = 0; t < kRowTokens; ++t) {
-        const uint32_t tok = min(t0 + t, a.m - 1u);
-        float xs;
-        mh::load_x_chunk(a.x + static_cast<size_t>(tok) * a.k + 32u * c, xr[t], xs);
-    }
-    const WT* w = static_cast<const WT*>(a.w) + 32u * c;
     float out[kMaxExpertGroups][kRowTokens];
 #pragma unroll
     for (int g = 0; g < kMaxExpertGroups; ++g)
 #pragma unroll
         for (int t = 0; t < kRowTokens; ++t) out[g][t] = 0.0f;
-    RowWords<WT> cur, nxt;
-    cur.load(w + static_cast<size_t>(e_begin) * a.k);
-    for (uint32_t e = e_begin; e < e_end; ++e) {
-        if (e + 1 < e_end) {
-            nxt.load(w + static_cast<size_t>(e + 1) * a.k);
-        }
-        float wr[32];
-        cur.to_f32(wr);
-        float h[kRowTokens];
+    if (e_begin < e_end) {
+        float xr[kRowTokens][32];
 #pragma unroll
         for (int t = 0; t < kRowTokens; ++t) {
-            float p = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                p = __builtin_fmaf(wr[i], xr[t][i], p);
+            const uint32_t tok = min(t0 + t, a.m - 1u);
+            float xs;
+            mh::load_x_chunk(a.x + static_cast<size_t>(tok) * a.k + 32u * c, xr[t], xs);
+        }
+        const WT* w = static_cast<const WT*>(a.w) + 32u * c;
+        RowWords<WT> cur, nxt;
+        cur.load(w + static_cast<size_t>(e_begin) * a.k);
+        for (uint32_t e = e_begin; e < e_end; ++e) {
+            if (e + 1 < e_end) {
+                nxt.load(w + static_cast<size_t>(e + 1) * a.k);
             }
-            h[t] = live ? 0.0f + p : 0.0f;
+            float wr[32];
+            cur.to_f32(wr);
+            float h[kRowTokens];
+#pragma unroll
+            for (int t = 0; t < kRowTokens; ++t) {
+                float p = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    p = __builtin_fmaf(wr[i], xr[t][i], p);
+                }
+                h[t] = live ? 0.0f + p : 0.0f;
+            }
+            const float v = mh::reduce_rows4(h, lane);
+            const uint32_t g = e >> 6, le = e & 63u;
+#pragma unroll
+            for (int t = 0; t < kRowTokens; ++t) {
+                const float vt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 60 + t));
+#pragma unroll
+                for (int gg = 0; gg < kMaxExpertGroups; ++gg) {
+                    if (gg == static_cast<int>(g) && static_cast<uint32_t>(lane) == le) {
+                        out[gg][t] = vt;
+                    }
+                }
+            }
+            cur = nxt;
         }
-        const float v = mh::reduce_rows4(h, lane);
-        const uint32_t g = e >> 6, le = e & 63u;
 #pragma unroll
         for (int t = 0; t < kRowTokens; ++t) {
-            const float vt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 60 + t));
+            if (t0 + t < a.m) {
 #pragma unroll
-            for (int gg = 0; gg < kMaxExpertGroups; ++gg) {
-                if (gg == static_cast<int>(g) && static_cast<uint32_t>(lane) == le) {
-                    out[gg][t] = vt;
+                for (int g = 0; g < kMaxExpertGroups; ++g) {
+                    const uint32_t e = g * 64u + lane;
+                    if (e >= e_begin && e < e_end) {
+                        a.y[static_cast<size_t>(t0 + t) * a.n + e] = out[g][t];
+                    }
                 }
             }
         }
-        cur = nxt;
     }
+    if (!a.route_rows) {
+        return;
+    }
+    // routing of the workgroup's tokens: logits through LDS, one wave per token
+    __shared__ float zl[kRowTokens][mh::kMaxExperts];
+    __shared__ float ss[kRowTokens][mh::kMaxExperts], cc[kRowTokens][mh::kMaxExperts];
 #pragma unroll
-    for (int t = 0; t < kRowTokens; ++t) {
-        if (t0 + t < a.m) {
+    for (int t = 0; t < kRowTokens; ++t)
 #pragma unroll
-            for (int g = 0; g < kMaxExpertGroups; ++g) {
-                const uint32_t e = g * 64u + lane;
-                if (e >= e_begin && e < e_end) {
-                    a.y[static_cast<size_t>(t0 + t) * a.n + e] = out[g][t];
-                }
+        for (int g = 0; g < kMaxExpertGroups; ++g) {
+            const uint32_t e = g * 64u + lane;
+            if (e >= e_begin && e < e_end) {
+                zl[t][e] = out[g][t];
             }
         }
+    __syncthreads();
+    const uint32_t t = static_cast<uint32_t>(wave);
+    if (t < static_cast<uint32_t>(kRowTokens) && t0 + t < a.m) {
+        for (uint32_t i = lane; i < a.n; i += 64) {
+            mh::route_score(zl[t][i], a.bias ? a.bias[i] : 0.0f, a.mode, ss[t][i], cc[t][i]);
+        }
+        mh::route_select(ss[t], cc[t], a.n, a.topk, a.mode, a.eps,
+                         a.ids + static_cast<size_t>(t0 + t) * a.topk,
+                         a.weights + static_cast<size_t>(t0 + t) * a.topk);
     }
 }
 
@@ -671,6 +696,45 @@ int mh_route_token(const float* logits, const float* bias, uint32_t* ids, uint16
                        weights, e, topk, mode, eps);
     return mh::launch_status("mh_route_token");
 }
+
+}  // extern "C"
+
+namespace mh {
+
+// Prefill router and routing in one launch (mh_moe_prefill's first step).
+int router_prefill_route(const uint16_t* x, const void* w, int w_dtype, float* logits,
+                         const float* bias, uint32_t* ids, uint16_t* gw, uint32_t m, uint32_t k,
+                         uint32_t e, uint32_t topk, int mode, float eps, mh_stream_t stream) {
+    const char* op = "mh_moe_prefill (router)";
+    MH_ENSURE(w_dtype == MH_DTYPE_F32 || w_dtype == MH_DTYPE_BF16, MH_ERR_INVALID,
+              "%s: router dtype %d", op, w_dtype);
+    MH_TRY(route_checks(op, logits, ids, gw, m, e, topk, mode));
+    DenseArgs a;
+    MH_TRY(dense_common(op, w, w_dtype == MH_DTYPE_F32, x, logits, m, e, k, a));
+    if (k > 2048u) {  // the register-resident rows kernel needs one chunk per lane
+        MH_TRY(w_dtype == MH_DTYPE_F32 ? dispatch_dense<float>(a, mh::as_stream(stream))
+                                       : dispatch_dense<uint16_t>(a, mh::as_stream(stream)));
+        return mh_moe_route_batch(logits, bias, ids, gw, m, e, topk, mode, eps, stream);
+    }
+    a.bias = bias;
+    a.ids = ids;
+    a.weights = gw;
+    a.topk = topk;
+    a.mode = mode;
+    a.eps = eps;
+    a.route_rows = 1u;
+    const dim3 grid((m + kRowTokens - 1) / kRowTokens);
+    if (w_dtype == MH_DTYPE_F32) {
+        hipLaunchKernelGGL(k_dense_rows<float>, grid, dim3(kThreads), 0, mh::as_stream(stream), a);
+    } else {
+        hipLaunchKernelGGL(k_dense_rows<uint16_t>, grid, dim3(kThreads), 0, mh::as_stream(stream), a);
+    }
+    return mh::launch_status("k_dense_rows (routed)");
+}
+
+}  // namespace mh
+
+extern "C" {
 
 int mh_moe_route_batch(const float* logits, const float* bias, uint32_t* ids, uint16_t* gw,
                        uint32_t m, uint32_t e, uint32_t topk, int mode, float eps,

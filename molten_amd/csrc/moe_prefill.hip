@@ -50,47 +50,79 @@ __global__ __launch_bounds__(1024) void k_offsets(const uint32_t* counts, uint32
     if (t < e) offsets[t] = sh[t] - counts[t];
 }
 
-// Stable scatter: one workgroup per expert walks the slots in order, 256 at a
-// time; a slot routed to the expert goes to offsets[e] + (number of earlier
-// slots routed to it), found with a ballot prefix count.
-__global__ __launch_bounds__(256) void k_sorted(const uint32_t* ids, const uint32_t* offsets,
-                                                uint32_t* ids_sorted, uint32_t* slotpos,
-                                                uint32_t s, uint32_t topk) {
-    __shared__ uint32_t wave_tot[4];
-    const uint32_t e = blockIdx.x;
+// Exclusive prefix sum over the workgroup (1024 threads, thread order) of
+// one value per thread; returns this thread's exclusive prefix, *total the
+// workgroup total.  Uses LDS wave totals; ends with a barrier.
+__device__ __forceinline__ uint32_t block_excl_scan_1024(uint32_t v, uint32_t* total) {
+    __shared__ uint32_t wtot[16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    uint32_t base = offsets[e];
-    for (uint32_t t0 = 0; t0 < s; t0 += 256) {
-        const uint32_t i = t0 + threadIdx.x;
-        const bool hit = i < s && ids[i] == e;
-        const unsigned long long m = __ballot(hit);
-        const uint32_t before = __popcll(m & ((1ull << lane) - 1ull));
-        if (lane == 0) wave_tot[wave] = __popcll(m);
-        __syncthreads();
-        uint32_t wbase = 0;
-        for (int w = 0; w < wave; ++w) wbase += wave_tot[w];
-        const uint32_t tile_total = wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
-        if (hit) {
-            const uint32_t pos = base + wbase + before;
-            ids_sorted[pos] = i / topk;
-            slotpos[i] = pos;
+    uint32_t inc = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t o = __shfl_up(inc, d);
+        if (lane >= d) inc += o;
+    }
+    if (lane == 63) wtot[wave] = inc;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+        const uint32_t t = wtot[w];
+        before += w < wave ? t : 0u;
+        all += t;
+    }
+    __syncthreads();
+    *total = all;
+    return before + inc - v;
+}
+
+// Stable scatter of expert e's slots by one 1024-thread workgroup: four
+// consecutive slots per thread per pass (slot order = thread order, then the
+// thread's four), positions from a workgroup prefix count.
+__device__ __forceinline__ void scatter_expert(const uint32_t* ids, uint32_t e, uint32_t base,
+                                               uint32_t* ids_sorted, uint32_t* slotpos, uint32_t s,
+                                               uint32_t topk) {
+    for (uint32_t t0 = 0; t0 < s; t0 += 4096u) {
+        const uint32_t i0 = t0 + 4u * threadIdx.x;
+        uint32_t id[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) id[j] = i0 + j < s ? ids[i0 + j] : 0xffffffffu;
+        uint32_t hit[4], cnt = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            hit[j] = id[j] == e ? 1u : 0u;
+            cnt += hit[j];
         }
-        base += tile_total;
-        __syncthreads();
+        uint32_t total;
+        uint32_t pos = base + block_excl_scan_1024(cnt, &total);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (hit[j]) {
+                ids_sorted[pos] = (i0 + j) / topk;
+                slotpos[i0 + j] = pos;
+                ++pos;
+            }
+        }
+        base += total;
     }
 }
 
-__global__ __launch_bounds__(64) void k_block_offsets(const uint32_t* counts, uint32_t* gu_off,
-                                                      uint32_t* dn_off, uint32_t e, uint32_t bm,
-                                                      uint32_t gu_tiles, uint32_t dn_tiles) {
-    if (threadIdx.x != 0) return;
-    uint32_t ag = 0, ad = 0;
-    for (uint32_t i = 0; i < e; ++i) {
-        gu_off[i] = ag;
-        dn_off[i] = ad;
-        const uint32_t rows = (counts[i] + bm - 1) / bm;
-        ag += rows * gu_tiles;
-        ad += rows * dn_tiles;
+__global__ __launch_bounds__(1024) void k_sorted(const uint32_t* ids, const uint32_t* offsets,
+                                                 uint32_t* ids_sorted, uint32_t* slotpos,
+                                                 uint32_t s, uint32_t topk) {
+    scatter_expert(ids, blockIdx.x, offsets[blockIdx.x], ids_sorted, slotpos, s, topk);
+}
+
+__global__ __launch_bounds__(1024) void k_block_offsets(const uint32_t* counts, uint32_t* gu_off,
+                                                        uint32_t* dn_off, uint32_t e, uint32_t bm,
+                                                        uint32_t gu_tiles, uint32_t dn_tiles) {
+    const uint32_t i = threadIdx.x;
+    const uint32_t rows = i < e ? (counts[i] + bm - 1) / bm : 0u;
+    uint32_t total;
+    const uint32_t before = block_excl_scan_1024(rows, &total);
+    if (i < e) {
+        gu_off[i] = before * gu_tiles;
+        dn_off[i] = before * dn_tiles;
     }
 }
 
@@ -179,6 +211,64 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t* sorted, const u
     }
 }
 
+// Prefill step, routing half 1: counts (LDS histogram of the slots),
+// offsets and both block-map offsets in one 1024-thread workgroup (e <= 1024).
+__global__ __launch_bounds__(1024) void k_count_scan(const uint32_t* ids, uint32_t s, uint32_t e,
+                                                     uint32_t* counts, uint32_t* offsets,
+                                                     uint32_t* gu_off, uint32_t* dn_off,
+                                                     uint32_t bm, uint32_t gu_tiles,
+                                                     uint32_t dn_tiles) {
+    __shared__ uint32_t hist[1024];
+    const uint32_t t = threadIdx.x;
+    hist[t] = 0u;
+    __syncthreads();
+    for (uint32_t i = t; i < s; i += 1024u) {
+        const uint32_t x = ids[i];
+        if (x < e) atomicAdd(&hist[x], 1u);
+    }
+    __syncthreads();
+    const uint32_t c = t < e ? hist[t] : 0u;
+    const uint32_t rows = (c + bm - 1u) / bm;
+    uint32_t total;
+    const uint32_t before = block_excl_scan_1024(c, &total);
+    const uint32_t rbefore = block_excl_scan_1024(rows, &total);
+    if (t < e) {
+        counts[t] = c;
+        offsets[t] = before;
+        gu_off[t] = rbefore * gu_tiles;
+        dn_off[t] = rbefore * dn_tiles;
+    }
+}
+
+// Prefill step, routing half 2: workgroup ex < e scatters expert ex's slots
+// and writes its block-map entries; workgroup e zeroes both maps' unused
+// tails (entries past the last expert's), which the GEMMs skip.
+__global__ __launch_bounds__(1024) void k_sorted_blocks(const uint32_t* ids, const uint32_t* counts,
+                                                        const uint32_t* offsets, const uint32_t* gu_off,
+                                                        const uint32_t* dn_off, uint32_t* ids_sorted,
+                                                        uint32_t* slotpos, uint32_t s, uint32_t topk,
+                                                        uint32_t e, uint4* gu, uint32_t max_gu,
+                                                        uint4* dn, uint32_t max_dn, uint32_t bm,
+                                                        uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n,
+                                                        uint32_t dn_n) {
+    const uint32_t ex = blockIdx.x;
+    if (ex == e) {
+        const uint32_t rows = (counts[e - 1] + bm - 1) / bm;
+        const uint32_t gu_end = gu_off[e - 1] + rows * (gu_n / gu_bn);
+        const uint32_t dn_end = dn_off[e - 1] + rows * (dn_n / dn_bn);
+        for (uint32_t i = gu_end + threadIdx.x; i < max_gu; i += blockDim.x) gu[i] = make_uint4(0, 0, 0, 0);
+        for (uint32_t i = dn_end + threadIdx.x; i < max_dn; i += blockDim.x) dn[i] = make_uint4(0, 0, 0, 0);
+        return;
+    }
+    const uint32_t n = counts[ex];
+    if (n == 0) {
+        return;
+    }
+    write_map(gu, max_gu, gu_off[ex], n, offsets[ex], ex, bm, gu_bn, gu_n);
+    write_map(dn, max_dn, dn_off[ex], n, offsets[ex], ex, bm, dn_bn, dn_n);
+    scatter_expert(ids, ex, offsets[ex], ids_sorted, slotpos, s, topk);
+}
+
 unsigned grid_for(size_t n, unsigned per = 256) {
     const size_t want = (n + per - 1) / per;
     const size_t cap = static_cast<size_t>(mh::cu_count()) * 16;
@@ -218,7 +308,7 @@ int mh_moe_sorted(const uint32_t* ids, const uint32_t* offsets, uint32_t* ids_so
     MH_ENSURE(ids && offsets && ids_sorted && slotpos, MH_ERR_INVALID, "mh_moe_sorted: NULL argument");
     MH_ENSURE(e >= 1 && topk >= 1, MH_ERR_INVALID, "mh_moe_sorted: e=%u topk=%u", e, topk);
     if (m == 0) return MH_OK;
-    hipLaunchKernelGGL(k_sorted, dim3(e), dim3(256), 0, mh::as_stream(stream), ids, offsets,
+    hipLaunchKernelGGL(k_sorted, dim3(e), dim3(1024), 0, mh::as_stream(stream), ids, offsets,
                        ids_sorted, slotpos, m * topk, topk);
     return mh::launch_status("mh_moe_sorted");
 }
@@ -241,7 +331,8 @@ int mh_moe_block_offsets(const uint32_t* counts, uint32_t* gu_off, uint32_t* dn_
     MH_ENSURE(bm > 0 && gu_bn > 0 && dn_bn > 0 && gu_n % gu_bn == 0 && dn_n % dn_bn == 0,
               MH_ERR_INVALID, "mh_moe_block_offsets: tiles bm=%u bn=%u/%u do not divide %u/%u",
               bm, gu_bn, dn_bn, gu_n, dn_n);
-    hipLaunchKernelGGL(k_block_offsets, dim3(1), dim3(64), 0, mh::as_stream(stream), counts, gu_off,
+    MH_ENSURE(e >= 1 && e <= 1024, MH_ERR_UNSUPPORTED, "mh_moe_block_offsets: %u experts", e);
+    hipLaunchKernelGGL(k_block_offsets, dim3(1), dim3(1024), 0, mh::as_stream(stream), counts, gu_off,
                        dn_off, e, bm, gu_n / gu_bn, dn_n / dn_bn);
     return mh::launch_status("mh_moe_block_offsets");
 }
@@ -262,6 +353,32 @@ int mh_moe_blocks(const uint32_t* counts, const uint32_t* offsets, const uint32_
                        reinterpret_cast<uint4*>(dn), max_dn, bm, gu_bn, dn_bn, gu_n, dn_n);
     return mh::launch_status("mh_moe_blocks");
 }
+
+}  // extern "C"
+
+namespace mh {
+
+// Internal to mh_moe_prefill (declared in mh_host.hpp, not in the public
+// header): the two fused routing launches above.
+int moe_sort_maps(const uint32_t* ids, uint32_t s, uint32_t e, uint32_t topk,
+                              uint32_t* counts, uint32_t* offsets, uint32_t* gu_off,
+                              uint32_t* dn_off, uint32_t* ids_sorted, uint32_t* slotpos,
+                              uint32_t* gu, uint32_t max_gu, uint32_t* dn, uint32_t max_dn,
+                              uint32_t bm, uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n,
+                              uint32_t dn_n, mh_stream_t stream) {
+    const hipStream_t st = mh::as_stream(stream);
+    hipLaunchKernelGGL(k_count_scan, dim3(1), dim3(1024), 0, st, ids, s, e, counts, offsets, gu_off,
+                       dn_off, bm, gu_n / gu_bn, dn_n / dn_bn);
+    MH_TRY(mh::launch_status("k_count_scan"));
+    hipLaunchKernelGGL(k_sorted_blocks, dim3(e + 1), dim3(1024), 0, st, ids, counts, offsets, gu_off,
+                       dn_off, ids_sorted, slotpos, s, topk, e, reinterpret_cast<uint4*>(gu), max_gu,
+                       reinterpret_cast<uint4*>(dn), max_dn, bm, gu_bn, dn_bn, gu_n, dn_n);
+    return mh::launch_status("k_sorted_blocks");
+}
+
+}  // namespace mh
+
+extern "C" {
 
 int mh_gather_rows_bf16(const uint16_t* table, const uint32_t* ids, uint16_t* out, uint32_t m,
                         uint32_t h, uint32_t n_table, mh_stream_t stream) {

@@ -1,10 +1,11 @@
 // moe_prefill_step.hip -- the whole prefill MoE block in one call
 // (src/lfm.rs:847-965 moe_prefill), on a caller-provided workspace.
 //
-// Sequence: router logits -> per-token top-k -> counting sort (counts,
-// offsets, stable scatter) -> block maps -> grouped gate/up GEMM with the
-// ids_sorted row gather and the SwiGLU epilogue fused -> grouped down GEMM ->
-// weighted combine.  Compared with the reference's sequence this drops the
+// Sequence (five launches and the combine): router logits with the per-token
+// top-k fused -> counts, offsets and block-map offsets in one workgroup ->
+// per-expert stable scatter with that expert's block-map entries -> grouped
+// gate/up GEMM with the ids_sorted row gather and the SwiGLU epilogue fused ->
+// grouped down GEMM -> weighted combine.  Compared with the reference's sequence this drops the
 // materialised gathered rows and the separate gate/up outputs (two 4-byte
 // round trips per routed element); the values are the same.
 #include "mh_device.hpp"
@@ -115,17 +116,11 @@ int mh_moe_prefill(const void* router, int router_dtype, const float* bias, int 
     uint16_t* ed = reinterpret_cast<uint16_t*>(at(MH_PREFILL_WS_ED));
     const uint32_t s = m * topk;
 
-    MH_TRY(mh_router_prefill(x, router, router_dtype, logits, m, d_model, n_experts, stream));
-    MH_TRY(mh_moe_route_batch(logits, bias, ids, gw, m, n_experts, topk, mode, eps, stream));
-    MH_TRY(mh_moe_zero_counts(counts, n_experts, stream));
-    MH_TRY(mh_moe_count_slots(ids, counts, s, n_experts, stream));
-    MH_TRY(mh_moe_offsets(counts, offsets, n_experts, stream));
-    MH_TRY(mh_moe_sorted(ids, offsets, ids_sorted, slotpos, m, n_experts, topk, stream));
-    MH_TRY(mh_moe_zero_blocks(gu_map, dn_map, l.max_gu, l.max_dn, stream));
-    MH_TRY(mh_moe_block_offsets(counts, gu_off, dn_off, n_experts, kBM, kGuBN, kDnBN, n_inter,
-                                d_model, stream));
-    MH_TRY(mh_moe_blocks(counts, offsets, gu_off, dn_off, gu_map, l.max_gu, dn_map, l.max_dn,
-                         n_experts, kBM, kGuBN, kDnBN, n_inter, d_model, stream));
+    MH_TRY(mh::router_prefill_route(x, router, router_dtype, logits, bias, ids, gw, m, d_model,
+                                    n_experts, topk, mode, eps, stream));
+    MH_TRY(mh::moe_sort_maps(ids, s, n_experts, topk, counts, offsets, gu_off, dn_off, ids_sorted,
+                             slotpos, gu_map, l.max_gu, dn_map, l.max_dn, kBM, kGuBN, kDnBN,
+                             n_inter, d_model, stream));
     MH_TRY(mh_gemm_q4_grouped_gu_act(x, ids_sorted, m, gate, up, act, gu_map, l.max_gu, s, n_inter,
                                      kBM, kGuBN, stream));
     MH_TRY(mh_gemm_q4_grouped(act, down, ed, dn_map, l.max_dn, s, d_model, kBM, kDnBN, stream));
