@@ -162,39 +162,15 @@ __device__ void finish_argmax(const GemvArgs& a, const float (&bv)[B], const uin
     collect_keys<B>(a, last, own);
 }
 
-// Wave max / min with the DPP tree of wave_sum_lane63 (valid in lane 63).
-__device__ __forceinline__ float wave_max_f32(float v) {
-    v = fmaxf(v, mh::dpp_move<0x111, 0xf>(v));
-    v = fmaxf(v, mh::dpp_move<0x112, 0xf>(v));
-    v = fmaxf(v, mh::dpp_move<0x114, 0xf>(v));
-    v = fmaxf(v, mh::dpp_move<0x118, 0xf>(v));
-    v = fmaxf(v, mh::dpp_move<0x142, 0xa>(v));
-    v = fmaxf(v, mh::dpp_move<0x143, 0xc>(v));
-    return mh::lane63(v);
-}
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(-1, static_cast<int>(v), CTRL, ROW_MASK, 0xf, false));
-}
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-    v = min(v, dpp_u32<0x111, 0xf>(v));
-    v = min(v, dpp_u32<0x112, 0xf>(v));
-    v = min(v, dpp_u32<0x114, 0xf>(v));
-    v = min(v, dpp_u32<0x118, 0xf>(v));
-    v = min(v, dpp_u32<0x142, 0xa>(v));
-    v = min(v, dpp_u32<0x143, 0xc>(v));
-    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
-}
-
 // Key of the wave's argmax over per-lane bests (bv, bi) kept by argmax_merge:
 // the greatest value (NaN never wins, -0 == +0), ties to the lowest index;
 // with no non-NaN candidate the serial scan's (-inf, 0).
 __device__ __forceinline__ unsigned long long wave_argmax_key(float bv, uint32_t bi) {
-    const float m = wave_max_f32(bv);
+    const float m = mh::wave_max_f32(bv);
     if (m != m) {
         return mh::argmax_key(-__builtin_inff(), 0u);
     }
-    const uint32_t i = wave_min_u32(bv == m ? bi : 0xffffffffu);
+    const uint32_t i = mh::wave_min_u32(bv == m ? bi : 0xffffffffu);
     return mh::argmax_key(m, i);
 }
 

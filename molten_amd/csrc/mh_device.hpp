@@ -185,6 +185,30 @@ __device__ __forceinline__ float lane63(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Wave max / min with the DPP tree of wave_sum_lane63 (valid in lane 63).
+__device__ __forceinline__ float wave_max_f32(float v) {
+    v = fmaxf(v, dpp_move<0x111, 0xf>(v));
+    v = fmaxf(v, dpp_move<0x112, 0xf>(v));
+    v = fmaxf(v, dpp_move<0x114, 0xf>(v));
+    v = fmaxf(v, dpp_move<0x118, 0xf>(v));
+    v = fmaxf(v, dpp_move<0x142, 0xa>(v));
+    v = fmaxf(v, dpp_move<0x143, 0xc>(v));
+    return lane63(v);
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(-1, static_cast<int>(v), CTRL, ROW_MASK, 0xf, false));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    v = min(v, dpp_u32<0x111, 0xf>(v));
+    v = min(v, dpp_u32<0x112, 0xf>(v));
+    v = min(v, dpp_u32<0x114, 0xf>(v));
+    v = min(v, dpp_u32<0x118, 0xf>(v));
+    v = min(v, dpp_u32<0x142, 0xa>(v));
+    v = min(v, dpp_u32<0x143, 0xc>(v));
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
 // ------------------------------------------------------------ argmax key ---
 // "value desc, index asc" as one orderable u64 (lfm.metal:1119-1124):
 // -0 ties +0, NaN candidates are never produced by the merge below.

@@ -31,12 +31,14 @@ __device__ __forceinline__ void route_score(float z, float bias, int mode, float
 
 // Selection over LDS-resident scores by one full wave.  For each slot every
 // lane takes the best eligible candidate among its experts (lane, lane + 64,
-// ...), then the wave reduces with the same rule.  "value desc, id asc" is a
-// strict total order on eligible candidates (ids are distinct), so the winner
-// does not depend on the reduction order and equals the serial scan's: that
-// scan starts from (-inf, id 0) and only replaces on v > best or (v == best and
-// a lower id), so used experts, NaN and -inf never win, and with no eligible
-// candidate it returns expert 0.  Lane 0 writes ids and weights.
+// ...), then the wave reduces with the same rule in two DPP passes: the
+// greatest candidate value, then the lowest id among the lanes holding it.
+// "value desc, id asc" is a strict total order on eligible candidates (ids
+// are distinct), so the winner does not depend on the reduction order and
+// equals the serial scan's: that scan starts from (-inf, id 0) and only
+// replaces on v > best or (v == best and a lower id), so used experts, NaN
+// and -inf never win, and with no eligible candidate it returns expert 0.
+// Lane 0 writes ids and weights.
 __device__ inline void route_select(const float* s, const float* cand, uint32_t e, uint32_t topk,
                                     int mode, float eps, uint32_t* ids_out, uint16_t* w_out) {
     const uint32_t lane = threadIdx.x & 63u;
@@ -57,14 +59,13 @@ __device__ inline void route_select(const float* s, const float* cand, uint32_t 
                 }
             }
         }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const uint32_t oi = __shfl_xor(bi, off);
-            if (oi != 0xffffffffu && (bi == 0xffffffffu || ov > bv || (ov == bv && oi < bi))) {
-                bv = ov;
-                bi = oi;
-            }
+        // lanes with no eligible candidate hold (-inf, none): they lose to
+        // any eligible value and are ignored when the best value is -inf
+        const float m = wave_max_f32(bv);
+        if (m > -__builtin_inff()) {
+            bi = wave_min_u32(bv == m ? bi : 0xffffffffu);
+        } else {
+            bi = 0xffffffffu;
         }
         const uint32_t pick = bi == 0xffffffffu ? 0u : bi;
         chosen[r] = pick;

@@ -320,6 +320,44 @@ __global__ __launch_bounds__(kThreads) void k_dense_rows(DenseArgs a) {
     }
 }
 
+// Decode router logits only (the routing runs in the expert kernel): one
+// wave per 4 experts, x in registers, the four rows reduced together.
+template <typename WT>
+__global__ __launch_bounds__(64) void k_router_logits(DenseArgs a) {
+    const int lane = threadIdx.x;
+    const uint32_t C = a.k / 32u;
+    const bool live = lane < static_cast<int>(C);
+    const uint32_t c = live ? lane : 0u;
+    const uint32_t e0 = blockIdx.x * 4u;
+    uint32_t xw[16];
+    mh::load_x_words(a.x + 32u * c, xw);
+    const WT* w = static_cast<const WT*>(a.w) + 32u * c;
+    RowWords<WT> rw[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        rw[r].load(w + static_cast<size_t>(min(e0 + r, a.n - 1u)) * a.k);
+    }
+    mh::x_words_fence(xw);
+    float xr[32], xs;
+    mh::x_words_to_f32(xw, xr, xs);
+    float h[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        float wr[32];
+        rw[r].to_f32(wr);
+        float p = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            p = __builtin_fmaf(wr[i], xr[i], p);
+        }
+        h[r] = live ? 0.0f + p : 0.0f;
+    }
+    const float v = mh::reduce_rows4(h, lane);
+    if (lane >= 60 && e0 + (lane - 60) < a.n) {
+        a.y[e0 + (lane - 60)] = v;
+    }
+}
+
 template <typename WT, int TT, int EPW>
 int launch_dense(const DenseArgs& a, hipStream_t stream) {
     const uint32_t C = a.k / 32u;
@@ -409,6 +447,14 @@ struct ActArgs {
     const uint32_t* ids;  // [slots] or null (dense)
     uint16_t* act;        // [slots, n_inter]
     uint32_t slots, n_inter, n_experts, k, gs, row_words, groups;
+    // in-kernel routing (decode step): when logits != null every workgroup
+    // routes the token itself from the logits, and workgroup 0 stores the
+    // ids and weights for the down kernel (ids above is then the output)
+    const float* logits;
+    const float* bias;
+    uint16_t* weights;
+    int mode;
+    float eps;
 };
 
 struct ActLoad {
@@ -497,7 +543,111 @@ __global__ __launch_bounds__(kThreads) void k_gather_act(ActArgs a) {
     gather_act_rows<R>(a, xr, xs, lane, wave, live);
 }
 
+// Block form of the expert gate/up + SwiGLU (K <= 2048 and n_inter a
+// multiple of 4): each wave owns 4 consecutive rows j of one slot, i.e. 4
+// consecutive rows of expert ids[slot] in both matrices.  The 8 rows' codes
+// are loaded at once (non-temporal), their scales and biases staged in LDS as
+// (scale | bias << 16) words, each matrix's 4 row values reduced with the
+// 4-row butterfly, and lanes 0..3 apply SwiGLU and store 4 consecutive
+// activations.  Chunk order as in k_gather_act.
+constexpr int kActBlock = 4;
+constexpr int kMaxG = 64;  // groups per row (K / group size) staged in LDS
+
+__device__ __forceinline__ void stage_sb_words(uint32_t* sb, const uint16_t* scales,
+                                               const uint16_t* biases, uint32_t elems, int lane) {
+    // elems bf16 of scales and of biases, contiguous; even G keeps them dword aligned
+    const uint32_t* s2 = reinterpret_cast<const uint32_t*>(scales);
+    const uint32_t* b2 = reinterpret_cast<const uint32_t*>(biases);
+    for (uint32_t i = lane; i < elems / 2u; i += 64u) {
+        const uint32_t sw = s2[i], bw = b2[i];
+        *reinterpret_cast<uint2*>(sb + 2u * i) =
+            make_uint2(__builtin_amdgcn_perm(bw, sw, 0x05040100u), __builtin_amdgcn_perm(bw, sw, 0x07060302u));
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_act_blocks(ActArgs a) {
+    constexpr int R = kActBlock;  // rows per matrix per wave (one 4-row butterfly each)
+    __shared__ uint32_t sbl[kWaves][2][R * kMaxG];
+    __shared__ float rs[mh::kMaxExperts], rc[mh::kMaxExperts];
+    __shared__ uint32_t rids[mh::kMaxTopk];
+    __shared__ uint16_t rw[mh::kMaxTopk];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t C = a.k / 32u;
+    const bool live = lane < static_cast<int>(C);
+    const uint32_t c = live ? lane : 0u;
+    const uint32_t G = a.groups;
+    uint32_t xw[16];
+    mh::load_x_words(a.x + 32u * c, xw);
+    if (a.logits != nullptr) {
+        if (wave == 0) {
+            for (uint32_t i = lane; i < a.n_experts; i += 64) {
+                mh::route_score(a.logits[i], a.bias ? a.bias[i] : 0.0f, a.mode, rs[i], rc[i]);
+            }
+            mh::route_select(rs, rc, a.n_experts, a.slots, a.mode, a.eps, rids, rw);
+            if (blockIdx.x == 0 && lane < static_cast<int>(a.slots)) {
+                const_cast<uint32_t*>(a.ids)[lane] = rids[lane];
+                a.weights[lane] = rw[lane];
+            }
+        }
+        __syncthreads();
+    }
+    const uint32_t blk = blockIdx.x * kWaves + wave;
+    const uint32_t v0 = blk * R;
+    if (v0 >= a.slots * a.n_inter) {
+        return;
+    }
+    const uint32_t slot = v0 / a.n_inter, j0 = v0 % a.n_inter;
+    uint32_t e = a.logits != nullptr ? rids[slot] : (a.ids ? a.ids[slot] : 0u);
+    e = e < a.n_experts ? e : 0u;  // an out-of-range id reads expert 0, never past W
+    const uint32_t row0 = e * a.n_inter + j0;
+    const uint32_t row_bytes = a.row_words * 4u;
+    const mh::gbytes gbase = mh::uniform_ptr(reinterpret_cast<const char*>(a.gc) + static_cast<size_t>(row0) * row_bytes);
+    const mh::gbytes ubase = mh::uniform_ptr(reinterpret_cast<const char*>(a.uc) + static_cast<size_t>(row0) * row_bytes);
+    const uint32_t code_off = c * 16u;
+    mh::Chunk<4> ch[2][R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        ch[0][r].load_nt(gbase, r * row_bytes + code_off);
+        ch[1][r].load_nt(ubase, r * row_bytes + code_off);
+    }
+    stage_sb_words(sbl[wave][0], a.gsc + static_cast<size_t>(row0) * G, a.gbi + static_cast<size_t>(row0) * G,
+                   R * G, lane);
+    stage_sb_words(sbl[wave][1], a.usc + static_cast<size_t>(row0) * G, a.ubi + static_cast<size_t>(row0) * G,
+                   R * G, lane);
+    mh::x_words_fence(xw);
+    float xr[32], xs;
+    mh::x_words_to_f32(xw, xr, xs);
+    mh::q4_scale_x(xr);
+    const uint32_t gc = (32u * c) / a.gs;
+    float yv[2];
+#pragma unroll
+    for (int mat = 0; mat < 2; ++mat) {
+        float h[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t w = sbl[wave][mat][r * G + gc];
+            const float p = ch[mat][r].dot(xr);
+            const float hv = __builtin_fmaf(__uint_as_float(w << 16), p, __uint_as_float(w & 0xffff0000u) * xs);
+            h[r] = live ? 0.0f + hv : 0.0f;
+        }
+        const float v = mh::reduce_rows4(h, lane);
+        yv[mat] = __int_as_float(__builtin_amdgcn_ds_bpermute((60 + (lane & 3)) * 4, __float_as_int(v)));
+    }
+    if (lane < R) {
+        const float g = mh::round_bf16(yv[0]);
+        const float u = mh::round_bf16(yv[1]);
+        a.act[v0 + lane] = mh::f32_to_bf16(mh::silu_bf16(g) * u);
+    }
+}
+
 int launch_gather_act(const ActArgs& a, hipStream_t stream) {
+    if (a.n_inter % kActBlock == 0 && a.groups % 2 == 0 && a.groups <= static_cast<uint32_t>(kMaxG) &&
+        a.gs % 32 == 0) {
+        const uint32_t blocks = a.slots * a.n_inter / kActBlock;
+        hipLaunchKernelGGL(k_act_blocks, dim3((blocks + kWaves - 1) / kWaves), dim3(kThreads), 0, stream, a);
+        return mh::launch_status("k_act_blocks");
+    }
     constexpr int R = 2;
     const uint32_t n_rg = (a.slots * a.n_inter + R - 1) / R;
     const uint32_t want = (n_rg + kWaves - 1) / kWaves;
@@ -620,7 +770,99 @@ __global__ __launch_bounds__(kThreads) void k_down_combine(DownArgs a) {
     down_rows<TK>(a, xr, xs, e, wt, lane, wave, live);
 }
 
+// Block form of the expert down + combine (K <= 2048, topk <= 4, n_out
+// even): each wave owns 2 consecutive outputs i; the activation rows of the
+// topk slots are in registers (lane c holds chunk c of each), output i's
+// topk row values are reduced together in one 4-row butterfly (slot r as row
+// r), and the combine bf16(sum_r bf16(w_r * bf16(v_r))) runs on the reduced
+// values.  Chunk order as in k_down_combine.
+constexpr int kDownOut = 2;
+
+template <int TK>
+__global__ __launch_bounds__(kThreads) void k_down_blocks(DownArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t C = a.k / 32u;
+    const bool live = lane < static_cast<int>(C);
+    const uint32_t c = live ? lane : 0u;
+    const uint32_t G = a.groups;
+    const uint32_t i0 = (blockIdx.x * kWaves + wave) * kDownOut;
+    if (i0 >= a.n_out) {
+        return;
+    }
+    uint32_t e[TK];
+    float wt[TK];
+#pragma unroll
+    for (int r = 0; r < TK; ++r) {
+        const uint32_t id = a.ids[r];
+        e[r] = id < a.n_experts ? id : 0u;
+        wt[r] = mh::bf16_to_f32(a.weights[r]);
+    }
+    uint32_t xw[TK][16];
+#pragma unroll
+    for (int r = 0; r < TK; ++r) {
+        mh::load_x_words(a.act + static_cast<size_t>(r) * a.k + 32u * c, xw[r]);
+    }
+    const uint32_t row_bytes = a.row_words * 4u;
+    const uint32_t code_off = c * 16u;
+    const uint32_t gc = (32u * c) / a.gs;
+    mh::Chunk<4> ch[kDownOut][TK];
+    uint16_t sr[kDownOut][TK], br[kDownOut][TK];
+#pragma unroll
+    for (int o = 0; o < kDownOut; ++o) {
+#pragma unroll
+        for (int r = 0; r < TK; ++r) {
+            const size_t row = static_cast<size_t>(e[r]) * a.n_out + i0 + o;
+            ch[o][r].load_nt(mh::uniform_ptr(reinterpret_cast<const char*>(a.codes) + row * row_bytes), code_off);
+            sr[o][r] = a.scales[row * G + gc];
+            br[o][r] = a.biases[row * G + gc];
+        }
+    }
+    float xr[TK][32], xs[TK];
+#pragma unroll
+    for (int r = 0; r < TK; ++r) {
+        mh::x_words_fence(xw[r]);
+        mh::x_words_to_f32(xw[r], xr[r], xs[r]);
+        mh::q4_scale_x(xr[r]);
+    }
+    float yv = 0.0f;
+#pragma unroll
+    for (int o = 0; o < kDownOut; ++o) {
+        float h[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int r = 0; r < TK; ++r) {
+            const float p = ch[o][r].dot(xr[r]);
+            const float hv = __builtin_fmaf(mh::bf16_to_f32(sr[o][r]), p, mh::bf16_to_f32(br[o][r]) * xs[r]);
+            h[r] = live ? 0.0f + hv : 0.0f;
+        }
+        const float v = mh::reduce_rows4(h, lane);
+        float total = 0.0f;
+#pragma unroll
+        for (int r = 0; r < TK; ++r) {
+            const float vr = mh::round_bf16(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 60 + r)));
+            total = total + mh::round_bf16(wt[r] * vr);
+        }
+        if (lane == o) {
+            yv = total;
+        }
+    }
+    if (lane < kDownOut && i0 + lane < a.n_out) {
+        a.out[i0 + lane] = mh::f32_to_bf16(yv);
+    }
+}
+
 int launch_down(const DownArgs& a, uint32_t topk, hipStream_t stream) {
+    if (a.n_out % kDownOut == 0 && a.gs % 32 == 0) {
+        const dim3 grid((a.n_out / kDownOut + kWaves - 1) / kWaves);
+        switch (topk) {
+            case 1: hipLaunchKernelGGL(k_down_blocks<1>, grid, dim3(kThreads), 0, stream, a); break;
+            case 2: hipLaunchKernelGGL(k_down_blocks<2>, grid, dim3(kThreads), 0, stream, a); break;
+            case 3: hipLaunchKernelGGL(k_down_blocks<3>, grid, dim3(kThreads), 0, stream, a); break;
+            case 4: hipLaunchKernelGGL(k_down_blocks<4>, grid, dim3(kThreads), 0, stream, a); break;
+            default: return mh::set_error(MH_ERR_UNSUPPORTED, "down combine: topk %u not in 1..4", topk);
+        }
+        return mh::launch_status("k_down_blocks");
+    }
     const uint32_t want = (a.n_out + kWaves - 1) / kWaves;
     const uint32_t cap = static_cast<uint32_t>(mh::cu_count()) * 4u;
     const dim3 grid(want < cap ? want : cap);
@@ -817,6 +1059,25 @@ int mh_moe_decode(const void* router, int router_dtype, const float* bias, int m
     MH_TRY(act_common(op, gate, up, x, ids, act, topk, n_inter, aa));
     DownArgs da;
     MH_TRY(down_common(op, down, act, ids, weights, out, topk, d_model, da));
+    const hipStream_t s = mh::as_stream(stream);
+    if (d_model <= 2048u && n_inter % kActBlock == 0 && aa.groups % 2 == 0 &&
+        aa.groups <= static_cast<uint32_t>(kMaxG) && d_model % kDownOut == 0) {
+        // logits -> (routing inside every expert workgroup) -> down + combine
+        const dim3 rg((n_experts + 3) / 4);
+        if (router_dtype == MH_DTYPE_F32) {
+            hipLaunchKernelGGL(k_router_logits<float>, rg, dim3(64), 0, s, ra);
+        } else {
+            hipLaunchKernelGGL(k_router_logits<uint16_t>, rg, dim3(64), 0, s, ra);
+        }
+        MH_TRY(mh::launch_status("k_router_logits"));
+        aa.logits = logits;
+        aa.bias = bias;
+        aa.weights = weights;
+        aa.mode = mode;
+        aa.eps = eps;
+        MH_TRY(launch_gather_act(aa, s));
+        return launch_down(da, topk, s);
+    }
     ra.bias = bias;
     ra.ids = ids;
     ra.weights = weights;
@@ -824,7 +1085,6 @@ int mh_moe_decode(const void* router, int router_dtype, const float* bias, int m
     ra.topk = topk;
     ra.mode = mode;
     ra.eps = eps;
-    const hipStream_t s = mh::as_stream(stream);
     const int rc = router_dtype == MH_DTYPE_F32 ? launch_dense<float, 1, 1>(ra, s)
                                                 : launch_dense<uint16_t, 1, 1>(ra, s);
     MH_TRY(rc);
