@@ -141,12 +141,12 @@ def bench_config3(torch, hip, dev, gen, steps, warmup):
     ids = torch.empty(topk, dtype=torch.int32, device=dev)
     wt = torch.empty(topk, dtype=torch.int16, device=dev)
     act = torch.empty((topk, I), dtype=torch.int16, device=dev)
-    counter = torch.zeros(1, dtype=torch.int32, device=dev)
+    scratch = torch.zeros(hip.MOE_DECODE_SCRATCH_WORDS, dtype=torch.int32, device=dev)
 
     def step(i):
         g, u, d, r = sets[i % len(sets)]
         hip.moe_decode(r, None, g[0], u[0], d[0], E, topk, xs[i % len(xs)], out, logits, ids, wt,
-                       act, counter, mode=hip.ROUTE_SOFTMAX)
+                       act, scratch, mode=hip.ROUTE_SOFTMAX)
 
     ms = timed(torch, step, steps, warmup)
     del sets

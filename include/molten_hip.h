@@ -190,12 +190,20 @@ int mh_gemv_gather_down_combine(const mh_quant_weights* down, const uint16_t* ac
  * :266): router GEMV + top-k -> gate/up + SwiGLU -> down + combine.
  * Stacked experts: gate/up [E*n_inter, d_model], down [E*d_model, n_inter].
  * logits f32 [E], ids [topk], weights bf16 [topk], act bf16 [topk, n_inter]
- * are written as intermediates; counter: one u32, zero on entry, left zero. */
+ * are written as intermediates.  scratch: MH_MOE_DECODE_SCRATCH_WORDS u32,
+ * 8-byte aligned, zeroed once before the first call and then owned by this
+ * function (it keeps the words consistent from call to call; no other use,
+ * and calls sharing one scratch must not overlap).  Runs as one launch
+ * (workgroups exchange logits and activations through the scratch, every
+ * workgroup resident) when d_model <= 2048, n_inter % 64 == 0, topk <= 4,
+ * topk * n_inter <= 8192, the router is 16-byte and act 4-byte aligned and
+ * the device has >= 256 CUs; otherwise as three launches. */
+#define MH_MOE_DECODE_SCRATCH_WORDS 10240u
 int mh_moe_decode(const void* router, int router_dtype, const float* bias, int mode, float eps,
                   const mh_quant_weights* gate, const mh_quant_weights* up,
                   const mh_quant_weights* down, uint32_t n_experts, uint32_t topk,
                   const uint16_t* x, uint16_t* out, float* logits, uint32_t* ids,
-                  uint16_t* weights, uint16_t* act, uint32_t* counter, mh_stream_t stream);
+                  uint16_t* weights, uint16_t* act, uint32_t* scratch, mh_stream_t stream);
 
 /* ------------------------------------------------- prefill routing ---
  * src/kernels/lfm.rs:366 router_prefill: logits f32 [m, e] = x [m, k] W^T,

@@ -31,7 +31,6 @@ typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kBK = 64;
-constexpr int kAPitch = kBK + 8;  // bf16 elements per LDS row
 
 enum Epi { EPI_STORE = 0, EPI_GATE_UP = 1, EPI_SWIGLU = 2 };
 

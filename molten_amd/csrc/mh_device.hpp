@@ -328,6 +328,10 @@ __device__ __forceinline__ void x_words_fence(uint32_t (&xw)[16]) {
                  : "memory");
 }
 
+// Ties a register to this point: a load feeding it is waited for here, and
+// nothing computed from it is moved above (keeps early-issued loads in flight).
+__device__ __forceinline__ void reg_fence(uint32_t& v) { asm volatile("" : "+v"(v)); }
+
 __device__ __forceinline__ void load_x_chunk(const uint16_t* xp, float (&xr)[32], float& xs) {
     uint32_t xw[16];
     load_x_words(xp, xw);
@@ -364,6 +368,9 @@ struct Chunk<4> {
         w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
     }
     __device__ __forceinline__ float dot(const float* xr) const { return q4_chunk_dot(w, xr); }
+    __device__ __forceinline__ void fence() {
+        reg_fence(w[0]); reg_fence(w[1]); reg_fence(w[2]); reg_fence(w[3]);
+    }
 };
 
 template <>
@@ -388,6 +395,45 @@ struct Chunk<6> {
         w[0] = a.x; w[1] = a.y; w[2] = b.x; w[3] = b.y; w[4] = c.x; w[5] = c.y;
     }
     __device__ __forceinline__ float dot(const float* xr) const { return q6_chunk_dot(w, xr); }
+};
+
+// One lane's 32-element chunk of a router row (bf16 or f32 weights), held
+// as raw words until converted.
+template <typename WT>
+struct RowWords;
+template <>
+struct RowWords<uint16_t> {  // 32 bf16 = 16 words
+    uint4 v[4];
+    __device__ __forceinline__ void load(const uint16_t* p) {
+        const uint4* q = reinterpret_cast<const uint4*>(p);
+        v[0] = q[0]; v[1] = q[1]; v[2] = q[2]; v[3] = q[3];
+    }
+    __device__ __forceinline__ void to_f32(float (&w)[32]) const {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t u[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                w[8 * i + 2 * j] = mh::bf16lo(u[j]);
+                w[8 * i + 2 * j + 1] = mh::bf16hi(u[j]);
+            }
+        }
+    }
+};
+template <>
+struct RowWords<float> {  // 32 f32
+    float4 v[8];
+    __device__ __forceinline__ void load(const float* p) {
+        const float4* q = reinterpret_cast<const float4*>(p);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = q[i];
+    }
+    __device__ __forceinline__ void to_f32(float (&w)[32]) const {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            w[4 * i] = v[i].x; w[4 * i + 1] = v[i].y; w[4 * i + 2] = v[i].z; w[4 * i + 3] = v[i].w;
+        }
+    }
 };
 
 }  // namespace mh

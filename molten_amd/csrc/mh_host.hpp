@@ -43,6 +43,11 @@ int moe_sort_maps(const uint32_t* ids, uint32_t s, uint32_t e, uint32_t topk, ui
                   uint32_t* slotpos, uint32_t* gu, uint32_t max_gu, uint32_t* dn, uint32_t max_dn,
                   uint32_t bm, uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n, uint32_t dn_n,
                   mh_stream_t stream);
+int moe_decode_fused(const void* router, int router_dtype, const float* bias, int mode, float eps,
+                     const mh_quant_weights* gate, const mh_quant_weights* up,
+                     const mh_quant_weights* down, uint32_t n_experts, uint32_t topk,
+                     const uint16_t* x, uint16_t* out, float* logits, uint32_t* ids,
+                     uint16_t* weights, uint16_t* act, uint32_t* scratch, hipStream_t stream);
 int router_prefill_route(const uint16_t* x, const void* w, int w_dtype, float* logits,
                          const float* bias, uint32_t* ids, uint16_t* gw, uint32_t m, uint32_t k,
                          uint32_t e, uint32_t topk, int mode, float eps, mh_stream_t stream);

@@ -100,4 +100,82 @@ __device__ inline void route_select(const float* s, const float* cand, uint32_t 
     }
 }
 
+// route_select with the scores in registers: lane l holds expert l + 64 j in
+// s[j] / cand[j] (cand -inf where l + 64 j >= e).  Same selection rule and
+// weight arithmetic as route_select; every lane of the wave returns the ids
+// and the bf16 weight bits (wave-uniform).  With e <= 64 a lane holds one
+// candidate and the lowest id among the lanes holding the maximum is the
+// lowest set bit of a ballot.  The weights are computed one slot per lane and
+// the denominator is summed slot by slot in order, as in route_select.
+template <int TK>
+__device__ inline void route_select_regs(const float (&s)[kMaxExperts / 64], const float (&cand)[kMaxExperts / 64],
+                                         uint32_t e, int mode, float eps, uint32_t (&ids)[TK],
+                                         uint32_t (&wbits)[TK]) {
+    constexpr int kPerLane = kMaxExperts / 64;
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t used = 0;
+    float sv[TK];
+#pragma unroll
+    for (int r = 0; r < TK; ++r) {
+        uint32_t pick;
+        if (e <= 64u) {
+            const float v = (used & 1u) ? -__builtin_inff() : cand[0];
+            const float m = wave_max_f32(v);
+            const unsigned long long hit = __ballot(v == m);
+            pick = m > -__builtin_inff() && hit != 0ull ? static_cast<uint32_t>(__builtin_ctzll(hit)) : 0u;
+        } else {
+            float bv = -__builtin_inff();
+            uint32_t bi = 0xffffffffu;
+#pragma unroll
+            for (int j = 0; j < kPerLane; ++j) {
+                if (64u * j < e) {
+                    // ids rise with j, so a strict > keeps the lowest id on ties
+                    const float v = cand[j];
+                    const bool take = !((used >> j) & 1u) && v > bv;
+                    bv = take ? v : bv;
+                    bi = take ? lane + 64u * j : bi;
+                }
+            }
+            const float m = wave_max_f32(bv);
+            bi = m > -__builtin_inff() ? wave_min_u32(bv == m ? bi : 0xffffffffu) : 0xffffffffu;
+            pick = bi == 0xffffffffu ? 0u : bi;
+        }
+        pick = __builtin_amdgcn_readfirstlane(pick);
+        ids[r] = pick;
+        float mine = s[0];
+#pragma unroll
+        for (int j = 1; j < kPerLane; ++j) {
+            mine = (pick >> 6) == static_cast<uint32_t>(j) ? s[j] : mine;
+        }
+        sv[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), pick & 63u));
+        used |= (pick & 63u) == lane ? 1u << (pick >> 6) : 0u;
+    }
+    float my = sv[0];
+#pragma unroll
+    for (int r = 1; r < TK; ++r) {
+        my = lane == static_cast<uint32_t>(r) ? sv[r] : my;
+    }
+    float num, denom;
+    if (mode == 0) {
+        num = my;
+        denom = eps;
+#pragma unroll
+        for (int r = 0; r < TK; ++r) {
+            denom = denom + sv[r];
+        }
+    } else {
+        num = expf_fixed(my - sv[0]);
+        denom = 0.0f;
+#pragma unroll
+        for (int r = 0; r < TK; ++r) {
+            denom = denom + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(num), r));
+        }
+    }
+    const int wl = static_cast<int>(f32_to_bf16(num / denom));
+#pragma unroll
+    for (int r = 0; r < TK; ++r) {
+        wbits[r] = static_cast<uint32_t>(__builtin_amdgcn_readlane(wl, r));
+    }
+}
+
 }  // namespace mh

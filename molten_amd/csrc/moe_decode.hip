@@ -183,43 +183,6 @@ __global__ __launch_bounds__(kThreads) void k_dense_gemv(DenseArgs a) {
 // chunk sums in one 4-row butterfly and gathers expert e's logits into lane
 // e % 64 of a per-token register; the logits are stored with one coalesced
 // store per token.  Same chunk order as k_dense_gemv.
-template <typename WT>
-struct RowWords;
-template <>
-struct RowWords<uint16_t> {  // 32 bf16 = 16 words
-    uint4 v[4];
-    __device__ __forceinline__ void load(const uint16_t* p) {
-        const uint4* q = reinterpret_cast<const uint4*>(p);
-        v[0] = q[0]; v[1] = q[1]; v[2] = q[2]; v[3] = q[3];
-    }
-    __device__ __forceinline__ void to_f32(float (&w)[32]) const {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t u[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                w[8 * i + 2 * j] = mh::bf16lo(u[j]);
-                w[8 * i + 2 * j + 1] = mh::bf16hi(u[j]);
-            }
-        }
-    }
-};
-template <>
-struct RowWords<float> {  // 32 f32
-    float4 v[8];
-    __device__ __forceinline__ void load(const float* p) {
-        const float4* q = reinterpret_cast<const float4*>(p);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = q[i];
-    }
-    __device__ __forceinline__ void to_f32(float (&w)[32]) const {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            w[4 * i] = v[i].x; w[4 * i + 1] = v[i].y; w[4 * i + 2] = v[i].z; w[4 * i + 3] = v[i].w;
-        }
-    }
-};
-
 constexpr int kRowTokens = 4;
 constexpr int kMaxExpertGroups = mh::kMaxExperts / 64;
 
@@ -248,7 +211,7 @@ __global__ __launch_bounds__(kThreads) void k_dense_rows(DenseArgs a) {
             mh::load_x_chunk(a.x + static_cast<size_t>(tok) * a.k + 32u * c, xr[t], xs);
         }
         const WT* w = static_cast<const WT*>(a.w) + 32u * c;
-        RowWords<WT> cur, nxt;
+        mh::RowWords<WT> cur, nxt;
         cur.load(w + static_cast<size_t>(e_begin) * a.k);
         for (uint32_t e = e_begin; e < e_end; ++e) {
             if (e + 1 < e_end) {
@@ -332,7 +295,7 @@ __global__ __launch_bounds__(64) void k_router_logits(DenseArgs a) {
     uint32_t xw[16];
     mh::load_x_words(a.x + 32u * c, xw);
     const WT* w = static_cast<const WT*>(a.w) + 32u * c;
-    RowWords<WT> rw[4];
+    mh::RowWords<WT> rw[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         rw[r].load(w + static_cast<size_t>(min(e0 + r, a.n - 1u)) * a.k);
@@ -1037,7 +1000,7 @@ int mh_moe_decode(const void* router, int router_dtype, const float* bias, int m
                   const mh_quant_weights* gate, const mh_quant_weights* up,
                   const mh_quant_weights* down, uint32_t n_experts, uint32_t topk,
                   const uint16_t* x, uint16_t* out, float* logits, uint32_t* ids,
-                  uint16_t* weights, uint16_t* act, uint32_t* counter, mh_stream_t stream) {
+                  uint16_t* weights, uint16_t* act, uint32_t* scratch, mh_stream_t stream) {
     const char* op = "mh_moe_decode";
     MH_ENSURE(gate && up && down, MH_ERR_INVALID, "%s: NULL weights", op);
     MH_ENSURE(n_experts > 0 && gate->out_features % n_experts == 0 &&
@@ -1052,7 +1015,7 @@ int mh_moe_decode(const void* router, int router_dtype, const float* bias, int m
     DenseArgs ra;
     MH_ENSURE(router_dtype == MH_DTYPE_F32 || router_dtype == MH_DTYPE_BF16, MH_ERR_INVALID,
               "%s: router dtype %d", op, router_dtype);
-    MH_ENSURE(counter != nullptr, MH_ERR_INVALID, "%s: counter is NULL", op);
+    MH_ENSURE(scratch != nullptr, MH_ERR_INVALID, "%s: scratch is NULL", op);
     MH_TRY(route_checks(op, logits, ids, weights, 1, n_experts, topk, mode));
     MH_TRY(dense_common(op, router, router_dtype == MH_DTYPE_F32, x, logits, 1, n_experts, d_model, ra));
     ActArgs aa;
@@ -1060,6 +1023,11 @@ int mh_moe_decode(const void* router, int router_dtype, const float* bias, int m
     DownArgs da;
     MH_TRY(down_common(op, down, act, ids, weights, out, topk, d_model, da));
     const hipStream_t s = mh::as_stream(stream);
+    const int fused = mh::moe_decode_fused(router, router_dtype, bias, mode, eps, gate, up, down, n_experts,
+                                           topk, x, out, logits, ids, weights, act, scratch, s);
+    if (fused != MH_ERR_UNSUPPORTED) {
+        return fused;
+    }
     if (d_model <= 2048u && n_inter % kActBlock == 0 && aa.groups % 2 == 0 &&
         aa.groups <= static_cast<uint32_t>(kMaxG) && d_model % kDownOut == 0) {
         // logits -> (routing inside every expert workgroup) -> down + combine
@@ -1081,7 +1049,7 @@ int mh_moe_decode(const void* router, int router_dtype, const float* bias, int m
     ra.bias = bias;
     ra.ids = ids;
     ra.weights = weights;
-    ra.done = counter;
+    ra.done = scratch + 256;  // a word the single-launch kernel never uses
     ra.topk = topk;
     ra.mode = mode;
     ra.eps = eps;

@@ -227,6 +227,7 @@ def gemv_head_argmax(w: QuantWeights, x, best, batch: int = 1, stream=None) -> N
 
 
 ARGMAX_SLOTS = 2048
+MOE_DECODE_SCRATCH_WORDS = 10240  # MH_MOE_DECODE_SCRATCH_WORDS
 
 
 def argmax_scratch_words(batch: int) -> int:
@@ -311,13 +312,14 @@ def gemv_gather_down_combine4(down: QuantWeights, act, ids, weights, out, topk: 
 
 
 def moe_decode(router, bias, gate: QuantWeights, up: QuantWeights, down: QuantWeights,
-               n_experts: int, topk: int, x, out, logits, ids, weights, act, counter,
+               n_experts: int, topk: int, x, out, logits, ids, weights, act, scratch,
                mode: int = ROUTE_SIGMOID_BIAS, eps: float = 1e-6, stream=None) -> None:
-    """One MoE decode step (src/lfm.rs:967-1011)."""
+    """One MoE decode step (src/lfm.rs:967-1011).  scratch: MOE_DECODE_SCRATCH_WORDS
+    u32 words, zeroed once before the first call, then left to this function."""
     check(load().mh_moe_decode(_ptr(router), _dtype_of(router), _ptr(bias), mode, eps,
                                _qref(gate), _qref(up), _qref(down), n_experts, topk, _ptr(x),
                                _ptr(out), _ptr(logits), _ptr(ids), _ptr(weights), _ptr(act),
-                               _ptr(counter), _stream(stream)), "moe_decode")
+                               _ptr(scratch), _stream(stream)), "moe_decode")
 
 
 def router_prefill(x, w, out, m: int, k: int, e: int, stream=None) -> None:

@@ -17,6 +17,14 @@ def _log(msg):
     print(msg, flush=True)
 
 
+def _check_scratch(words, steps):
+    """After `steps` single-launch decode steps each of the 256 workgroups'
+    launch counts (words 0..255) equals steps, and word 256 (the three-launch
+    path's done counter) is zero."""
+    assert (words[:256] == steps).all(), words[:256]
+    assert words[256] == 0
+
+
 @pytest.fixture(scope="module")
 def experts():
     """Config 3's 64 experts (uploaded once for the module)."""
@@ -152,7 +160,7 @@ def test_expert_kernels_extreme_activations(dev, orc, experts, huge):
 def test_moe_decode_step_bit_exact(dev, orc, experts, mode, f32):
     """Config 3: router -> top-4 -> gate/up/SwiGLU -> down -> combine, all
     intermediates and the output bit-exact, for several inputs (different
-    routings), with the counter left zero between steps."""
+    routings), with the scratch words consistent between steps."""
     _log(f"moe decode mode={mode} f32={f32}")
     gate, up, down = experts["h"]
     dg, du, dd = experts["d"]
@@ -166,11 +174,11 @@ def test_moe_decode_step_bit_exact(dev, orc, experts, mode, f32):
     ids = empty_dev((TOPK,), np.uint32)
     wt = empty_dev((TOPK,), np.uint16)
     act = empty_dev((TOPK, I), np.uint16)
-    counter = zeros_dev((1,), np.uint32)
+    scratch = zeros_dev((hip.MOE_DECODE_SCRATCH_WORDS,), np.uint32)
     seen = set()
     for trial in range(4):
         x = layout.synth_bf16(rng, (1, H))[0]
-        hip.moe_decode(rd, bd, dg, du, dd, E, TOPK, to_dev(x), out, logits, ids, wt, act, counter,
+        hip.moe_decode(rd, bd, dg, du, dd, E, TOPK, to_dev(x), out, logits, ids, wt, act, scratch,
                        mode=mode)
         want = orc.moe_decode(router, bias, mode, gate, up, down, E, TOPK, H, I, x)
         assert from_dev(ids, np.uint32).tolist() == want["ids"].tolist()
@@ -178,9 +186,44 @@ def test_moe_decode_step_bit_exact(dev, orc, experts, mode, f32):
         np.testing.assert_array_equal(from_dev(wt, np.uint16), want["w"])
         np.testing.assert_array_equal(from_dev(act, np.uint16), want["act"])
         np.testing.assert_array_equal(from_dev(out, np.uint16), want["out"])
-        assert from_dev(counter, np.uint32)[0] == 0
+        _check_scratch(from_dev(scratch, np.uint32), trial + 1)
         seen.add(tuple(want["ids"].tolist()))
     assert len(seen) > 1  # the inputs exercised different routings
+
+
+@pytest.mark.parametrize("e,h,i,topk,shifted", [(8, 512, 256, 2, False), (16, 1024, 128, 1, False),
+                                                 (32, 768, 192, 3, False), (8, 512, 128, 2, True)])
+def test_moe_decode_step_shapes(dev, orc, e, h, i, topk, shifted):
+    """Decode step at other shapes and top-k, bit-exact, over repeated steps
+    sharing one scratch.  Activations that are not 4-byte aligned (shifted)
+    take the three-launch path instead of the single-launch kernel."""
+    _log(f"moe decode shape e={e} h={h} i={i} topk={topk} shifted={shifted}")
+    rng = np.random.default_rng(7 * e + i + topk)
+    gate, up, down = moe_weights(rng, e, h, i)
+    dg, kg = dev_quant(gate)
+    du, ku = dev_quant(up)
+    dd, kd = dev_quant(down)
+    router = router_weights(rng, e, h, False)
+    rd = to_dev(router)
+    out = empty_dev((h,), np.uint16)
+    logits = empty_dev((e,), np.float32)
+    ids = empty_dev((topk,), np.uint32)
+    wt = empty_dev((topk,), np.uint16)
+    act = empty_dev((topk * i + 1,), np.uint16)[1:] if shifted else empty_dev((topk * i,), np.uint16)
+    assert (act.data_ptr() % 4 != 0) == shifted
+    scratch = zeros_dev((hip.MOE_DECODE_SCRATCH_WORDS,), np.uint32)
+    for trial in range(3):
+        x = layout.synth_bf16(rng, (1, h))[0]
+        hip.moe_decode(rd, None, dg, du, dd, e, topk, to_dev(x), out, logits, ids, wt, act, scratch,
+                       mode=1)
+        want = orc.moe_decode(router, None, 1, gate, up, down, e, topk, h, i, x)
+        assert from_dev(ids, np.uint32).tolist() == want["ids"].tolist()
+        np.testing.assert_array_equal(from_dev(logits, np.float32), want["logits"])
+        np.testing.assert_array_equal(from_dev(wt, np.uint16), want["w"])
+        np.testing.assert_array_equal(from_dev(act, np.uint16).reshape(topk, i), want["act"])
+        np.testing.assert_array_equal(from_dev(out, np.uint16), want["out"])
+        _check_scratch(from_dev(scratch, np.uint32), 0 if shifted else trial + 1)
+    del kg, ku, kd
 
 
 def test_prefill_router_and_route_batch(dev, orc):
