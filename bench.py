@@ -69,16 +69,29 @@ def bf16_randn(torch, shape, dev, gen, std=1.0):
     return (torch.randn(shape, device=dev, generator=gen) * std).to(torch.bfloat16).view(torch.int16)
 
 
+EAGER = False  # --eager: no graph capture (counter collection sees only eager dispatches)
+
+
 def timed(torch, fn, steps, warmup):
     """Average ms per call of fn(i) over `steps` calls after `warmup` eager
     calls.  The `steps` calls are captured once in a HIP graph; the graph is
     replayed five times, each replay between two events on the launch stream
     and bracketed by synchronizes, and the median replay is returned.  Host
     launch overhead (ctypes, Python) is not timed: the GPU runs the kernels
-    back to back, as a decode loop captured in a graph would."""
+    back to back, as a decode loop captured in a graph would.  With EAGER the
+    `steps` calls are launched directly between the two events instead."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
+    if EAGER:
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(steps):
+            fn(warmup + i)
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for i in range(steps):
@@ -233,8 +246,14 @@ def main() -> int:
                     help="time budget of the CPU baseline sample (0 = skip)")
     ap.add_argument("--only-headline", action="store_true", help="skip configs 1, 3, 4, 5")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
-                    help="also run a plain device copy of this many MiB (PMC byte calibration)")
+                    help="also run a plain elementwise copy (f32 negate) of this many MiB "
+                         "(PMC byte calibration)")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch the timed steps directly instead of replaying a graph "
+                         "(for counter collection; host launch overhead is then timed)")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
               "(--gpus must be 1).", file=sys.stderr)
@@ -255,10 +274,11 @@ def main() -> int:
     ms2 = bench_lm_head(torch, hip, dev, gen, 4, 1, steps, warmup, copies=5)
     gbs2 = BYTES["config2"] / (ms2 * 1e-3) / 1e9
     if args.calibrate_copy_mib > 0:
-        src = torch.ones(args.calibrate_copy_mib << 20, dtype=torch.uint8, device=dev)
+        # reads and writes exactly calibrate_copy_mib MiB each, in one kernel
+        src = torch.ones((args.calibrate_copy_mib << 20) // 4, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
         for _ in range(3):
-            dst.copy_(src)
+            torch.neg(src, out=dst)
         torch.cuda.synchronize()
         del src, dst
     others = {}
