@@ -184,15 +184,15 @@ def bench_config4(torch, hip, dev, gen, steps, warmup):
     g, u, d, r = sets[(max(2, steps // 4) + max(1, warmup // 4) - 1) % len(sets)]
     base = ws.data_ptr()
     s = m * topk
-    gu_bn, dn_bn, bm = 128, 256, 128
+    gu_bn, dn_bn, bm = hip.MoeTile.GU512[1], hip.MoeTile.DN512[1], hip.MoeTile.GU512[0]
     m_tiles = -(-s // bm) + E
     max_gu, max_dn = m_tiles * I // gu_bn, m_tiles * H // dn_bn
 
     def gemms(i):
         hip.gemm_q4_grouped_gu_act(x, base + offs["ids_sorted"], m, g[0], u[0], base + offs["act"],
-                                   base + offs["gu_map"], max_gu, s, I, hip.MoeTile.GU128)
+                                   base + offs["gu_map"], max_gu, s, I, hip.MoeTile.GU512)
         hip.gemm_q4_grouped_mlx(base + offs["act"], d[0], base + offs["ed"], base + offs["dn_map"],
-                                max_dn, s, H, hip.MoeTile.DN128)
+                                max_dn, s, H, hip.MoeTile.DN512)
 
     ms_gemm = timed(torch, gemms, max(2, steps // 4), 1)
     del sets, ws

@@ -20,6 +20,8 @@
 //     block are one 16-byte load.
 // Epilogues: store C; store gate and up separately; or SwiGLU
 // act = bf16(bf16(silu(bf16 g)) * bf16 u) with two accumulators per tile.
+#include <type_traits>
+
 #include "mh_device.hpp"
 #include "mh_host.hpp"
 
@@ -68,6 +70,22 @@ __device__ __forceinline__ bf16x8_t deq_word(uint32_t w, float s, float s16, flo
 }
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// Workgroup -> block-map entry.  Entries come in groups of nt = n / bn (the
+// column tiles of one expert row tile, which read the same A rows); groups
+// are dealt round-robin to the 8 XCDs (workgroup i runs on XCD i % 8), so
+// every XCD gets an equal share of the real entries (the map's tail is
+// padding) and a group's tiles share one XCD's L2.  The grid is a multiple
+// of 8 * nt (grid_for_map); indices past the map are padding.
+__device__ __forceinline__ uint32_t entry_of_block(uint32_t nt) {
+    const uint32_t x = blockIdx.x % 8u, j = blockIdx.x / 8u;
+    return ((j / nt) * 8u + x) * nt + j % nt;
+}
+
+inline uint32_t grid_for_map(uint32_t n_blocks, uint32_t nt) {
+    const uint32_t unit = 8u * nt;
+    return (n_blocks + unit - 1u) / unit * unit;
+}
 typedef const __attribute__((address_space(1))) void* glb_ptr;
 
 constexpr int kStages = 3;  // LDS ring depth: two K-blocks in flight while one is consumed
@@ -100,6 +118,21 @@ __device__ __forceinline__ uint32_t lds_read4(uint32_t addr) {
     asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
     return v;
 }
+// The same reads with a constant byte offset in the instruction (no address add).
+template <int OFF>
+__device__ __forceinline__ uint4 lds_read16_at(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+    uint4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_read4_at(uint32_t addr) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
+    return v;
+}
 
 // Tile of BM rows x (NW * NBW * 32) columns per matrix; NW waves, wave w owns
 // column blocks [w * NBW, (w + 1) * NBW) of every matrix and all BM rows.
@@ -113,9 +146,7 @@ __device__ __forceinline__ uint32_t lds_read4(uint32_t addr) {
 // Each wave waits for its own loads of a stage (vmcnt), one barrier then
 // publishes the A block and frees the slot the next stage overwrites.
 // Row blocks of 32 past the expert's segment are skipped.  Block-map entries
-// are taken XCD by XCD: workgroup i runs entry (i % 8) * L + i / 8, so the
-// entries that share A rows (one expert's row tile across its column tiles)
-// run on one XCD and hit its L2.
+// are dealt to XCDs in column-tile groups (entry_of_block).
 template <int BM, int NBW, int NW, bool GATHER, int EPI>
 __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void k_grouped(GemmArgs a, uint32_t n_entries) {
     constexpr int kThr = NW * 64;
@@ -132,8 +163,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void k_grouped(GemmArgs a
     extern __shared__ __attribute__((aligned(16))) char lds[];
     (void)kThr;
 
-    const uint32_t per_xcd = (n_entries + 7u) / 8u;
-    const uint32_t ent = (blockIdx.x % 8u) * per_xcd + blockIdx.x / 8u;
+    const uint32_t ent = entry_of_block(a.n / (NW * NBW * 32u));
     if (ent >= n_entries) {
         return;
     }
@@ -319,6 +349,440 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void k_grouped(GemmArgs a
             }
 }
 
+// ------------------------------------------------------------------------
+// Segment kernel: one workgroup per block-map entry of any row count (maps
+// built with bm = 256 or 512), 4 waves, one workgroup per CU.  The entry's
+// rows are covered in passes of RB <= 8 row blocks of 32 (passes balanced:
+// a 270-row segment runs as 5 + 4 blocks, not 8 + 1); RB is a template
+// argument of the pass, so the K loop has no per-row-block branches.  The
+// accumulators (RB x NMAT x NBW tiles of 32x32 f32, up to 256 registers)
+// live in AGPRs.  Per K-step of 16 the wave issues the next step's A
+// fragment reads before this step's MFMAs and dequantizes the next step's B
+// words between them, so LDS latency and the dequant VALU work run under
+// the matrix pipe.
+
+constexpr int kSegWaves = 4;
+#ifndef MH_SEG_RBMAX
+#define MH_SEG_RBMAX 8
+#endif
+constexpr int kSegRBMax = MH_SEG_RBMAX;  // row blocks of 32 per pass (max)
+#ifndef MH_SEG_STAGES
+#define MH_SEG_STAGES 3
+#endif
+constexpr int kSegStages = MH_SEG_STAGES;  // LDS ring depth
+
+// Compile-time loop: f(std::integral_constant<int, i>) for i in [0, N).
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for_impl(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for_impl<I + 1, N>(f);
+    }
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl<0, N>(f);
+}
+
+// s_waitcnt lgkmcnt(N), tied to the registers it guards so that no use of
+// them can be scheduled above it.
+template <int N, int M>
+__device__ __forceinline__ void lgkm_wait(uint4 (&v)[M]) {
+    static_assert(N >= 0 && N <= 15, "lgkmcnt field");
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        mh::u32x4 t = {v[i].x, v[i].y, v[i].z, v[i].w};
+        asm volatile("" : "+v"(t));
+        v[i] = make_uint4(t.x, t.y, t.z, t.w);
+    }
+}
+template <int N, int M>
+__device__ __forceinline__ void lgkm_wait(uint32_t (&v)[M]) {
+    static_assert(N >= 0 && N <= 15, "lgkmcnt field");
+    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        auto t = v[i];
+        asm volatile("" : "+v"(t));
+        v[i] = t;
+    }
+}
+
+// Fast SiLU for the GEMM epilogue (the gate/up values it sees already
+// carry MFMA accumulation error): g * 1 / (1 + 2^(-g log2 e)) with the
+// hardware exp2 and reciprocal (1 ulp each).
+__device__ __forceinline__ float silu_hw(float g) {
+    const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+    return g * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+__device__ __forceinline__ float bf16_round_hw(float v) {
+    const f32x2_t p = {v, 0.0f};
+    const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector(p, bf16x2_t));
+    return __uint_as_float(u << 16);
+}
+
+// Wait until at most c (<= C) later stages of OPS vector memory ops each are
+// still in flight.
+template <int OPS, int C>
+__device__ __forceinline__ void wait_stages(uint32_t c) {
+    if constexpr (C == 0) {
+        wait_vmcnt<0>();
+    } else {
+        static_assert(C * OPS <= 63, "vmcnt field");
+        if (c >= static_cast<uint32_t>(C)) {
+            wait_vmcnt<C * OPS>();
+        } else {
+            wait_stages<OPS, C - 1>(c);
+        }
+    }
+}
+
+template <int RBMAX, int NBW, int NMAT, int NS = kStages>
+struct SegLayout {
+    static constexpr int NB = NMAT * NBW;                    // B fragments per wave
+    static constexpr int A_STAGE = RBMAX * 32 * 128;         // RBMAX*32 rows x 64 k bf16
+    static constexpr int B_HALF = kSegWaves * NB * 2048;     // codes of 2 stages (k 128)
+    static constexpr int SB_BLK = kSegWaves * NB * 1024;     // scales + biases of 8 groups
+    static constexpr int B_OFF = NS * A_STAGE;               // A ring, then two B slots,
+    static constexpr int SB_OFF = B_OFF + 2 * B_HALF;        // then two scale/bias slots
+    static constexpr int LDS = SB_OFF + 2 * SB_BLK;
+};
+
+// One pass: rows [mp0, mp0 + 32 RB) of the segment (clamped to m_end),
+// columns of this wave, the whole K.
+//
+// Loads are direct-to-LDS and shaped for few L2 requests per 64-k stage:
+//   * A: RB*32 rows x 128 bytes (one line per row) into a 3-slot ring shared
+//     by the workgroup, 16-byte chunks XOR-swizzled by row;
+//   * B codes: every other stage, the next two stages' codes of each column
+//     (64 bytes, half a line; 4 lanes per column) into a per-wave region of
+//     one of two slots, chunks swizzled by ((column >> 1) & 3) so the MFMA
+//     operand reads (lane i32, half h, stage s: chunk 2s + h) are
+//     bank-conflict free;
+//   * scales and biases: every 8 stages, 16 bytes (8 groups) of the column's
+//     scale row (lanes 0-31) and bias row (lanes 32-63), two slots.
+// Stage g's loads ("group g": its A, plus the B half-block that starts at g,
+// plus the scale/bias block that starts at g) are issued at iteration g - 2,
+// so before stage kb is read the wave waits until only group kb + 1 may
+// still be in flight; one barrier per stage publishes everyone's loads.
+template <int RB, int RBMAX, int NS, int NBW, int NMAT, bool GATHER, int EPI>
+__device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint32_t n0,
+                                         uint32_t mp0, uint32_t m_end, uint32_t lds0, int lane,
+                                         int wave) {
+    using L = SegLayout<RBMAX, NBW, NMAT, NS>;
+    static_assert(NS == 3, "loads run two stages ahead through a 3-slot A ring");
+    constexpr int NB = L::NB;
+    constexpr int QA = RB;  // A loads (8 rows each) per wave per stage
+    const int i32 = lane & 31, h = lane >> 5;
+    const uint32_t K = a.k, nkb = K / kBK, groups = K / 64u;
+
+    const mh::gbytes abase = mh::uniform_ptr(a.a);
+    mh::gbytes cbase[NMAT], sbase[NMAT], bbase[NMAT];
+    cbase[0] = mh::uniform_ptr(a.c0);
+    sbase[0] = mh::uniform_ptr(a.s0);
+    bbase[0] = mh::uniform_ptr(a.b0);
+    if (NMAT == 2) {
+        cbase[NMAT - 1] = mh::uniform_ptr(a.c1);
+        sbase[NMAT - 1] = mh::uniform_ptr(a.s1);
+        bbase[NMAT - 1] = mh::uniform_ptr(a.b1);
+    }
+    uint32_t aoffs[QA];
+#pragma unroll
+    for (int q = 0; q < QA; ++q) {
+        const uint32_t r = 8u * (wave * QA + q) + static_cast<uint32_t>(lane >> 3);
+        const uint32_t m = min(mp0 + r, m_end - 1u);
+        uint32_t src = GATHER ? a.gather[m] : m;
+        src = min(src, a.a_rows - 1u);
+        const uint32_t chunk = static_cast<uint32_t>(lane & 7) ^ (r & 7u);
+        aoffs[q] = src * K * 2u + chunk * 16u;
+    }
+    // B half-block load p of fragment t: columns 16p .. 16p + 15, lane l =
+    // 4c' + q stores LDS chunk q of column c = 16p + c', holding global chunk
+    // q ^ ((c >> 1) & 3).  Scale/bias block: lane (i32, h) loads 16 bytes of
+    // column i32's scale (h = 0) or bias (h = 1) row.
+    uint32_t bcoffs[NB][2], sboff[NB];
+#pragma unroll
+    for (int cb = 0; cb < NBW; ++cb) {
+#pragma unroll
+        for (int mat = 0; mat < NMAT; ++mat) {
+            const int t = mat * NBW + cb;
+            const uint32_t col0 = brow + static_cast<uint32_t>((wave * NBW + cb) * 32);
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const uint32_t c = 16u * p + static_cast<uint32_t>(lane >> 2);
+                const uint32_t r = min(col0 + c, a.w_rows - 1u);
+                const uint32_t g = static_cast<uint32_t>(lane & 3) ^ ((c >> 1) & 3u);
+                bcoffs[t][p] = r * (K / 2u) + g * 16u;
+            }
+            sboff[t] = min(col0 + static_cast<uint32_t>(i32), a.w_rows - 1u) * groups * 2u;
+        }
+    }
+    auto issue_group = [&](uint32_t g) {
+        const uint32_t abuf = lds0 + (g % 3u) * L::A_STAGE;
+        const mh::gbytes ag = mh::uniform_ptr(abase + g * 128u);
+#pragma unroll
+        for (int q = 0; q < QA; ++q) {
+            dma16(ag + aoffs[q], abuf + (wave * QA + q) * 1024u);
+        }
+        if ((g & 1u) == 0) {
+            const uint32_t hb = g >> 1;
+            const uint32_t bbuf = lds0 + L::B_OFF + (hb & 1u) * L::B_HALF + wave * NB * 2048u;
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+                const mh::gbytes cg = mh::uniform_ptr(cbase[t / NBW] + hb * 64u);
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    dma16(cg + bcoffs[t][p], bbuf + t * 2048u + p * 1024u);
+                }
+            }
+        }
+        if ((g & 7u) == 0) {
+            const uint32_t sbk = g >> 3;
+            const uint32_t sbuf = lds0 + L::SB_OFF + (sbk & 1u) * L::SB_BLK + wave * NB * 1024u;
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+                const mh::gbytes src = h ? bbase[t / NBW] : sbase[t / NBW];
+                dma16(src + sboff[t] + sbk * 16u, sbuf + t * 1024u);
+            }
+        }
+    };
+
+    f32x16_t acc[NMAT][RB][NBW];
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < NBW; ++cb)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) acc[mat][rb][cb][q] = 0.0f;
+
+    uint32_t aoff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        aoff[j] = static_cast<uint32_t>(i32) * 128u +
+                  ((static_cast<uint32_t>(4 * h + j) ^ static_cast<uint32_t>(i32 & 7)) * 16u);
+    }
+
+    // Stage kb's inputs become readable once group kb has landed (only group
+    // kb + 1 may still be in flight) and every wave has passed a barrier.
+    auto wait_group = [&](uint32_t kb) {
+        const uint32_t g1 = kb + 1;
+        if (g1 >= nkb) {
+            wait_vmcnt<0>();
+        } else if ((g1 & 7u) == 0) {
+            wait_vmcnt<QA + 3 * NB>();
+        } else if ((g1 & 1u) == 0) {
+            wait_vmcnt<QA + 2 * NB>();
+        } else {
+            wait_vmcnt<QA>();
+        }
+        __builtin_amdgcn_s_barrier();
+    };
+    // LDS reads of a stage's B codes (chunk 2 (kb % 2) + h of the lane's
+    // column), scale/bias words (group kb: word (kb % 8) / 2) and first
+    // A fragments; issued without waiting.
+    auto read_stage = [&](uint32_t kb, uint4 (&bc)[NB], uint32_t (&sbw)[2 * NB], uint4 (&av)[RB]) {
+        const uint32_t pos = ((2u * (kb & 1u) + static_cast<uint32_t>(h)) ^ ((static_cast<uint32_t>(i32) >> 1) & 3u)) * 16u;
+        const uint32_t bl = lds0 + L::B_OFF + ((kb >> 1) & 1u) * L::B_HALF + wave * NB * 2048u + i32 * 64u + pos;
+        static_for<NB>([&](auto t) { bc[t] = lds_read16_at<t * 2048>(bl); });
+        const uint32_t sl = lds0 + L::SB_OFF + ((kb >> 3) & 1u) * L::SB_BLK + wave * NB * 1024u + i32 * 16u + ((kb & 7u) >> 1) * 4u;
+        static_for<NB>([&](auto t) {
+            sbw[2 * t] = lds_read4_at<t * 1024>(sl);
+            sbw[2 * t + 1] = lds_read4_at<t * 1024 + 512>(sl);
+        });
+        const uint32_t ab = lds0 + (kb % 3u) * L::A_STAGE + aoff[0];
+        static_for<RB>([&](auto rb) { av[rb] = lds_read16_at<rb * 4096>(ab); });
+    };
+    float sf[NB], s16[NB], bf[NB];
+    auto scale_bias = [&](uint32_t kb, const uint32_t (&sbw)[2 * NB]) {
+        const uint32_t half = (kb & 1u) ? 0u : 16u;  // group kb's bf16 is the high half when kb is odd
+#pragma unroll
+        for (int t = 0; t < NB; ++t) {
+            sf[t] = __uint_as_float((sbw[2 * t] << half) & 0xffff0000u);
+            s16[t] = sf[t] * 0.0625f;
+            bf[t] = __uint_as_float((sbw[2 * t + 1] << half) & 0xffff0000u);
+        }
+    };
+
+    issue_group(0);
+    if (nkb > 1) {
+        issue_group(1);
+    }
+    for (uint32_t kb = 0; kb < nkb; ++kb) {
+        wait_group(kb);
+        if (kb + 2 < nkb) {
+            issue_group(kb + 2);
+        }
+        uint4 bc[NB];
+        uint32_t sbw[2 * NB];
+        uint4 av[2][RB];
+        read_stage(kb, bc, sbw, av[0]);
+        lgkm_wait<RB>(bc);
+        lgkm_wait<RB>(sbw);
+        scale_bias(kb, sbw);
+        bf16x8_t bfr[2][NB];
+#pragma unroll
+        for (int t = 0; t < NB; ++t) {
+            bfr[0][t] = deq_word(bc[t].x, sf[t], s16[t], bf[t]);
+        }
+        const uint32_t base = lds0 + (kb % 3u) * L::A_STAGE;
+        // next step's A reads in flight and its B words dequantized while this
+        // step's MFMAs run
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int cur = j & 1, nxt = cur ^ 1;
+            if (j < 3) {
+                const uint32_t ab = base + aoff[j + 1];
+                static_for<RB>([&](auto rb) { av[nxt][rb] = lds_read16_at<rb * 4096>(ab); });
+                lgkm_wait<RB>(av[cur]);
+            } else {
+                lgkm_wait<0>(av[cur]);
+            }
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                const bf16x8_t af = __builtin_bit_cast(bf16x8_t, av[cur][rb]);
+#pragma unroll
+                for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+                    for (int cb = 0; cb < NBW; ++cb)
+                        acc[mat][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                            bfr[cur][mat * NBW + cb], af, acc[mat][rb][cb], 0, 0, 0);
+                if (j < 3 && rb == 0) {
+#pragma unroll
+                    for (int t = 0; t < NB; ++t) {
+                        const uint32_t wv = j == 0 ? bc[t].y : j == 1 ? bc[t].z : bc[t].w;
+                        bfr[nxt][t] = deq_word(wv, sf[t], s16[t], bf[t]);
+                    }
+                }
+            }
+        }
+    }
+    // every wave is done with the ring before another pass refills it
+    __builtin_amdgcn_s_barrier();
+
+    // ---- epilogue.  The MFMAs computed C^T (W fragment as the first
+    // operand): lane (i32, h) holds row mp0 + 32 rb + i32 and, at q = 4p + r,
+    // column 8p + 4h + r of its 32-column block.  Values become bf16 pairs;
+    // permlane32_swap of the (p even, p odd) pairs gives lane h = 0 columns
+    // 8p..8p+7 of p = 0, 2 and lane h = 1 those of p = 1, 3, stored 16 bytes
+    // at a time.
+    const mh::gbytes ob0 = mh::uniform_ptr(reinterpret_cast<const char*>(a.out0));
+    const mh::gbytes ob1 = mh::uniform_ptr(reinterpret_cast<const char*>(a.out1 ? a.out1 : a.out0));
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const uint32_t row = mp0 + rb * 32u + static_cast<uint32_t>(i32);
+#pragma unroll
+        for (int cb = 0; cb < NBW; ++cb) {
+            constexpr int NOUT = (EPI == EPI_GATE_UP) ? 2 : 1;
+            uint32_t w[NOUT][4][2];  // [output][p][pair]
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                float v[NOUT][4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int q = 4 * p + r;
+                    if constexpr (EPI == EPI_SWIGLU) {
+                        const float g = bf16_round_hw(acc[0][rb][cb][q]);
+                        const float u = bf16_round_hw(acc[1][rb][cb][q]);
+                        v[0][r] = bf16_round_hw(silu_hw(g)) * u;
+                    } else {
+#pragma unroll
+                        for (int o = 0; o < NOUT; ++o) {
+                            v[o][r] = acc[o][rb][cb][q];
+                        }
+                    }
+                }
+#pragma unroll
+                for (int o = 0; o < NOUT; ++o) {
+                    w[o][p][0] = pack_bf16(v[o][0], v[o][1]);
+                    w[o][p][1] = pack_bf16(v[o][2], v[o][3]);
+                }
+            }
+            const uint32_t col = n0 + static_cast<uint32_t>((wave * NBW + cb) * 32 + 8 * h);
+            const uint32_t off = (row * a.n + col) * 2u;
+#pragma unroll
+            for (int o = 0; o < NOUT; ++o) {
+#pragma unroll
+                for (int pp = 0; pp < 2; ++pp) {
+#pragma unroll
+                    for (int d = 0; d < 2; ++d) {
+                        const auto r = __builtin_amdgcn_permlane32_swap(w[o][2 * pp][d], w[o][2 * pp + 1][d], false, false);
+                        w[o][2 * pp][d] = r[0];
+                        w[o][2 * pp + 1][d] = r[1];
+                    }
+                }
+                if (row < m_end) {
+                    const mh::gbytes ob = o == 0 ? ob0 : ob1;
+                    typedef __attribute__((address_space(1))) mh::u32x4* g4;
+                    // columns 8h .. 8h+7 (pp = 0) and 16 + 8h .. (pp = 1)
+                    *reinterpret_cast<g4>(const_cast<char __attribute__((address_space(1)))*>(ob) + off) =
+                        mh::u32x4{w[o][0][0], w[o][0][1], w[o][1][0], w[o][1][1]};
+                    *reinterpret_cast<g4>(const_cast<char __attribute__((address_space(1)))*>(ob) + off + 32u) =
+                        mh::u32x4{w[o][2][0], w[o][2][1], w[o][3][0], w[o][3][1]};
+                }
+            }
+        }
+    }
+}
+
+template <int RBMAX, int NS, int NBW, int NMAT, bool GATHER, int EPI>
+__global__ __launch_bounds__(kSegWaves * 64, (SegLayout<RBMAX, NBW, NMAT, NS>::LDS <= 80 * 1024 ? 2 : 1))
+void k_seg(GemmArgs a, uint32_t n_entries) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    const uint32_t ent = entry_of_block(a.n / (kSegWaves * NBW * 32u));
+    if (ent >= n_entries) {
+        return;
+    }
+    const uint4 blk = a.blocks[ent];
+    const uint32_t m0 = blk.x, brow = blk.y, n0 = blk.z, m_end = blk.w;
+    if (m0 >= m_end) {
+        return;
+    }
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lds0 = static_cast<uint32_t>((uintptr_t)((lds_ptr)lds));
+    const uint32_t nrb = (m_end - m0 + 31u) / 32u;
+    const uint32_t passes = (nrb + RBMAX - 1u) / RBMAX;
+    uint32_t mp0 = m0;
+    for (uint32_t p = 0; p < passes; ++p) {
+        // balanced passes: this one takes ceil(remaining blocks / remaining passes)
+        const uint32_t left = (m_end - mp0 + 31u) / 32u;
+        const uint32_t rb = (left + (passes - p) - 1u) / (passes - p);
+#define MH_SEG_CASE(R)                                                                      \
+    case R:                                                                                 \
+        if constexpr (R <= RBMAX) {                                                         \
+            seg_pass<R, RBMAX, NS, NBW, NMAT, GATHER, EPI>(a, brow, n0, mp0, m_end, lds0, lane, wave); \
+        }                                                                                   \
+        break;
+        switch (rb) {
+            MH_SEG_CASE(1) MH_SEG_CASE(2) MH_SEG_CASE(3) MH_SEG_CASE(4)
+            MH_SEG_CASE(5) MH_SEG_CASE(6) MH_SEG_CASE(7) MH_SEG_CASE(8)
+            default: break;
+        }
+#undef MH_SEG_CASE
+        mp0 += rb * 32u;
+    }
+}
+
+template <int RBMAX, int NS, int NBW, int NMAT, bool GATHER, int EPI>
+int launch_seg(const GemmArgs& a, uint32_t n_blocks, hipStream_t s) {
+    constexpr size_t lds = SegLayout<RBMAX, NBW, NMAT, NS>::LDS;
+    static_assert(lds <= 160 * 1024, "LDS per workgroup");
+    auto kern = k_seg<RBMAX, NS, NBW, NMAT, GATHER, EPI>;
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(lds));
+    if (e != hipSuccess) {
+        return mh::hip_error(e, "k_seg");
+    }
+    const uint32_t grid = grid_for_map(n_blocks, a.n / (kSegWaves * NBW * 32u));
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kSegWaves * 64), lds, s, a, n_blocks);
+    return mh::launch_status("k_seg");
+}
+
 template <int BM, int NBW, int NW, bool GATHER, int EPI>
 int launch_t(const GemmArgs& a, uint32_t n_blocks, hipStream_t s) {
     constexpr int NMAT = (EPI == EPI_STORE) ? 1 : 2;
@@ -332,7 +796,7 @@ int launch_t(const GemmArgs& a, uint32_t n_blocks, hipStream_t s) {
             return mh::hip_error(e, "k_grouped");
         }
     }
-    const uint32_t grid = (n_blocks + 7u) / 8u * 8u;
+    const uint32_t grid = grid_for_map(n_blocks, a.n / (NW * NBW * 32u));
     hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), lds, s, a, n_blocks);
     return mh::launch_status("k_grouped");
 }
@@ -341,14 +805,25 @@ int launch_t(const GemmArgs& a, uint32_t n_blocks, hipStream_t s) {
 // with one column block per wave and matrix.
 template <bool GATHER, int EPI>
 int dispatch(const GemmArgs& a, uint32_t n_blocks, uint32_t bm, uint32_t bn, hipStream_t s) {
+    MH_ENSURE(bn > 0 && a.n % bn == 0, MH_ERR_INVALID, "grouped GEMM: N %u not a multiple of the tile width %u",
+              a.n, bn);
+    // segment kernels: 32-bit byte offsets from uniform bases for every
+    // operand, 16-byte output stores
+    const bool seg = (bm == 256 || bm == 512) && a.k % 512u == 0u &&
+                     static_cast<uint64_t>(a.a_rows) * a.k * 2u < (1ull << 32) &&
+                     static_cast<uint64_t>(a.w_rows) * a.k / 2u < (1ull << 32) &&
+                     static_cast<uint64_t>(a.s_rows) * a.n * 2u < (1ull << 32) &&
+                     mh::aligned(a.out0, 16) && (a.out1 == nullptr || mh::aligned(a.out1, 16));
     if constexpr (EPI == EPI_STORE) {
         if (bm == 32 && bn == 64) return launch_t<32, 2, 1, GATHER, EPI>(a, n_blocks, s);
         if (bm == 128 && bn == 64) return launch_t<128, 2, 1, GATHER, EPI>(a, n_blocks, s);
         if (bm == 128 && bn == 256) return launch_t<128, 2, 4, GATHER, EPI>(a, n_blocks, s);
+        if (seg && bn == 256) return launch_seg<kSegRBMax, kSegStages, 2, 1, GATHER, EPI>(a, n_blocks, s);
     } else {
         if (bm == 32 && bn == 64) return launch_t<32, 1, 2, GATHER, EPI>(a, n_blocks, s);
         if (bm == 128 && bn == 64) return launch_t<128, 1, 2, GATHER, EPI>(a, n_blocks, s);
         if (bm == 128 && bn == 128) return launch_t<128, 1, 4, GATHER, EPI>(a, n_blocks, s);
+        if (seg && bn == 128) return launch_seg<kSegRBMax, kSegStages, 1, 2, GATHER, EPI>(a, n_blocks, s);
     }
     return mh::set_error(MH_ERR_UNSUPPORTED, "grouped GEMM: no %ux%u tile for this form", bm, bn);
 }

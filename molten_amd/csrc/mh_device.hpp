@@ -33,6 +33,12 @@ __device__ __forceinline__ gbytes uniform_ptr(const void* p) {
     const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
     return reinterpret_cast<gbytes>((static_cast<uint64_t>(hi) << 32) | lo);
 }
+__device__ __forceinline__ gbytes uniform_ptr(gbytes p) {
+    const uint64_t u = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+    return reinterpret_cast<gbytes>((static_cast<uint64_t>(hi) << 32) | lo);
+}
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));

@@ -13,7 +13,7 @@
 
 namespace {
 
-constexpr uint32_t kBM = 128;      // row tile of both grouped GEMMs
+constexpr uint32_t kBM = 512;      // row tile of both grouped GEMMs (segment kernels)
 constexpr uint32_t kGuBN = 128;    // gate/up tile width (fused SwiGLU)
 constexpr uint32_t kDnBN = 256;    // down tile width
 

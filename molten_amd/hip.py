@@ -339,13 +339,16 @@ def moe_route_batch(logits, bias, ids, gw, m: int, e: int, topk: int,
 
 class MoeTile:
     """Row x column tile of a grouped GEMM block map (src/kernels/quant.rs:19-40).
-    T32 / T128 are the reference's shapes; GU128 / DN128 are the MI355X tiles
-    the fused prefill uses for gate/up and down."""
+    T32 / T128 are the reference's shapes; GU128 / DN128 are MI355X tiles of
+    128 rows; GU512 / DN512 map whole expert segments of up to 512 rows (the
+    segment kernels the fused prefill uses for gate/up and down)."""
 
     T32 = (32, 64)
     T128 = (128, 64)
     GU128 = (128, 128)
     DN128 = (128, 256)
+    GU512 = (512, 128)
+    DN512 = (512, 256)
 
 
 def moe_zero_counts(counts, e: int, stream=None) -> None:

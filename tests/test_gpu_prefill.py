@@ -119,15 +119,17 @@ def _map(orc, counts, bm, bn, n):
     return gu, max_e, offsets
 
 
-@pytest.mark.parametrize("tile", [(128, 256), (128, 64), (32, 64)])
+@pytest.mark.parametrize("tile", [(512, 256), (256, 256), (128, 256), (128, 64), (32, 64)])
 def test_grouped_gemm_one_hot_is_exact_dequant(dev, orc, tile):
     """A = unit rows: every output is one dequantized weight, so the in-register
     bf16(fma(s, q, b)) dequant must match the oracle's bit for bit."""
     bm, bn = tile
     rng = np.random.default_rng(bm + bn)
-    e, n, k = 3, 512, 2048
+    e, n, k = 4, 512, 2048
     w = layout.synth_quant(rng, e * n, k, 4)
-    counts = np.array([40, 0, 200], np.uint32)
+    # 300 rows: two balanced passes of the segment kernels (5 + 5 blocks);
+    # 513: two map entries at bm = 512, one of a single row
+    counts = np.array([40, 0, 300, 513], np.uint32)
     s = int(counts.sum())
     cols = rng.integers(0, k, s)
     a = np.zeros((s, k), np.uint16)
@@ -143,7 +145,7 @@ def test_grouped_gemm_one_hot_is_exact_dequant(dev, orc, tile):
             np.testing.assert_array_equal(got[i], deq[ex * n:(ex + 1) * n, cols[i]])
 
 
-@pytest.mark.parametrize("tile", [(128, 256), (128, 64), (32, 64)])
+@pytest.mark.parametrize("tile", [(512, 256), (256, 256), (128, 256), (128, 64), (32, 64)])
 def test_grouped_gemm_vs_oracle(dev, orc, tile):
     rng = np.random.default_rng(7 + tile[0] + tile[1])
     e, n, k = 8, 1024, 1536
@@ -161,7 +163,7 @@ def test_grouped_gemm_vs_oracle(dev, orc, tile):
     assert_close(from_dev(c, np.uint16), want, f"grouped gemm {tile}")
 
 
-@pytest.mark.parametrize("tile", [(128, 128), (128, 64), (32, 64)])
+@pytest.mark.parametrize("tile", [(512, 128), (256, 128), (128, 128), (128, 64), (32, 64)])
 def test_grouped_gate_up_and_fused_act(dev, orc, tile):
     rng = np.random.default_rng(11 + tile[0] + tile[1])
     e, n, k, t = 6, 512, 2048, 300
