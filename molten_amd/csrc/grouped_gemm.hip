@@ -109,6 +109,24 @@ __device__ __forceinline__ uint4 lds_read16(uint32_t addr) {
 __device__ __forceinline__ void dma16(mh::gbytes src, uint32_t lds_base) {
     __builtin_amdgcn_global_load_lds((glb_ptr)src, (lds_ptr)(uintptr_t)lds_base, 16, 0, 0);
 }
+// The same 16-byte load in the scalar-base form: base (uniform) + a 32-bit
+// per-lane offset, LDS destination lds_base (uniform) + 16 l.  M0 carries
+// the LDS address; it is saved and restored around the load, so the
+// compiler's own use of M0 is unaffected.  The compiler does not count this
+// load for its vmcnt waits (those can then only wait longer, never less);
+// the kernel waits for it explicitly.
+__device__ __forceinline__ void dma16s(mh::gbytes base, uint32_t voff, uint32_t lds_base) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(voff), "s"(base), "s"(lds_base)
+        : "memory");
+}
 // Direct-to-LDS 4-byte load: lane l's dword lands at lds_base + 4 l.
 __device__ __forceinline__ void dma4(mh::gbytes src, uint32_t lds_base) {
     __builtin_amdgcn_global_load_lds((glb_ptr)src, (lds_ptr)(uintptr_t)lds_base, 4, 0, 0);
@@ -455,18 +473,21 @@ struct SegLayout {
 //
 // Loads are direct-to-LDS and shaped for few L2 requests per 64-k stage:
 //   * A: RB*32 rows x 128 bytes (one line per row) into a 3-slot ring shared
-//     by the workgroup, 16-byte chunks XOR-swizzled by row;
+//     by the workgroup; chunk c of row r sits at position c ^ ((r >> 1) & 7),
+//     so a 16-byte read by 16 lanes (16 rows, one chunk each) covers all 64
+//     banks once;
 //   * B codes: every other stage, the next two stages' codes of each column
 //     (64 bytes, half a line; 4 lanes per column) into a per-wave region of
-//     one of two slots, chunks swizzled by ((column >> 1) & 3) so the MFMA
-//     operand reads (lane i32, half h, stage s: chunk 2s + h) are
-//     bank-conflict free;
+//     one of two slots, chunks swizzled by ((column >> 2) & 3) so the MFMA
+//     operand reads (lane i32, half h, stage s: chunk 2s + h; 16 lanes per
+//     64-bank cycle) are bank-conflict free;
 //   * scales and biases: every 8 stages, 16 bytes (8 groups) of the column's
 //     scale row (lanes 0-31) and bias row (lanes 32-63), two slots.
 // Stage g's loads ("group g": its A, plus the B half-block that starts at g,
-// plus the scale/bias block that starts at g) are issued at iteration g - 2,
-// so before stage kb is read the wave waits until only group kb + 1 may
-// still be in flight; one barrier per stage publishes everyone's loads.
+// plus the scale/bias block that starts at g) are issued after the barrier
+// that ends stage g - 3, two stages ahead of use; the wave waits for its own
+// loads of a group (vmcnt) and one barrier per stage publishes the A rows
+// of all four waves.
 template <int RB, int RBMAX, int NS, int NBW, int NMAT, bool GATHER, int EPI>
 __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint32_t n0,
                                          uint32_t mp0, uint32_t m_end, uint32_t lds0, int lane,
@@ -495,12 +516,12 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
         const uint32_t m = min(mp0 + r, m_end - 1u);
         uint32_t src = GATHER ? a.gather[m] : m;
         src = min(src, a.a_rows - 1u);
-        const uint32_t chunk = static_cast<uint32_t>(lane & 7) ^ (r & 7u);
+        const uint32_t chunk = static_cast<uint32_t>(lane & 7) ^ ((r >> 1) & 7u);
         aoffs[q] = src * K * 2u + chunk * 16u;
     }
     // B half-block load p of fragment t: columns 16p .. 16p + 15, lane l =
     // 4c' + q stores LDS chunk q of column c = 16p + c', holding global chunk
-    // q ^ ((c >> 1) & 3).  Scale/bias block: lane (i32, h) loads 16 bytes of
+    // q ^ ((c >> 2) & 3).  Scale/bias block: lane (i32, h) loads 16 bytes of
     // column i32's scale (h = 0) or bias (h = 1) row.
     uint32_t bcoffs[NB][2], sboff[NB];
 #pragma unroll
@@ -513,28 +534,28 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
             for (int p = 0; p < 2; ++p) {
                 const uint32_t c = 16u * p + static_cast<uint32_t>(lane >> 2);
                 const uint32_t r = min(col0 + c, a.w_rows - 1u);
-                const uint32_t g = static_cast<uint32_t>(lane & 3) ^ ((c >> 1) & 3u);
+                const uint32_t g = static_cast<uint32_t>(lane & 3) ^ ((c >> 2) & 3u);
                 bcoffs[t][p] = r * (K / 2u) + g * 16u;
             }
             sboff[t] = min(col0 + static_cast<uint32_t>(i32), a.w_rows - 1u) * groups * 2u;
         }
     }
     auto issue_group = [&](uint32_t g) {
-        const uint32_t abuf = lds0 + (g % 3u) * L::A_STAGE;
+        const uint32_t abuf = __builtin_amdgcn_readfirstlane(lds0 + (g % 3u) * L::A_STAGE + wave * QA * 1024u);
         const mh::gbytes ag = mh::uniform_ptr(abase + g * 128u);
 #pragma unroll
         for (int q = 0; q < QA; ++q) {
-            dma16(ag + aoffs[q], abuf + (wave * QA + q) * 1024u);
+            dma16s(ag, aoffs[q], abuf + q * 1024u);
         }
         if ((g & 1u) == 0) {
             const uint32_t hb = g >> 1;
-            const uint32_t bbuf = lds0 + L::B_OFF + (hb & 1u) * L::B_HALF + wave * NB * 2048u;
+            const uint32_t bbuf = __builtin_amdgcn_readfirstlane(lds0 + L::B_OFF + (hb & 1u) * L::B_HALF + wave * NB * 2048u);
 #pragma unroll
             for (int t = 0; t < NB; ++t) {
                 const mh::gbytes cg = mh::uniform_ptr(cbase[t / NBW] + hb * 64u);
 #pragma unroll
                 for (int p = 0; p < 2; ++p) {
-                    dma16(cg + bcoffs[t][p], bbuf + t * 2048u + p * 1024u);
+                    dma16s(cg, bcoffs[t][p], bbuf + t * 2048u + p * 1024u);
                 }
             }
         }
@@ -563,13 +584,15 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         aoff[j] = static_cast<uint32_t>(i32) * 128u +
-                  ((static_cast<uint32_t>(4 * h + j) ^ static_cast<uint32_t>(i32 & 7)) * 16u);
+                  ((static_cast<uint32_t>(4 * h + j) ^ ((static_cast<uint32_t>(i32) >> 1) & 7u)) * 16u);
     }
 
-    // Stage kb's inputs become readable once group kb has landed (only group
-    // kb + 1 may still be in flight) and every wave has passed a barrier.
-    auto wait_group = [&](uint32_t kb) {
-        const uint32_t g1 = kb + 1;
+    // Own loads of group g are complete once only the group after it may
+    // still be in flight.  B codes and scale/bias words sit in per-wave
+    // regions that only the wave's own loads fill, so they are readable then;
+    // A (loaded by all four waves) also needs a barrier.
+    auto wait_own = [&](uint32_t g) {
+        const uint32_t g1 = g + 1;
         if (g1 >= nkb) {
             wait_vmcnt<0>();
         } else if ((g1 & 7u) == 0) {
@@ -579,13 +602,11 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
         } else {
             wait_vmcnt<QA>();
         }
-        __builtin_amdgcn_s_barrier();
     };
-    // LDS reads of a stage's B codes (chunk 2 (kb % 2) + h of the lane's
-    // column), scale/bias words (group kb: word (kb % 8) / 2) and first
-    // A fragments; issued without waiting.
-    auto read_stage = [&](uint32_t kb, uint4 (&bc)[NB], uint32_t (&sbw)[2 * NB], uint4 (&av)[RB]) {
-        const uint32_t pos = ((2u * (kb & 1u) + static_cast<uint32_t>(h)) ^ ((static_cast<uint32_t>(i32) >> 1) & 3u)) * 16u;
+    // LDS reads (no wait) of stage kb's B codes (chunk 2 (kb % 2) + h of the
+    // lane's column) and scale/bias words (group kb: word (kb % 8) / 2)
+    auto read_bsb = [&](uint32_t kb, uint4 (&bc)[NB], uint32_t (&sbw)[2 * NB]) {
+        const uint32_t pos = ((2u * (kb & 1u) + static_cast<uint32_t>(h)) ^ ((static_cast<uint32_t>(i32) >> 2) & 3u)) * 16u;
         const uint32_t bl = lds0 + L::B_OFF + ((kb >> 1) & 1u) * L::B_HALF + wave * NB * 2048u + i32 * 64u + pos;
         static_for<NB>([&](auto t) { bc[t] = lds_read16_at<t * 2048>(bl); });
         const uint32_t sl = lds0 + L::SB_OFF + ((kb >> 3) & 1u) * L::SB_BLK + wave * NB * 1024u + i32 * 16u + ((kb & 7u) >> 1) * 4u;
@@ -593,7 +614,9 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
             sbw[2 * t] = lds_read4_at<t * 1024>(sl);
             sbw[2 * t + 1] = lds_read4_at<t * 1024 + 512>(sl);
         });
-        const uint32_t ab = lds0 + (kb % 3u) * L::A_STAGE + aoff[0];
+    };
+    auto read_a = [&](uint32_t kb, int j, uint4 (&av)[RB]) {
+        const uint32_t ab = lds0 + (kb % 3u) * L::A_STAGE + aoff[j];
         static_for<RB>([&](auto rb) { av[rb] = lds_read16_at<rb * 4096>(ab); });
     };
     float sf[NB], s16[NB], bf[NB];
@@ -607,40 +630,38 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
         }
     };
 
+    // Group g is issued after the barrier that ends stage g - 3 (the barrier
+    // frees that stage's A slot, which g reuses), groups 0..2 up front.
     issue_group(0);
     if (nkb > 1) {
         issue_group(1);
     }
+    uint4 bc[NB];
+    uint32_t sbw[2 * NB];
+    uint4 av[2][RB];
+    bf16x8_t bfr[2][NB];
+    wait_own(0);
+    read_bsb(0, bc, sbw);
+    lgkm_wait<0>(bc);
+    lgkm_wait<0>(sbw);
+    scale_bias(0, sbw);
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+        bfr[0][t] = deq_word(bc[t].x, sf[t], s16[t], bf[t]);
+    }
+    __builtin_amdgcn_s_barrier();
+    if (nkb > 2) {
+        issue_group(2);
+    }
+    read_a(0, 0, av[0]);
     for (uint32_t kb = 0; kb < nkb; ++kb) {
-        wait_group(kb);
-        if (kb + 2 < nkb) {
-            issue_group(kb + 2);
-        }
-        uint4 bc[NB];
-        uint32_t sbw[2 * NB];
-        uint4 av[2][RB];
-        read_stage(kb, bc, sbw, av[0]);
-        lgkm_wait<RB>(bc);
-        lgkm_wait<RB>(sbw);
-        scale_bias(kb, sbw);
-        bf16x8_t bfr[2][NB];
+        // steps 0..2: the next step's A reads in flight and its B words
+        // dequantized while this step's MFMAs run
 #pragma unroll
-        for (int t = 0; t < NB; ++t) {
-            bfr[0][t] = deq_word(bc[t].x, sf[t], s16[t], bf[t]);
-        }
-        const uint32_t base = lds0 + (kb % 3u) * L::A_STAGE;
-        // next step's A reads in flight and its B words dequantized while this
-        // step's MFMAs run
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 3; ++j) {
             const int cur = j & 1, nxt = cur ^ 1;
-            if (j < 3) {
-                const uint32_t ab = base + aoff[j + 1];
-                static_for<RB>([&](auto rb) { av[nxt][rb] = lds_read16_at<rb * 4096>(ab); });
-                lgkm_wait<RB>(av[cur]);
-            } else {
-                lgkm_wait<0>(av[cur]);
-            }
+            read_a(kb, j + 1, av[nxt]);
+            lgkm_wait<RB>(av[cur]);
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
                 const bf16x8_t af = __builtin_bit_cast(bf16x8_t, av[cur][rb]);
@@ -650,7 +671,7 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
                     for (int cb = 0; cb < NBW; ++cb)
                         acc[mat][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                             bfr[cur][mat * NBW + cb], af, acc[mat][rb][cb], 0, 0, 0);
-                if (j < 3 && rb == 0) {
+                if (rb == 0) {
 #pragma unroll
                     for (int t = 0; t < NB; ++t) {
                         const uint32_t wv = j == 0 ? bc[t].y : j == 1 ? bc[t].z : bc[t].w;
@@ -658,6 +679,42 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
                     }
                 }
             }
+        }
+        // step 3; under its MFMAs the wave reads stage kb + 1's B codes and
+        // scale/bias words (its own loads) and dequantizes that stage's step 0
+        const bool next = kb + 1 < nkb;
+        lgkm_wait<0>(av[1]);
+        if (next) {
+            wait_own(kb + 1);
+            read_bsb(kb + 1, bc, sbw);
+        }
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const bf16x8_t af = __builtin_bit_cast(bf16x8_t, av[1][rb]);
+#pragma unroll
+            for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+                for (int cb = 0; cb < NBW; ++cb)
+                    acc[mat][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        bfr[1][mat * NBW + cb], af, acc[mat][rb][cb], 0, 0, 0);
+            if (rb == (RB - 1) / 2 && next) {
+                lgkm_wait<0>(bc);
+                lgkm_wait<0>(sbw);
+                scale_bias(kb + 1, sbw);
+#pragma unroll
+                for (int t = 0; t < NB; ++t) {
+                    bfr[0][t] = deq_word(bc[t].x, sf[t], s16[t], bf[t]);
+                }
+            }
+        }
+        if (next) {
+            // every wave's group kb + 1 has landed and every wave is done with
+            // stage kb's A slot
+            __builtin_amdgcn_s_barrier();
+            if (kb + 3 < nkb) {
+                issue_group(kb + 3);
+            }
+            read_a(kb + 1, 0, av[0]);
         }
     }
     // every wave is done with the ring before another pass refills it
@@ -728,11 +785,61 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
     }
 }
 
+
+// Balanced workgroup -> entry mapping of the segment kernels.  A "group" is
+// nt consecutive map entries (one expert row tile across its column tiles,
+// which read the same A rows), weighted by its row count (0 for padding).
+// Groups are ranked by weight (descending, ties by index) and dealt to the
+// 8 XCDs in snake order (rank k -> XCD k % 8 on even rounds, 7 - k % 8 on
+// odd ones; slot k / 8), so XCD totals come out nearly equal and each XCD
+// runs its largest groups first; workgroup i (XCD i % 8, j = i / 8) takes
+// column tile j % nt of the group in slot j / nt of its XCD.  Every
+// workgroup computes the same ranking (a few hundred instructions; the
+// group weights go through the LDS, which is free before the pass starts).
+// Returns n_entries for padding workgroups.
+__device__ uint32_t balanced_entry(const uint4* blocks, uint32_t n_entries, uint32_t nt, char* lds,
+                                   int lane, int wave) {
+    uint32_t* wts = reinterpret_cast<uint32_t*>(lds);  // [C] group weights
+    __shared__ uint32_t s_group;
+    const uint32_t C = (n_entries + nt - 1u) / nt;
+    const uint32_t x = blockIdx.x % 8u, j = blockIdx.x / 8u, slot = j / nt;
+    const uint32_t k_target = slot * 8u + ((slot & 1u) ? 7u - x : x);
+    for (uint32_t c = threadIdx.x; c < C; c += blockDim.x) {
+        const uint4 e = blocks[c * nt];
+        wts[c] = e.x < e.w ? e.w - e.x : 0u;
+    }
+    if (threadIdx.x == 0) {
+        s_group = 0xffffffffu;
+    }
+    __syncthreads();
+    if (k_target < C) {
+        for (uint32_t c = threadIdx.x; c < C; c += blockDim.x) {
+            const uint32_t w = wts[c];
+            uint32_t rank = 0;
+            for (uint32_t d = 0; d < C; ++d) {
+                const uint32_t v = wts[d];
+                rank += (v > w || (v == w && d < c)) ? 1u : 0u;
+            }
+            if (rank == k_target) {
+                s_group = c;
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t g = s_group;
+    (void)lane;
+    (void)wave;
+    return g == 0xffffffffu ? n_entries : g * nt + j % nt;
+}
+
 template <int RBMAX, int NS, int NBW, int NMAT, bool GATHER, int EPI>
 __global__ __launch_bounds__(kSegWaves * 64, (SegLayout<RBMAX, NBW, NMAT, NS>::LDS <= 80 * 1024 ? 2 : 1))
 void k_seg(GemmArgs a, uint32_t n_entries) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const uint32_t ent = entry_of_block(a.n / (kSegWaves * NBW * 32u));
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lds0 = static_cast<uint32_t>((uintptr_t)((lds_ptr)lds));
+    const uint32_t ent = balanced_entry(a.blocks, n_entries, a.n / (kSegWaves * NBW * 32u), lds, lane, wave);
     if (ent >= n_entries) {
         return;
     }
@@ -741,9 +848,6 @@ void k_seg(GemmArgs a, uint32_t n_entries) {
     if (m0 >= m_end) {
         return;
     }
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t lds0 = static_cast<uint32_t>((uintptr_t)((lds_ptr)lds));
     const uint32_t nrb = (m_end - m0 + 31u) / 32u;
     const uint32_t passes = (nrb + RBMAX - 1u) / RBMAX;
     uint32_t mp0 = m0;
@@ -760,6 +864,7 @@ void k_seg(GemmArgs a, uint32_t n_entries) {
         switch (rb) {
             MH_SEG_CASE(1) MH_SEG_CASE(2) MH_SEG_CASE(3) MH_SEG_CASE(4)
             MH_SEG_CASE(5) MH_SEG_CASE(6) MH_SEG_CASE(7) MH_SEG_CASE(8)
+            MH_SEG_CASE(9)
             default: break;
         }
 #undef MH_SEG_CASE
