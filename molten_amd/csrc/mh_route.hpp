@@ -100,25 +100,23 @@ __device__ inline void route_select(const float* s, const float* cand, uint32_t 
     }
 }
 
-// route_select with the scores in registers: lane l holds expert l + 64 j in
-// s[j] / cand[j] (cand -inf where l + 64 j >= e).  Same selection rule and
-// weight arithmetic as route_select; every lane of the wave returns the ids
-// and the bf16 weight bits (wave-uniform).  With e <= 64 a lane holds one
-// candidate and the lowest id among the lanes holding the maximum is the
-// lowest set bit of a ballot.  The weights are computed one slot per lane and
-// the denominator is summed slot by slot in order, as in route_select.
-template <int TK>
-__device__ inline void route_select_regs(const float (&s)[kMaxExperts / 64], const float (&cand)[kMaxExperts / 64],
-                                         uint32_t e, int mode, float eps, uint32_t (&ids)[TK],
-                                         uint32_t (&wbits)[TK]) {
-    constexpr int kPerLane = kMaxExperts / 64;
+// route_select's choice with the scores in registers: lane l holds expert
+// l + 64 j in s[j] / cand[j] for j < EB (cand -inf where l + 64 j >= e).
+// Same selection rule as route_select; every lane returns the ids and the
+// chosen experts' scores sv (wave-uniform), from which route_weights_regs
+// computes the weights.  With EB == 1 (e <= 64) a lane holds one candidate
+// and the lowest id among the lanes holding the maximum is the lowest set bit
+// of a ballot.
+template <int TK, int EB>
+__device__ inline void route_select_ids(const float (&s)[EB], const float (&cand)[EB], uint32_t (&ids)[TK],
+                                        float (&sv)[TK]) {
+    static_assert(EB >= 1 && EB <= kMaxExperts / 64, "experts per lane");
     const uint32_t lane = threadIdx.x & 63u;
     uint32_t used = 0;
-    float sv[TK];
 #pragma unroll
     for (int r = 0; r < TK; ++r) {
         uint32_t pick;
-        if (e <= 64u) {
+        if (EB == 1) {
             const float v = (used & 1u) ? -__builtin_inff() : cand[0];
             const float m = wave_max_f32(v);
             const unsigned long long hit = __ballot(v == m);
@@ -127,14 +125,13 @@ __device__ inline void route_select_regs(const float (&s)[kMaxExperts / 64], con
             float bv = -__builtin_inff();
             uint32_t bi = 0xffffffffu;
 #pragma unroll
-            for (int j = 0; j < kPerLane; ++j) {
-                if (64u * j < e) {
-                    // ids rise with j, so a strict > keeps the lowest id on ties
-                    const float v = cand[j];
-                    const bool take = !((used >> j) & 1u) && v > bv;
-                    bv = take ? v : bv;
-                    bi = take ? lane + 64u * j : bi;
-                }
+            for (int j = 0; j < EB; ++j) {
+                // ids rise with j, so a strict > keeps the lowest id on ties;
+                // -inf (absent experts) and NaN are never taken
+                const float v = cand[j];
+                const bool take = !((used >> j) & 1u) && v > bv;
+                bv = take ? v : bv;
+                bi = take ? lane + 64u * j : bi;
             }
             const float m = wave_max_f32(bv);
             bi = m > -__builtin_inff() ? wave_min_u32(bv == m ? bi : 0xffffffffu) : 0xffffffffu;
@@ -142,14 +139,27 @@ __device__ inline void route_select_regs(const float (&s)[kMaxExperts / 64], con
         }
         pick = __builtin_amdgcn_readfirstlane(pick);
         ids[r] = pick;
+        // the chosen score: each block's lane value, then a uniform select
+        // (the opaque copies keep the compiler from indexing an array in
+        // private memory instead)
         float mine = s[0];
 #pragma unroll
-        for (int j = 1; j < kPerLane; ++j) {
-            mine = (pick >> 6) == static_cast<uint32_t>(j) ? s[j] : mine;
+        for (int j = 1; j < EB; ++j) {
+            float sj = s[j];
+            asm volatile("" : "+v"(sj));
+            mine = (pick >> 6) == static_cast<uint32_t>(j) ? sj : mine;
         }
         sv[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), pick & 63u));
         used |= (pick & 63u) == lane ? 1u << (pick >> 6) : 0u;
     }
+}
+
+// route_select's weight arithmetic on the chosen scores sv (wave-uniform):
+// one slot per lane, the denominator summed slot by slot in order; returns
+// the bf16 weight bits of every slot (wave-uniform).
+template <int TK>
+__device__ inline void route_weights_regs(const float (&sv)[TK], int mode, float eps, uint32_t (&wbits)[TK]) {
+    const uint32_t lane = threadIdx.x & 63u;
     float my = sv[0];
 #pragma unroll
     for (int r = 1; r < TK; ++r) {

@@ -3,27 +3,31 @@
 //
 // kGrid workgroups of kWaves waves (one per CU on a 256-CU part, all
 // resident at once) run three phases:
-//   1. router logits, one row per wave, spread over the workgroups;
+//   1. router logits: wave 0 of workgroup e computes row e;
 //   2. every wave routes the token itself (from the logits, in registers),
-//      issues the loads of its down-projection rows, then computes pairs of
-//      gate/up rows of the chosen experts and their SwiGLU activations;
+//      computes three SwiGLU activations (three gate rows and three up rows
+//      of the chosen experts), then issues the loads of its down-projection
+//      rows;
 //   3. each workgroup stages all activations in LDS and each wave produces
 //      one output of the down projection + weighted combine.
 // Same arithmetic (chunk order, roundings) as the three-launch path in
 // moe_decode.hip, so outputs are bit-identical to it and to the oracle.
 //
-// Cross-workgroup exchange without grid barriers: a logit, or a pair of
-// activations, travels as one 64-bit word {data, epoch} written with a single
+// Cross-workgroup exchange without grid barriers: a logit, or three
+// activations, travel as one 64-bit word {data, tag} written with a single
 // device-coherent store; a consumer polls the words it needs with
-// device-coherent loads until each carries the current launch's epoch.  Data
+// device-coherent loads until each carries the current launch's tag.  Data
 // and tag arrive together, so there is no store-acknowledge wait and no
-// arrival counter on the critical path.  Only wave 0 of a workgroup polls
-// (with a pause between rounds), so the polls do not crowd out the stores
-// they wait for.  The epoch: workgroup b keeps a launch count in scratch
-// word b, reads it at its start and writes it back plus one; every launch
-// runs all kGrid workgroups once, so the counts advance in lockstep and all
-// workgroups of a launch see the same value.  epoch = count + 1 (32-bit,
-// never 0, so zeroed words never match, and consecutive launches differ).
+// arrival counter on the critical path.  The logits are stored kReplicas
+// times (one copy per XCD: workgroup b reads copy b % kReplicas), so the
+// pollers of a copy are the 32 workgroups of one XCD.  The epoch: workgroup
+// b keeps a launch count in scratch word b, reads it at its start and writes
+// it back plus one; every launch runs all kGrid workgroups once, so the
+// counts advance in lockstep and all workgroups of a launch see the same
+// value.  epoch = count + 1 (32-bit, never 0, so zeroed words never match,
+// and consecutive launches differ); activation words carry the 16-bit tag
+// epoch % 65535 + 1 (never 0; every launch rewrites every word it reads, so
+// a word's previous tag is the previous launch's).
 //
 // Replaces the decode sequence of src/lfm.rs:967-1011 (router_addnorm_route,
 // gemv_gather_act, gemv_gather_down_combine4).
@@ -36,18 +40,21 @@ namespace {
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr uint32_t kGrid = 256;
+constexpr uint32_t kReplicas = 8;   // logit copies, one per XCD
+constexpr int kPollWave = 1;        // polls the logits (wave 0 has the router row's stores in flight)
 // scratch layout (u32 words)
-constexpr uint32_t kEpochWords = 0;       // [kGrid] launch counts
-constexpr uint32_t kLogitWords = 512;     // [kMaxExperts] tagged logits (64-bit)
-constexpr uint32_t kActWords = 1024;      // [kMaxAct / 2] tagged activation pairs (64-bit)
-constexpr int kPairs = 2;          // gate/up row pairs a wave has in flight
+constexpr uint32_t kEpochWords = 0;       // [kGrid] launch counts (word 256: the three-launch path's counter)
+constexpr uint32_t kLogitWords = 512;     // kReplicas x [kMaxExperts] tagged logits (64-bit)
+constexpr uint32_t kLogitStride = 2u * mh::kMaxExperts;
+constexpr uint32_t kActWords = kLogitWords + kReplicas * kLogitStride;  // tagged activation triples (64-bit)
 constexpr int kMaxTk = 4;
 constexpr uint32_t kMaxAct = 8192;  // bf16 activations staged per workgroup (16 KB)
+constexpr uint32_t kMaxTriples = ((kMaxAct + 2u) / 3u + 1u) / 2u * 2u;  // ceil(kMaxAct / 3), rounded up to even
 constexpr uint32_t kSpinLimit = 1u << 20;
-constexpr uint32_t kSample = 64;          // activation words wave 0 watches before the full read
-static_assert(kGrid <= 256 && kLogitWords + 2u * mh::kMaxExperts <= kActWords &&
-                  kActWords + kMaxAct <= MH_MOE_DECODE_SCRATCH_WORDS,
-              "scratch layout (word 256 is the three-launch path's counter)");
+constexpr int kReadsPerThread = (kMaxTriples / 2 + kThreads - 1) / kThreads;  // 16-byte reads
+static_assert(kMaxTriples % 2 == 0 && 3u * kMaxTriples >= kMaxAct && mh::kMaxExperts <= kGrid &&
+                  kActWords + 2u * kMaxTriples <= MH_MOE_DECODE_SCRATCH_WORDS,
+              "scratch layout");
 
 struct FusedArgs {
     const void* rw;        // router [E, K], f32 or bf16
@@ -63,22 +70,37 @@ struct FusedArgs {
     uint16_t* weights;     // [topk]
     uint16_t* act;         // [topk, NI]
     uint16_t* out;         // [K]
-    uint32_t* scratch;     // launch counts, tagged logits, tagged activation pairs
+    uint32_t* scratch;     // launch counts, tagged logits, tagged activation triples
     uint32_t E, K, NI, gs;
 };
 
-__device__ __forceinline__ void put_tagged(uint32_t* scratch, uint32_t word, uint32_t data, uint32_t epoch) {
-    __hip_atomic_store(reinterpret_cast<uint64_t*>(scratch) + word,
-                       (static_cast<uint64_t>(epoch) << 32) | data, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void put_tagged(uint32_t* scratch, uint32_t word, uint64_t v) {
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(scratch) + word, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint64_t get_tagged(const uint32_t* scratch, uint32_t word) {
     return __hip_atomic_load(reinterpret_cast<const uint64_t*>(scratch) + word, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ bool fresh(uint64_t w, uint32_t epoch) { return static_cast<uint32_t>(w >> 32) == epoch; }
 
-template <typename WT, int TK>
+// Three device-coherent 16-byte loads (the same cache policy as the 64-bit
+// atomic loads above: sc1) and the wait for them.  Each 64-bit half is
+// checked for its tag by the caller, so a half read before its store simply
+// fails the check.
+__device__ __forceinline__ void load3_coherent(const uint32_t* p0, const uint32_t* p1, const uint32_t* p2,
+                                               mh::u32x4& a, mh::u32x4& b, mh::u32x4& c) {
+    asm volatile(
+        "global_load_dwordx4 %0, %3, off sc1\n\t"
+        "global_load_dwordx4 %1, %4, off sc1\n\t"
+        "global_load_dwordx4 %2, %5, off sc1\n\t"
+        "s_waitcnt vmcnt(0)"
+        : "=&v"(a), "=&v"(b), "=&v"(c)
+        : "v"(p0), "v"(p1), "v"(p2)
+        : "memory");
+}
+
+template <typename WT, int TK, int EB>
 __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
+    static_assert(kReadsPerThread == 3, "load3_coherent covers a thread's share");
     __shared__ __attribute__((aligned(16))) uint16_t act_l[kMaxAct];
     __shared__ __attribute__((aligned(16))) float actf_l[kMaxAct];
     __shared__ float xs_l[kMaxAct / 32];
@@ -92,60 +114,88 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
     const bool live = lane < static_cast<int>(C);
     const uint32_t c = live ? lane : 0u;
     uint32_t* const tl = a.scratch + kLogitWords;  // tagged logits (64-bit words)
-    uint32_t* const ta = a.scratch + kActWords;    // tagged activation pairs
+    uint32_t* const ta = a.scratch + kActWords;    // tagged activation triples
 
-    if (threadIdx.x == 0) {
-        uint32_t* cnt = a.scratch + kEpochWords + blockIdx.x;
-        const uint32_t n = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-        __hip_atomic_store(cnt, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        epoch_l = n;
-        bad_l = 0u;
-    }
+    // ---- phase 1: router logits; row e is computed by wave 0 of workgroup e
+    // (e < kMaxExperts <= kGrid).  Wave 0 issues the read of the launch
+    // count first and waits for it with the router's loads (loads complete
+    // in order), so the two round trips overlap.
+    const uint32_t re = blockIdx.x;
     uint32_t xw[16];
     mh::load_x_words(a.x + 32u * c, xw);
-
-    // ---- phase 1: router logits; row e is computed by wave e / kGrid of
-    // workgroup e % kGrid, so the router reads are spread over many CUs
-    const uint32_t re = blockIdx.x + static_cast<uint32_t>(wave) * kGrid;
-    const bool router = re < a.E;
-    float logit = 0.0f;
-    if (router) {
-        mh::RowWords<WT> rw;
-        rw.load(static_cast<const WT*>(a.rw) + static_cast<size_t>(re) * a.K + 32u * c);
-        float xr[32], xs, wr[32];
-        mh::x_words_to_f32(xw, xr, xs);
-        rw.to_f32(wr);
-        float p = 0.0f;
+    float bias_r[EB];
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            p = __builtin_fmaf(wr[i], xr[i], p);
+    for (int j = 0; j < EB; ++j) {
+        const uint32_t i = lane + 64u * j;
+        bias_r[j] = a.bias != nullptr && i < a.E ? a.bias[i] : 0.0f;
+    }
+    float logit = 0.0f;
+    uint32_t epoch = 0;
+    if (wave == 0) {
+        uint32_t count;
+        asm volatile("global_load_dword %0, %1, off sc1"
+                     : "=v"(count)
+                     : "v"(a.scratch + kEpochWords + blockIdx.x)
+                     : "memory");
+        if (re < a.E) {
+            mh::RowWords<WT> rw;
+            rw.load(static_cast<const WT*>(a.rw) + static_cast<size_t>(re) * a.K + 32u * c);
+            float xr[32], xs, wr[32];
+            mh::x_words_to_f32(xw, xr, xs);
+            rw.to_f32(wr);
+            float p = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                p = __builtin_fmaf(wr[i], xr[i], p);
+            }
+            float h[4] = {live ? 0.0f + p : 0.0f, 0.0f, 0.0f, 0.0f};
+            logit = mh::reduce_rows4(h, lane);
         }
-        float h[4] = {live ? 0.0f + p : 0.0f, 0.0f, 0.0f, 0.0f};
-        logit = mh::reduce_rows4(h, lane);
+        asm volatile("s_waitcnt vmcnt(0)" : "+v"(count) : : "memory");
+        epoch = count + 1u;
+    }
+    // x and the bias are in registers from here on, before any store: no
+    // later use waits again (behind this wave's stores)
+    mh::x_words_fence(xw);
+#pragma unroll
+    for (int j = 0; j < EB; ++j) {
+        asm volatile("" : "+v"(bias_r[j]));
+    }
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(a.scratch + kEpochWords + blockIdx.x, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        epoch_l = epoch;
+        bad_l = 0u;
     }
     __syncthreads();  // epoch_l
-    const uint32_t epoch = epoch_l;
-    if (router && lane == 60) {
-        put_tagged(tl, re, __float_as_uint(logit), epoch);
+    epoch = epoch_l;
+    if (wave == 0 && re < a.E && lane == 60) {
+        const uint64_t word = (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(logit);
+#pragma unroll
+        for (uint32_t rp = 0; rp < kReplicas; ++rp) {
+            put_tagged(tl + rp * kLogitStride, re, word);
+        }
         a.logits[re] = logit;
     }
 
-    // ---- routing: wave 0 polls the tagged logits into LDS, then every wave
-    // routes the token itself
-    uint32_t ex[TK], wb[TK];
-    bool ok = true;
-    if (wave == 0) {
+    // ---- routing: one wave polls this XCD's copy of the tagged logits into
+    // LDS, then every wave chooses the experts itself
+    uint32_t ex[TK];
+    float exs[TK];     // the chosen experts' scores
+    uint32_t exv = 0;  // lane r < TK: ex[r] (read back with a lane-select, not an indexed array)
+    if (wave == kPollWave) {
+        const uint32_t* rep = tl + (blockIdx.x % kReplicas) * kLogitStride;
         uint32_t pending = 0;
-        for (uint32_t i = lane; i < a.E; i += 64u) {
-            pending |= 1u << (i / 64u);
+#pragma unroll
+        for (int j = 0; j < EB; ++j) {
+            pending |= lane + 64u * j < a.E ? 1u << j : 0u;
         }
         uint32_t spins = 0;
         while (__any(pending != 0u) && spins < kSpinLimit) {
 #pragma unroll
-            for (int j = 0; j < mh::kMaxExperts / 64; ++j) {
+            for (int j = 0; j < EB; ++j) {
                 if ((pending >> j) & 1u) {
-                    const uint64_t w = get_tagged(tl, lane + 64u * j);
-                    if (fresh(w, epoch)) {
+                    const uint64_t w = get_tagged(rep, lane + 64u * j);
+                    if (static_cast<uint32_t>(w >> 32) == epoch) {
                         logit_l[lane + 64u * j] = __uint_as_float(static_cast<uint32_t>(w));
                         pending &= ~(1u << j);
                     }
@@ -159,33 +209,125 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
         }
     }
     __syncthreads();
-    ok = bad_l == 0u;
+    bool ok = bad_l == 0u;
     {
-        constexpr int kPerLane = mh::kMaxExperts / 64;
-        float sc[kPerLane], cd[kPerLane];
+        float sc[EB], cd[EB];
 #pragma unroll
-        for (int j = 0; j < kPerLane; ++j) {
+        for (int j = 0; j < EB; ++j) {
             const uint32_t i = lane + 64u * j;
             sc[j] = 0.0f;
             cd[j] = -__builtin_inff();
-            if (64u * j < a.E && i < a.E) {
-                mh::route_score(logit_l[i], a.bias ? a.bias[i] : 0.0f, a.mode, sc[j], cd[j]);
+            if (i < a.E) {
+                mh::route_score(logit_l[i], bias_r[j], a.mode, sc[j], cd[j]);
             }
         }
-        mh::route_select_regs<TK>(sc, cd, a.E, a.mode, a.eps, ex, wb);
-        if (gw == 0 && lane < TK) {
-            uint32_t id = ex[0], w = wb[0];
+        mh::route_select_ids<TK, EB>(sc, cd, ex, exs);
+        exv = ex[0];
 #pragma unroll
-            for (int r = 1; r < TK; ++r) {
-                id = lane == r ? ex[r] : id;
-                w = lane == r ? wb[r] : w;
-            }
-            a.ids[lane] = id;
-            a.weights[lane] = static_cast<uint16_t>(w);
+        for (int r = 1; r < TK; ++r) {
+            exv = lane == r ? ex[r] : exv;
         }
     }
 
-    // ---- this wave's down rows (output gw), loaded now, used in phase 3
+    // ---- phase 2: gate/up + SwiGLU on triples of activations: triple t is
+    // activations 3t .. 3t+2 of the flattened [TK, NI] block (its six rows'
+    // dot products share two 4-row butterflies); triples gw, gw + nw, ...
+    // A triple's loads go out row by row (codes, scale, bias) and its dots
+    // are taken in the same order, so each waits only for its own row.
+    const uint32_t acts = TK * a.NI;
+    const uint32_t triples = (acts + 2u) / 3u;
+    const uint32_t row_bytes = a.K / 2u;
+    const uint32_t G = a.K / a.gs;
+    const uint32_t gc = (32u * c) / a.gs;
+    mh::Chunk<4> ch[6];
+    uint16_t sv[6], bv[6];
+    auto load_triple = [&](uint32_t t) {
+        // activations past the end (last triple) load a valid row and are
+        // never stored
+        const uint32_t slot0 = (3u * t) / a.NI;
+        const uint32_t i0 = 3u * t - slot0 * a.NI;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const bool wrap = i0 + j >= a.NI;
+            const bool past = 3u * t + j >= acts;
+            const uint32_t slot = past ? slot0 : slot0 + (wrap ? 1u : 0u);
+            const uint32_t i = past ? i0 : i0 + j - (wrap ? a.NI : 0u);
+            const uint32_t e = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(exv), slot));
+            const size_t row = static_cast<size_t>(e) * a.NI + i;
+            const size_t sbi = row * G + gc;
+            ch[2 * j].load_nt(mh::uniform_ptr(reinterpret_cast<const char*>(a.gc) + row * row_bytes), c * 16u);
+            sv[2 * j] = a.gsc[sbi];
+            bv[2 * j] = a.gbi[sbi];
+            ch[2 * j + 1].load_nt(mh::uniform_ptr(reinterpret_cast<const char*>(a.uc) + row * row_bytes), c * 16u);
+            sv[2 * j + 1] = a.usc[sbi];
+            bv[2 * j + 1] = a.ubi[sbi];
+        }
+    };
+    uint32_t t = gw;
+    if (t < triples) {
+        load_triple(t);
+    }
+
+    // routing weights, off the gate/up loads' path
+    uint32_t wb[TK];
+    mh::route_weights_regs<TK>(exs, a.mode, a.eps, wb);
+    if (gw == 0 && lane < TK) {
+        uint32_t w = wb[0];
+#pragma unroll
+        for (int r = 1; r < TK; ++r) {
+            w = lane == r ? wb[r] : w;
+        }
+        a.ids[lane] = exv;
+        a.weights[lane] = static_cast<uint16_t>(w);
+    }
+
+    const uint32_t tag = epoch % 65535u + 1u;
+    {
+        float xr[32], xs;
+        mh::x_words_to_f32(xw, xr, xs);
+        mh::q4_scale_x(xr);
+        while (t < triples) {
+            float h[8];
+#pragma unroll
+            for (int q = 0; q < 6; ++q) {
+                const float d = ch[q].dot(xr);
+                const float hv = __builtin_fmaf(mh::bf16_to_f32(sv[q]), d, mh::bf16_to_f32(bv[q]) * xs);
+                h[q] = live ? 0.0f + hv : 0.0f;
+            }
+            h[6] = h[7] = 0.0f;
+            const float h0[4] = {h[0], h[1], h[2], h[3]}, h1[4] = {h[4], h[5], h[6], h[7]};
+            const int v0 = __float_as_int(mh::reduce_rows4(h0, lane));
+            const int v1 = __float_as_int(mh::reduce_rows4(h1, lane));
+            // the three SwiGLUs side by side: lane j < 3 takes activation j
+            const int g0 = __builtin_amdgcn_readlane(v0, 60), u0 = __builtin_amdgcn_readlane(v0, 61);
+            const int g1 = __builtin_amdgcn_readlane(v0, 62), u1 = __builtin_amdgcn_readlane(v0, 63);
+            const int g2 = __builtin_amdgcn_readlane(v1, 60), u2 = __builtin_amdgcn_readlane(v1, 61);
+            const float g = __int_as_float(lane == 0 ? g0 : lane == 1 ? g1 : g2);
+            const float u = __int_as_float(lane == 0 ? u0 : lane == 1 ? u1 : u2);
+            const int av = static_cast<int>(mh::f32_to_bf16(mh::silu_bf16(mh::round_bf16(g)) * mh::round_bf16(u)));
+            const uint32_t a0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(av, 0));
+            const uint32_t a1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(av, 1));
+            const uint32_t a2 = static_cast<uint32_t>(__builtin_amdgcn_readlane(av, 2));
+            if (lane == 0) {
+                put_tagged(ta, t, (static_cast<uint64_t>(a2 | (tag << 16)) << 32) | a0 | (a1 << 16));
+                a.act[3u * t] = static_cast<uint16_t>(a0);
+                if (3u * t + 1u < acts) {
+                    a.act[3u * t + 1u] = static_cast<uint16_t>(a1);
+                }
+                if (3u * t + 2u < acts) {
+                    a.act[3u * t + 2u] = static_cast<uint16_t>(a2);
+                }
+            }
+            t += nw;
+            if (t < triples) {
+                load_triple(t);
+            }
+        }
+    }
+
+    // ---- this wave's down rows (output gw), loaded once its gate/up rows
+    // are in (they are not needed before the activations arrive), used in
+    // phase 3
     const uint32_t CD = a.NI / 32u;
     const bool dlive = lane < static_cast<int>(CD);
     const uint32_t cd = dlive ? lane : 0u;
@@ -204,136 +346,73 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
         }
     }
 
-    // ---- phase 2: gate/up + SwiGLU on pairs of rows (2p, 2p + 1) of one
-    // slot, pairs gw, gw + nw, ...; the gate and up dot products of a pair
-    // share one 4-row butterfly
-    const uint32_t pairs = TK * a.NI / 2u;
+    // ---- phase 3: once the workgroup's own activations are out, every
+    // thread polls its share of the activation words (16 bytes at a time)
+    // into LDS, then one down output per wave with the combine.  (The down
+    // rows arrive while the words are polled.)  Waves that finish early do
+    // not start polling alone: their rounds would only load the memory
+    // system the workgroup's remaining gate/up rows are streaming through.
     {
-        float xr[32], xs;
-        mh::x_words_to_f32(xw, xr, xs);
-        mh::q4_scale_x(xr);
-        const uint32_t row_bytes = a.K / 2u;
-        const uint32_t G = a.K / a.gs;
-        const uint32_t gc = (32u * c) / a.gs;
-        for (uint32_t p0 = gw; p0 < pairs; p0 += nw * kPairs) {
-            mh::Chunk<4> ch[kPairs][4];
-            uint16_t sv[kPairs][4], bv[kPairs][4];
-#pragma unroll
-            for (int k = 0; k < kPairs; ++k) {
-                const uint32_t p = p0 + k * nw;
-                if (p < pairs) {
-                    const uint32_t slot = (2u * p) / a.NI;
-                    uint32_t e = ex[0];
-#pragma unroll
-                    for (int r = 1; r < TK; ++r) {
-                        e = slot == static_cast<uint32_t>(r) ? ex[r] : e;
-                    }
-                    const size_t row0 = static_cast<size_t>(e) * a.NI + (2u * p - slot * a.NI);
-                    const mh::gbytes gb = mh::uniform_ptr(reinterpret_cast<const char*>(a.gc) + row0 * row_bytes);
-                    const mh::gbytes ub = mh::uniform_ptr(reinterpret_cast<const char*>(a.uc) + row0 * row_bytes);
-#pragma unroll
-                    for (int r = 0; r < 2; ++r) {
-                        ch[k][2 * r].load_nt(gb, r * row_bytes + c * 16u);
-                        ch[k][2 * r + 1].load_nt(ub, r * row_bytes + c * 16u);
-                        const size_t sbi = (row0 + r) * G + gc;
-                        sv[k][2 * r] = a.gsc[sbi]; bv[k][2 * r] = a.gbi[sbi];
-                        sv[k][2 * r + 1] = a.usc[sbi]; bv[k][2 * r + 1] = a.ubi[sbi];
-                    }
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < kPairs; ++k) {
-                const uint32_t p = p0 + k * nw;
-                if (p < pairs) {
-                    float h[4];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const float d = ch[k][q].dot(xr);
-                        const float hv = __builtin_fmaf(mh::bf16_to_f32(sv[k][q]), d, mh::bf16_to_f32(bv[k][q]) * xs);
-                        h[q] = live ? 0.0f + hv : 0.0f;
-                    }
-                    const int v = __float_as_int(mh::reduce_rows4(h, lane));
-                    uint32_t word = 0;
-#pragma unroll
-                    for (int r = 0; r < 2; ++r) {
-                        const float g = mh::round_bf16(__int_as_float(__builtin_amdgcn_readlane(v, 60 + 2 * r)));
-                        const float u = mh::round_bf16(__int_as_float(__builtin_amdgcn_readlane(v, 61 + 2 * r)));
-                        word |= static_cast<uint32_t>(mh::f32_to_bf16(mh::silu_bf16(g) * u)) << (16 * r);
-                    }
-                    if (lane == 0) {
-                        put_tagged(ta, p, word, epoch);
-                        reinterpret_cast<uint32_t*>(a.act)[p] = word;
-                    }
-                }
-            }
-        }
-    }
-
-    // ---- phase 3: wave 0 watches kSample activation words spread over the
-    // buffer; once they are all current every thread reads its share (all of
-    // a thread's loads in flight together, stragglers polled again), then one
-    // down output per wave with the combine
-    {
-        if (wave == 0) {
-            const uint32_t i = static_cast<uint32_t>(lane) * pairs / kSample;
-            bool got = static_cast<uint32_t>(lane) >= kSample;
-            uint32_t spins = 0;
-            while (!__all(got) && spins < kSpinLimit) {
-                if (!got) {
-                    got = fresh(get_tagged(ta, i), epoch);
-                }
-                ++spins;
-                __builtin_amdgcn_s_sleep(1);
-            }
-        }
         __syncthreads();
-        constexpr int kPer = kMaxAct / 2 / kThreads;  // tagged words per thread
-        uint32_t pending = 0, vals[kPer];
+        // thread's 16-byte reads q = threadIdx.x + k * kThreads hold triples
+        // 2q and 2q + 1; bit 2k + h of pending: triple 2q + h not yet current
+        const uint32_t pairs = (triples + 1u) / 2u;
+        uint32_t pending = 0;
+        const uint32_t* src[kReadsPerThread];
 #pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-            pending |= threadIdx.x + q * kThreads < pairs ? 1u << q : 0u;
-            vals[q] = 0;
+        for (int k = 0; k < kReadsPerThread; ++k) {
+            const uint32_t q = threadIdx.x + k * kThreads;
+            src[k] = ta + 4u * (q < pairs ? q : 0u);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                pending |= q < pairs && 2u * q + h < triples ? 1u << (2 * k + h) : 0u;
+            }
         }
+        auto take = [&](const mh::u32x4 (&v)[kReadsPerThread]) {
+#pragma unroll
+            for (int k = 0; k < kReadsPerThread; ++k) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t lo = h ? v[k].z : v[k].x, hi = h ? v[k].w : v[k].y;
+                    if (((pending >> (2 * k + h)) & 1u) && (hi >> 16) == tag) {
+                        const uint32_t tr = 2u * (threadIdx.x + k * kThreads) + h;
+                        act_l[3u * tr] = static_cast<uint16_t>(lo);
+                        if (3u * tr + 1u < acts) {
+                            act_l[3u * tr + 1u] = static_cast<uint16_t>(lo >> 16);
+                        }
+                        if (3u * tr + 2u < acts) {
+                            act_l[3u * tr + 2u] = static_cast<uint16_t>(hi);
+                        }
+                        pending &= ~(1u << (2 * k + h));
+                    }
+                }
+            }
+        };
         uint32_t spins = 0;
         while (pending != 0u && spins < kSpinLimit) {
-            uint64_t w[kPer];
-#pragma unroll
-            for (int q = 0; q < kPer; ++q) {
-                if ((pending >> q) & 1u) {
-                    w[q] = get_tagged(ta, threadIdx.x + q * kThreads);
-                }
+            if (spins != 0u) {
+                __builtin_amdgcn_s_sleep(8);  // ~0.25 us: fewer rounds in flight
             }
-#pragma unroll
-            for (int q = 0; q < kPer; ++q) {
-                if (((pending >> q) & 1u) && fresh(w[q], epoch)) {
-                    vals[q] = static_cast<uint32_t>(w[q]);
-                    pending &= ~(1u << q);
-                }
-            }
-            if (pending != 0u) {
-                __builtin_amdgcn_s_sleep(1);
-            }
+            mh::u32x4 v[kReadsPerThread];
+            load3_coherent(src[0], src[1], src[2], v[0], v[1], v[2]);
+            take(v);
             ++spins;
         }
         if (pending != 0u) {
             bad_l = 1u;
         }
-#pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-            const uint32_t i = threadIdx.x + q * kThreads;
-            if (i < pairs) {
-                reinterpret_cast<uint32_t*>(act_l)[i] = vals[q];
-            }
-        }
         __syncthreads();
         // one thread per 32-activation chunk: f32, odd positions scaled for
-        // the Q4 dot, float4 k of chunk j stored at slot (k + j) % 8 (the
-        // waves' reads below then spread over the LDS banks), and the chunk
-        // sum in the order x_words_to_f32 uses
+        // the Q4 dot, and the chunk sum in the order x_words_to_f32 uses.
+        // LDS has 64 banks (256 bytes a cycle, 16 lanes of a 16-byte access):
+        // float4 k of chunk j (128 bytes of f32) is stored at slot
+        // (k + j / 2) % 8, so the 16 consecutive chunks read by 16 lanes in
+        // the waves' down dots below touch 16 distinct bank groups
         const uint32_t chunks = TK * a.NI / 32u;
         if (threadIdx.x < chunks) {
+            const uint32_t j = threadIdx.x;
             uint32_t w16[16];
-            const uint4* src = reinterpret_cast<const uint4*>(&act_l[32u * threadIdx.x]);
+            const uint4* src = reinterpret_cast<const uint4*>(&act_l[32u * j]);
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const uint4 v = src[k];
@@ -342,22 +421,16 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
             float xr[32], xs;
             mh::x_words_to_f32(w16, xr, xs);
             mh::q4_scale_x(xr);
-            float4* dst = reinterpret_cast<float4*>(&actf_l[32u * threadIdx.x]);
+            float4* dst = reinterpret_cast<float4*>(&actf_l[32u * j]);
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                dst[(k + threadIdx.x) & 7u] = make_float4(xr[4 * k], xr[4 * k + 1], xr[4 * k + 2], xr[4 * k + 3]);
+                dst[(k + (j >> 1)) & 7u] = make_float4(xr[4 * k], xr[4 * k + 1], xr[4 * k + 2], xr[4 * k + 3]);
             }
-            xs_l[threadIdx.x] = xs;
+            xs_l[j] = xs;
         }
         __syncthreads();
         ok = ok && bad_l == 0u;
         if (has_out) {
-#pragma unroll
-            for (int r = 0; r < TK; ++r) {
-                dch[r].fence();
-                mh::reg_fence(dsr[r]);
-                mh::reg_fence(dbr[r]);
-            }
             float h[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int r = 0; r < TK; ++r) {
@@ -366,7 +439,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
                 float xr[32];
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
-                    const float4 v = qv[(k + j) & 7u];
+                    const float4 v = qv[(k + (j >> 1)) & 7u];
                     xr[4 * k] = v.x; xr[4 * k + 1] = v.y; xr[4 * k + 2] = v.z; xr[4 * k + 3] = v.w;
                 }
                 const float d = dch[r].dot(xr);
@@ -418,15 +491,20 @@ int moe_decode_fused(const void* router, int router_dtype, const float* bias, in
     a.logits = logits; a.ids = ids; a.weights = weights; a.act = act; a.out = out; a.scratch = scratch;
     a.E = n_experts; a.K = K; a.NI = NI; a.gs = gate->group_size;
     const bool f32 = router_dtype == MH_DTYPE_F32;
-#define MH_FUSED_LAUNCH(TK)                                                                                  \
-    if (f32) hipLaunchKernelGGL((k_moe_decode_fused<float, TK>), dim3(kGrid), dim3(kThreads), 0, stream, a); \
-    else hipLaunchKernelGGL((k_moe_decode_fused<uint16_t, TK>), dim3(kGrid), dim3(kThreads), 0, stream, a);
+    const bool eb1 = n_experts <= 64u;  // one expert per lane in the routing
+#define MH_FUSED_LAUNCH_EB(TK, EB)                                                                               \
+    if (f32) hipLaunchKernelGGL((k_moe_decode_fused<float, TK, EB>), dim3(kGrid), dim3(kThreads), 0, stream, a); \
+    else hipLaunchKernelGGL((k_moe_decode_fused<uint16_t, TK, EB>), dim3(kGrid), dim3(kThreads), 0, stream, a);
+#define MH_FUSED_LAUNCH(TK)            \
+    if (eb1) { MH_FUSED_LAUNCH_EB(TK, 1) } \
+    else { MH_FUSED_LAUNCH_EB(TK, 4) }
     switch (topk) {
         case 1: MH_FUSED_LAUNCH(1) break;
         case 2: MH_FUSED_LAUNCH(2) break;
         case 3: MH_FUSED_LAUNCH(3) break;
         default: MH_FUSED_LAUNCH(4) break;
     }
+#undef MH_FUSED_LAUNCH_EB
 #undef MH_FUSED_LAUNCH
     return mh::launch_status("k_moe_decode_fused");
 }
