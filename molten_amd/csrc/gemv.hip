@@ -545,6 +545,14 @@ int gemv_common(const char* op, const mh_quant_weights* w, const uint16_t* x, ui
     a.row_words = w->in_features * w->bits / 32u;
     a.groups = w->in_features / w->group_size;
     const hipStream_t s = mh::as_stream(stream);
+    // batch > 1 without the reference's atomic-max key: the matrix-core
+    // kernel where its shape limits allow
+    if (batch > 1 && (finisher || best == nullptr)) {
+        const int rc = mh::gemv_mfma(w, x, y, finisher ? best : nullptr, ids, batch, s);
+        if (rc != MH_ERR_UNSUPPORTED) {
+            return rc;
+        }
+    }
     return w->bits == 4 ? dispatch_gemv<4>(a, batch, s) : dispatch_gemv<6>(a, batch, s);
 }
 

@@ -1,0 +1,629 @@
+// gemv_mfma.hip -- the quantized head GEMV for 2..8 rows of x on the matrix
+// cores (src/kernels/quant.rs gemv / gemv_head_argmax at batch > 1).
+//
+// A row's codes are widened to bf16 as q + 128 (exact: the bf16 with bits
+// 0x4300 | q), x stays bf16, and v_mfma_f32_16x16x32_bf16 forms the exact
+// products and sums each 64-code group in f32; then, per group,
+//     y += s * P_g + (b - 128 s) * X_g,   P_g = sum (q + 128) x,  X_g = sum x.
+// The logits agree with the chunk-order oracle to f32 rounding, not bit for
+// bit.  The argmax stays exact: every row value v carries a bound E with
+// |v - v_chunk| <= E (v_chunk: the chunk-order value), the rows whose upper
+// bound can reach the greatest lower bound (in bf16, the argmax's domain)
+// are kept as candidates, and the last workgroup recomputes them in chunk
+// order and takes the reference's key (value desc, index asc).
+//
+// Tiles of 16 rows x all of K per wave.  MFMA operand layout (16x16x32):
+// lane l holds A row l % 16 and B column l % 16, k = 8 (l / 16) .. + 8; the
+// result rows 4 (l / 16) .. + 4 of column l % 16.  The k order inside a
+// group is permuted so that lane quarter q owns the 16 consecutive codes
+// 16q .. 16q + 15 of the group (step t of the group uses codes 16q + 8t ..
+// + 8): its codes are one contiguous 12-byte (Q6) or 8-byte (Q4) piece, and
+// x is staged in LDS in the same order.  The B columns are the batch rows
+// (columns >= batch are zero).
+#include "mh_device.hpp"
+#include "mh_host.hpp"
+
+namespace {
+
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr uint32_t kGrid = 256;
+constexpr int kTileRows = 16;
+constexpr int kStageGroups = 8;  // groups of 64 codes per pipeline stage
+constexpr int kDepth = 4;        // stages whose loads are in flight (even: LDS regions alternate)
+constexpr uint32_t kMaxK = 2048;
+constexpr uint32_t kMaxG = kMaxK / 64;
+constexpr int kMaxB = 8;
+constexpr int kSlotWords = 6;  // per (batch row, workgroup): lower bound, dropped bound, 4 candidates
+constexpr int kCand = 4;
+constexpr uint32_t kArgSlots = MH_ARGMAX_SLOTS;
+constexpr uint32_t kMaxCand = kTileRows * 68;  // finisher's candidate list (a wave's stage buffer)
+constexpr uint32_t kSpinLimit = 1u << 24;
+static_assert((kGrid - 1) * kSlotWords <= kArgSlots, "finisher slots");
+static_assert(kGrid * kCand <= kMaxCand, "candidate list");
+
+struct MfmaArgs {
+    const char* codes;
+    const uint16_t* scales;
+    const uint16_t* biases;
+    const uint16_t* x;          // [batch, K] bf16, 16-byte aligned
+    uint16_t* y;                // [batch, N] bf16, or null
+    unsigned long long* slots;  // [batch][kArgSlots] finisher scratch, or null (no argmax)
+    uint32_t* ids;              // [batch]
+    uint32_t n, k, groups, row_bytes;
+};
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Codes of one lane for one group (16 codes) and their bf16(q + 128) pairs.
+template <int BITS>
+struct Piece;
+template <>
+struct Piece<6> {
+    uint32_t w[3];
+    __device__ __forceinline__ void read(const uint32_t* l) {  // LDS, 4-byte aligned
+        w[0] = l[0];
+        w[1] = l[1];
+        w[2] = l[2];
+    }
+    // pair j: the 12-bit field 12 j .. 12 j + 11 (codes 2j, 2j + 1)
+    __device__ __forceinline__ void widen(uint32_t (&o)[8]) const {
+        uint32_t t[8];
+        t[0] = w[0] & 0xfffu;
+        t[1] = __builtin_amdgcn_ubfe(w[0], 12, 12);
+        t[2] = __builtin_amdgcn_alignbit(w[1], w[0], 24) & 0xfffu;
+        t[3] = __builtin_amdgcn_ubfe(w[1], 4, 12);
+        t[4] = __builtin_amdgcn_ubfe(w[1], 16, 12);
+        t[5] = __builtin_amdgcn_alignbit(w[2], w[1], 28) & 0xfffu;
+        t[6] = __builtin_amdgcn_ubfe(w[2], 8, 12);
+        t[7] = w[2] >> 20;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            // low code to bits 0..5, high code to bits 16..21, exponent of 128
+            o[j] = (((t[j] << 10) | t[j]) & 0x003f003fu) | 0x43004300u;
+        }
+    }
+};
+template <>
+struct Piece<4> {
+    uint32_t w[2];
+    __device__ __forceinline__ void read(const uint32_t* l) {  // LDS, 8-byte aligned
+        w[0] = l[0];
+        w[1] = l[1];
+    }
+    // pair j: byte j (codes 2j, 2j + 1 are its low and high nibble)
+    __device__ __forceinline__ void widen(uint32_t (&o)[8]) const {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t t = __builtin_amdgcn_ubfe(w[j >> 2], 8 * (j & 3), 8);
+            o[j] = (((t << 12) | t) & 0x000f000fu) | 0x43004300u;
+        }
+    }
+};
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    const mh::u32x4 v = {a, b, c, d};
+    return __builtin_bit_cast(bf16x8, v);
+}
+
+// Value of an argmax_key (its high word), the inverse of the orderable map
+// (a select, no branch).
+__device__ __forceinline__ float key_value(unsigned long long key) {
+    const uint32_t o = static_cast<uint32_t>(key >> 32);
+    const uint32_t neg = static_cast<uint32_t>(static_cast<int32_t>(o) >> 31);  // all ones if the value is >= +0
+    return __uint_as_float((o & 0x7fffffffu & neg) | (~o & ~neg));
+}
+
+// Chunk-order value of one row for batch row b (the staged kernel's formula:
+// lane c owns chunk c, K <= 2048): the exact value the argmax is taken on.
+template <int BITS>
+__device__ float chunk_value(const MfmaArgs& a, uint32_t row, const float (&xr)[32], float xs, bool live,
+                             uint32_t c) {
+    mh::Chunk<BITS> ch;
+    ch.load(reinterpret_cast<const uint32_t*>(a.codes + static_cast<size_t>(row) * a.row_bytes) + c * BITS);
+    const uint32_t g = (32u * c) / 64u;
+    const float s = mh::bf16_to_f32(a.scales[static_cast<size_t>(row) * a.groups + g]);
+    const float b = mh::bf16_to_f32(a.biases[static_cast<size_t>(row) * a.groups + g]);
+    const float p = ch.dot(xr);
+    const float acc = live ? 0.0f + __builtin_fmaf(s, p, b * xs) : 0.0f;
+    return mh::lane63(mh::wave_sum_lane63(acc));
+}
+
+// A stage of a tile: 16 rows x kStageGroups groups of codes, loaded with
+// contiguous 16-byte pieces (lane and load i take piece 64 i + lane, row =
+// piece / RP), staged in the wave's LDS rows (stride: conflict-free reads of
+// the lanes' pieces), read back as (row l % 16, piece 16 codes of quarter
+// l / 16).
+template <int BITS>
+struct StageShape {
+    static constexpr int kRowBytes = kStageGroups * 64 * BITS / 8;      // 384 (Q6), 256 (Q4)
+    static constexpr int kRowPieces = kRowBytes / 16;
+    static constexpr int kLoads = kTileRows * kRowPieces / 64;          // 6, 4
+    static constexpr int kStrideWords = BITS == 6 ? 100 : 68;           // LDS row stride
+};
+
+template <int BITS, int B>
+__global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
+    constexpr int PW = BITS == 6 ? 12 : 8;  // bytes of a lane's piece of a group
+    using SS = StageShape<BITS>;
+    __shared__ __attribute__((aligned(16))) uint32_t stg[kWaves][kTileRows * SS::kStrideWords];
+    __shared__ __attribute__((aligned(16))) mh::u32x4 xl[kMaxG * 2 * 4 * 16];  // x in B-operand order, 16 columns
+    __shared__ float xg[kMaxG * 16];                                         // group sums of x, 16 columns
+    __shared__ float xga[kMaxG * 16];                                       // group sums of |x|
+    __shared__ float xa[B];                                                 // sum |x| per batch row
+    __shared__ __attribute__((aligned(16))) float sbl[kWaves][2][2][kStageGroups][kTileRows];  // s, b - 128 s
+    __shared__ float mrow[kWaves][2][kTileRows];                            // max |s|, max |b| per row
+    __shared__ float m_lb[B][kWaves * 4], m_u1[B][kWaves * 4], m_du[B][kWaves * 4];
+    __shared__ uint32_t m_r1[B][kWaves * 4];
+    __shared__ unsigned long long own[B][kSlotWords];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t q = static_cast<uint32_t>(lane) >> 4;  // lane quarter
+    const uint32_t n = static_cast<uint32_t>(lane) & 15u;  // B column (batch row)
+    const bool col = n < static_cast<uint32_t>(B);
+    const uint32_t G = a.groups;
+    const uint32_t K = a.k;
+
+    // ---- tiles: stages of kStageGroups groups; the next stage's codes and
+    // scales / biases are in flight while a stage is computed (buffers A, B
+    // and LDS regions 0, 1 alternate)
+    const uint32_t n_st = (G + kStageGroups - 1) / kStageGroups;  // stages per tile
+    const uint32_t n_tiles = a.n / kTileRows;
+    const uint32_t stride = gridDim.x * kWaves;
+    mh::u32x4 pbuf[kDepth][SS::kLoads];         // codes of the stages in flight
+    uint32_t svbuf[kDepth], bvbuf[kDepth];        // scales / biases: row l / 4, groups 2 (l % 4) .. + 1
+    const uint32_t srow = static_cast<uint32_t>(lane) >> 2, sg = 2u * (static_cast<uint32_t>(lane) & 3u);
+
+    auto issue = [&](uint32_t tile, uint32_t st, mh::u32x4(&p)[SS::kLoads], uint32_t& sv, uint32_t& bv) {
+        const uint32_t g0 = st * kStageGroups;
+        const mh::gbytes base = mh::uniform_ptr(a.codes + static_cast<size_t>(tile) * kTileRows * a.row_bytes +
+                                                st * SS::kRowBytes);
+#pragma unroll
+        for (int i = 0; i < SS::kLoads; ++i) {
+            const uint32_t pc = i * 64u + static_cast<uint32_t>(lane);
+            const uint32_t off = (pc / SS::kRowPieces) * a.row_bytes + (pc % SS::kRowPieces) * 16u;
+            p[i] = __builtin_nontemporal_load(reinterpret_cast<const __attribute__((address_space(1))) mh::u32x4*>(base + off));
+        }
+        const size_t sbi = (static_cast<size_t>(tile) * kTileRows + srow) * G + g0 + sg;
+        sv = *reinterpret_cast<const uint32_t*>(a.scales + sbi);
+        bv = *reinterpret_cast<const uint32_t*>(a.biases + sbi);
+    };
+    // a stage's scales / biases into LDS as f32 (s, b - 128 s), and the
+    // rows' running max |s|, |b| (restarted at a tile's first stage)
+    auto stage_sb = [&](int region, uint32_t st, uint32_t sv, uint32_t bv) {
+        float ms = 0.0f, mb = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const float s = e ? mh::bf16hi(sv) : mh::bf16lo(sv);
+            const float b = e ? mh::bf16hi(bv) : mh::bf16lo(bv);
+            sbl[wave][region][0][sg + e][srow] = s;
+            sbl[wave][region][1][sg + e][srow] = __builtin_fmaf(-128.0f, s, b);
+            ms = fmaxf(ms, fabsf(s));
+            mb = fmaxf(mb, fabsf(b));
+        }
+        // max over the row's four lanes (lanes 4 srow .. + 3)
+        ms = fmaxf(ms, __shfl_xor(ms, 1));
+        ms = fmaxf(ms, __shfl_xor(ms, 2));
+        mb = fmaxf(mb, __shfl_xor(mb, 1));
+        mb = fmaxf(mb, __shfl_xor(mb, 2));
+        if ((lane & 3) == 0) {
+            mrow[wave][0][srow] = st == 0u ? ms : fmaxf(mrow[wave][0][srow], ms);
+            mrow[wave][1][srow] = st == 0u ? mb : fmaxf(mrow[wave][1][srow], mb);
+        }
+    };
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute = [&](int region, uint32_t st, const mh::u32x4(&p)[SS::kLoads]) {
+        const uint32_t g0 = st * kStageGroups;
+        const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+        uint32_t* const sw = stg[wave];
+#pragma unroll
+        for (int i = 0; i < SS::kLoads; ++i) {
+            const uint32_t pc = i * 64u + static_cast<uint32_t>(lane);
+            *reinterpret_cast<mh::u32x4*>(sw + (pc / SS::kRowPieces) * SS::kStrideWords + (pc % SS::kRowPieces) * 4u) = p[i];
+        }
+        const uint32_t* const mine = sw + static_cast<uint32_t>(lane & 15) * SS::kStrideWords + q * (PW / 4);
+#pragma unroll
+        for (int g = 0; g < kStageGroups; ++g) {
+            {
+                const uint32_t ga = g0 + g;
+                Piece<BITS> pg_codes;
+                pg_codes.read(mine + g * PW);
+                uint32_t o[8];
+                pg_codes.widen(o);
+                const mh::u32x4 b0 = xl[(ga * 8u + q) * 16u + n];
+                const mh::u32x4 b1 = xl[(ga * 8u + 4u + q) * 16u + n];
+                const float xgv = xg[ga * 16u + n];
+                f32x4 pg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(o[0], o[1], o[2], o[3]),
+                                                                   __builtin_bit_cast(bf16x8, b0), zero, 0, 0, 0);
+                pg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(o[4], o[5], o[6], o[7]),
+                                                             __builtin_bit_cast(bf16x8, b1), pg, 0, 0, 0);
+                const float4 s4 = *reinterpret_cast<const float4*>(&sbl[wave][region][0][g][4u * q]);
+                const float4 b4 = *reinterpret_cast<const float4*>(&sbl[wave][region][1][g][4u * q]);
+                acc[0] = __builtin_fmaf(s4.x, pg[0], acc[0]);
+                acc[1] = __builtin_fmaf(s4.y, pg[1], acc[1]);
+                acc[2] = __builtin_fmaf(s4.z, pg[2], acc[2]);
+                acc[3] = __builtin_fmaf(s4.w, pg[3], acc[3]);
+                acc[0] = __builtin_fmaf(b4.x, xgv, acc[0]);
+                acc[1] = __builtin_fmaf(b4.y, xgv, acc[1]);
+                acc[2] = __builtin_fmaf(b4.z, xgv, acc[2]);
+                acc[3] = __builtin_fmaf(b4.w, xgv, acc[3]);
+            }
+        }
+    };
+
+    // argmax state of this lane's batch row (lanes with col)
+    float lbv = -__builtin_inff();         // greatest bf16 lower bound seen
+    float u1 = -__builtin_inff();          // greatest upper bound, its row
+    uint32_t r1 = 0xffffffffu;
+    float du = -__builtin_inff();          // greatest upper bound of the other rows
+    const float an = col ? xa[n] : 0.0f;
+
+    // a tile's rows 4q .. 4q + 3 of batch row n: store, bounds, candidates
+    auto finish_tile = [&](uint32_t tile) {
+        // rows 4q .. 4q + 3 of batch row n
+        const uint32_t row0 = tile * kTileRows + 4u * q;
+        if (col) {
+            uint16_t yb[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                yb[i] = mh::f32_to_bf16(acc[i]);
+            }
+            if (a.y != nullptr) {
+                *reinterpret_cast<uint2*>(a.y + static_cast<size_t>(n) * a.n + row0) =
+                    make_uint2(yb[0] | (static_cast<uint32_t>(yb[1]) << 16), yb[2] | (static_cast<uint32_t>(yb[3]) << 16));
+            }
+            if (a.slots != nullptr) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    // |acc - chunk value| <= 2^-16 (336 max|s| + 3 max|b|) sum|x|: f32
+                    // rounding of both orders (at most 130 and 40 roundings deep,
+                    // K <= 2048); 2^-85 covers bf16 / f32 denormals the matrix core
+                    // may flush.  e doubles the bound and adds 2^-21 |v| and the
+                    // least normal, so fl(v - e) and fl(v + e) bracket the chunk value.
+                    const float ms = mrow[wave][0][4u * q + i], mb = mrow[wave][1][4u * q + i];
+                    const float v = acc[i];
+                    const float e = __builtin_fmaf(__builtin_fmaf(0x1p-15f, an, 0x1p-85f),
+                                                   __builtin_fmaf(336.0f, ms, 3.0f * mb),
+                                                   __builtin_fmaf(0x1p-21f, fabsf(v), 0x1p-126f));
+                    const float lo = v - e, hi = v + e;
+                    const uint32_t row = row0 + i;
+                    if (!(fabsf(lo) <= 3.0e38f && fabsf(hi) <= 3.0e38f)) {
+                        du = __builtin_inff();  // no usable bound: the finisher recomputes every row
+                        continue;
+                    }
+                    lbv = fmaxf(lbv, mh::round_bf16(lo));
+                    if (hi > u1 || (hi == u1 && row < r1)) {
+                        du = fmaxf(du, u1);
+                        u1 = hi;
+                        r1 = row;
+                    } else {
+                        du = fmaxf(du, hi);
+                    }
+                }
+            }
+        }
+    };
+
+    // the wave's stages in order: stage s is stage s % n_st of its tile
+    // s / n_st (tiles first, first + stride, ...); kDepth - 1 stages ahead
+    // are in flight
+    const uint32_t first = blockIdx.x * kWaves + wave;
+    const uint32_t my_tiles = first < n_tiles ? (n_tiles - first + stride - 1) / stride : 0u;
+    const uint32_t n_stages = my_tiles * n_st;
+    auto tile_of = [&](uint32_t st) { return first + (st / n_st) * stride; };
+    // stages past the end reload the wave's last stage (valid addresses, an
+    // L2 hit), so every step issues the same loads and the compiler's load
+    // counting stays exact across the loop
+    const uint32_t last_st = n_stages > 0u ? n_stages - 1u : 0u;
+    const uint32_t first_c = first < n_tiles ? first : 0u;
+    auto tile_c = [&](uint32_t st) { return n_stages > 0u ? tile_of(st < n_stages ? st : last_st) : first_c; };
+    auto stage_c = [&](uint32_t st) { return (st < n_stages ? st : last_st) % n_st; };
+    // ---- x to LDS in operand order (columns >= B zero): every thread's x
+    // loads go out first (clamped addresses, no branches), then the first
+    // stages' code loads, then the x stores wait for the x loads only
+    constexpr int kXPer = kMaxG * 8 * 16 / kThreads;
+    mh::u32x4 xv[kXPer];
+#pragma unroll
+    for (int j = 0; j < kXPer; ++j) {
+        const uint32_t u = threadIdx.x + j * kThreads;
+        const uint32_t nb = u % 16u, qq = (u / 16u) % 4u, t = (u / 64u) % 2u, g = u / 128u;
+        const uint32_t nc = nb < static_cast<uint32_t>(B) ? nb : 0u, gcl = g < G ? g : 0u;
+        const uint4 v = *reinterpret_cast<const uint4*>(a.x + static_cast<size_t>(nc) * K + 64u * gcl + 16u * qq + 8u * t);
+        xv[j] = mh::u32x4{v.x, v.y, v.z, v.w};
+    }
+#pragma unroll
+    for (int u = 0; u < kDepth - 1; ++u) {
+        issue(tile_c(u), stage_c(u), pbuf[u], svbuf[u], bvbuf[u]);
+    }
+#pragma unroll
+    for (int j = 0; j < kXPer; ++j) {
+        const uint32_t u = threadIdx.x + j * kThreads;
+        if (u / 128u < G) {
+            const bool live_col = u % 16u < static_cast<uint32_t>(B);
+            xl[u] = live_col ? xv[j] : mh::u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+    __syncthreads();
+    for (uint32_t u = threadIdx.x; u < G * 16u; u += kThreads) {
+        const uint32_t nb = u % 16u, g = u / 16u;
+        float s = 0.0f, sa = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {  // the group's 64 values in order: pieces (q, t) = (j / 2, j % 2)
+            const mh::u32x4 v = xl[(g * 8u + (j & 1) * 4u + (j >> 1)) * 16u + nb];
+            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                s = s + mh::bf16lo(w4[e]);
+                s = s + mh::bf16hi(w4[e]);
+                sa = sa + fabsf(mh::bf16lo(w4[e]));
+                sa = sa + fabsf(mh::bf16hi(w4[e]));
+            }
+        }
+        xg[u] = s;
+        xga[u] = sa;
+    }
+    __syncthreads();
+    if (threadIdx.x < static_cast<uint32_t>(B)) {
+        float s = 0.0f;
+        for (uint32_t g = 0; g < G; ++g) {
+            s = s + xga[g * 16u + threadIdx.x];
+        }
+        xa[threadIdx.x] = s;
+    }
+    __syncthreads();
+
+    for (uint32_t s0 = 0; s0 < n_stages; s0 += kDepth) {
+#pragma unroll
+        for (int u = 0; u < kDepth; ++u) {
+            const uint32_t st = s0 + u;
+            const uint32_t sn = st + kDepth - 1;
+            const int un = (u + kDepth - 1) % kDepth;  // a constant once unrolled
+            issue(tile_c(sn), stage_c(sn), pbuf[un], svbuf[un], bvbuf[un]);
+            if (st < n_stages) {
+                stage_sb(u & 1, st % n_st, svbuf[u], bvbuf[u]);
+                compute(u & 1, st % n_st, pbuf[u]);
+                if (st % n_st == n_st - 1u) {
+                    finish_tile(tile_of(st));
+                    acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+            }
+        }
+    }
+    if (a.slots == nullptr) {
+        return;
+    }
+
+    // ---- workgroup summary per batch row: greatest lower bound, the four
+    // greatest upper bounds (candidates), the greatest of the rest
+    if (col) {
+        m_lb[n][wave * 4 + q] = lbv;
+        m_u1[n][wave * 4 + q] = u1;
+        m_r1[n][wave * 4 + q] = r1;
+        m_du[n][wave * 4 + q] = du;
+    }
+    __syncthreads();
+    // wave b < B summarises batch row b: lane e < 32 holds entry e (wave e / 4,
+    // quarter e % 4); the candidates are the four greatest keys (upper bound
+    // desc, row asc), taken one per round by a wave max
+    const uint32_t last = gridDim.x - 1;
+    if (wave < B) {
+        const uint32_t b = static_cast<uint32_t>(wave);
+        const bool ent = lane < kWaves * 4;
+        const int e = ent ? lane : 0;
+        float lb = ent ? m_lb[b][e] : -__builtin_inff();
+        float dmax = ent ? m_du[b][e] : -__builtin_inff();
+        unsigned long long key = ent && m_r1[b][e] != 0xffffffffu ? mh::argmax_key(m_u1[b][e], m_r1[b][e]) : 0ull;
+        lb = mh::wave_max_f32(lb);
+        unsigned long long out[kSlotWords];
+        out[0] = mh::argmax_key(lb, 0u);
+#pragma unroll
+        for (int c = 0; c < kCand; ++c) {
+            unsigned long long m = key;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const unsigned long long o = __shfl_xor(m, off);
+                m = o > m ? o : m;
+            }
+            out[2 + c] = m != 0ull ? m : mh::argmax_key(-__builtin_inff(), 0xffffffffu);
+            key = key == m ? 0ull : key;  // keys are distinct (distinct rows)
+        }
+        // the rest of the entries' upper bounds join the dropped bound
+        dmax = fmaxf(dmax, key != 0ull ? key_value(key) : -__builtin_inff());
+        dmax = mh::wave_max_f32(dmax);
+        out[1] = mh::argmax_key(dmax, 0u);
+        if (blockIdx.x != last) {
+            if (lane < kSlotWords) {
+                unsigned long long w = out[0];
+#pragma unroll
+                for (int j = 1; j < kSlotWords; ++j) {
+                    w = lane == j ? out[j] : w;
+                }
+                __hip_atomic_store(a.slots + static_cast<size_t>(b) * kArgSlots + blockIdx.x * kSlotWords + lane, w,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        } else if (lane == 0) {
+#pragma unroll
+            for (int j = 0; j < kSlotWords; ++j) {
+                own[b][j] = out[j];
+            }
+        }
+    }
+    if (blockIdx.x != last) {
+        return;
+    }
+
+    // ---- finisher (the last workgroup: every other one has started).  Wave
+    // b takes batch row b: it reads the other workgroups' words (polling the
+    // ones not yet written), clears them, and forms the greatest lower bound,
+    // the greatest dropped upper bound and the candidates.  The argmax row is
+    // always a candidate unless a dropped bound reaches the lower bound, so a
+    // single candidate is the answer; several are recomputed in chunk order;
+    // otherwise every row is.
+    __syncthreads();
+    if (wave >= B) {
+        return;
+    }
+    const uint32_t b = static_cast<uint32_t>(wave);
+    const uint32_t words = last * kSlotWords;
+    constexpr int kPer = ((kGrid - 1) * kSlotWords + 63) / 64;  // words per lane
+    static_assert(kPer <= 32, "pending mask");
+    unsigned long long* const sl = a.slots + static_cast<size_t>(b) * kArgSlots;
+    unsigned long long v[kPer];
+    uint32_t pend = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const uint32_t i = static_cast<uint32_t>(lane) + 64u * j;
+        v[j] = i < words ? __hip_atomic_load(sl + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1ull;
+        pend |= (v[j] == 0ull ? 1u : 0u) << j;
+    }
+    uint32_t spins = 0;
+    while (__any(pend != 0u) && ++spins < kSpinLimit) {
+        __builtin_amdgcn_s_sleep(1);
+        // all of a round's loads in flight together, then the checks
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            if ((pend >> j) & 1u) {
+                v[j] = __hip_atomic_load(sl + lane + 64u * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            if (v[j] != 0ull) {
+                pend &= ~(1u << j);
+            }
+        }
+    }
+    const bool lost = __any(pend != 0u);
+    float lb = lane == 0 ? key_value(own[b][0]) : -__builtin_inff();
+    float dmax = lane == 0 ? key_value(own[b][1]) : -__builtin_inff();
+    // word i = lane + 64 j has kind i % 6 (64 = 4 mod 6): branch-free scan
+    uint32_t kinds[kPer];
+    {
+        uint32_t kd = static_cast<uint32_t>(lane) % kSlotWords;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            kinds[j] = kd;
+            kd = kd + 4u >= kSlotWords ? kd + 4u - kSlotWords : kd + 4u;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const bool valid = static_cast<uint32_t>(lane) + 64u * j < words;
+        const float val = key_value(v[j]);
+        lb = valid && kinds[j] == 0u ? fmaxf(lb, val) : lb;
+        dmax = valid && kinds[j] == 1u ? fmaxf(dmax, val) : dmax;
+    }
+    lb = mh::wave_max_f32(lb);
+    dmax = mh::wave_max_f32(dmax);
+    // candidates (row ids) into this wave's stage buffer (free now)
+    uint32_t* const cand = stg[wave];
+    uint32_t nc = 0;
+    auto collect = [&](unsigned long long key, bool valid) {
+        const uint32_t r = ~static_cast<uint32_t>(key & 0xffffffffull);
+        const bool take = valid && r != 0xffffffffu && mh::round_bf16(key_value(key)) >= lb;
+        const unsigned long long m = __ballot(take);
+        if (m != 0ull) {  // uniform: most words hold no candidate
+            if (take) {
+                cand[nc + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u))] = r;
+            }
+            nc += static_cast<uint32_t>(__popcll(m));
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        collect(v[j], static_cast<uint32_t>(lane) + 64u * j < words && kinds[j] >= 2u);
+    }
+    collect(lane < kCand ? own[b][2 + (lane < kCand ? lane : 0)] : 0ull, lane < kCand);
+    const bool all_rows = !(mh::round_bf16(dmax) < lb);
+    uint32_t id;
+    if (!all_rows && nc == 1u) {
+        id = cand[0];
+    } else {
+        // chunk-order values of the candidates (or of every row); the staged
+        // kernel's merge: NaN never wins, with no other value (-inf, 0)
+        const uint32_t C = K / 32u;
+        const bool live = static_cast<uint32_t>(lane) < C;
+        const uint32_t c = live ? static_cast<uint32_t>(lane) : 0u;
+        float xr[32], xs;
+        mh::load_x_chunk(a.x + static_cast<size_t>(b) * K + 32u * c, xr, xs);
+        if (BITS == 4) {
+            mh::q4_scale_x(xr);
+        }
+        const uint32_t count = all_rows ? a.n : nc;
+        unsigned long long best = mh::argmax_key(-__builtin_inff(), 0u);
+        for (uint32_t i = 0; i < count; ++i) {
+            const uint32_t row = all_rows ? i : cand[i];
+            const float val = mh::round_bf16(chunk_value<BITS>(a, row, xr, xs, live, c));
+            if (val == val) {
+                const unsigned long long key = mh::argmax_key(val, row);
+                best = key > best ? key : best;
+            }
+        }
+        id = ~static_cast<uint32_t>(best & 0xffffffffull);
+    }
+    if (lane == 0) {
+        a.ids[b] = lost ? 0xffffffffu : id;
+    }
+    // clear the words for the next launch (last: no later load waits on them)
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const uint32_t i = static_cast<uint32_t>(lane) + 64u * j;
+        if (i < words) {
+            __hip_atomic_store(sl + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+template <int BITS, int B>
+int launch(const MfmaArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL((k_gemv_mfma<BITS, B>), dim3(kGrid), dim3(kThreads), 0, stream, a);
+    return mh::launch_status("k_gemv_mfma");
+}
+
+template <int BITS>
+int dispatch(const MfmaArgs& a, uint32_t batch, hipStream_t stream) {
+    switch (batch) {
+        case 2: return launch<BITS, 2>(a, stream);
+        case 3: return launch<BITS, 3>(a, stream);
+        case 4: return launch<BITS, 4>(a, stream);
+        case 5: return launch<BITS, 5>(a, stream);
+        case 6: return launch<BITS, 6>(a, stream);
+        case 7: return launch<BITS, 7>(a, stream);
+        default: return launch<BITS, 8>(a, stream);
+    }
+}
+
+}  // namespace
+
+namespace mh {
+
+// Batched head GEMV on the matrix cores; MH_ERR_UNSUPPORTED when the shape
+// needs the staged chunk-order kernel (the caller then uses it).
+int gemv_mfma(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint64_t* slots, uint32_t* ids,
+              uint32_t batch, hipStream_t stream) {
+    const uint32_t K = w->in_features;
+    if (batch < 2 || batch > static_cast<uint32_t>(kMaxB) || w->group_size != 64u || K % (64u * kStageGroups) != 0 ||
+        K > kMaxK || w->out_features % kTileRows != 0 || !mh::aligned(x, 16) || !mh::aligned(w->codes, 8) ||
+        !mh::aligned(w->scales, 8) || !mh::aligned(w->biases, 8) ||
+        (y != nullptr && !mh::aligned(y, 8)) || (slots != nullptr && ids == nullptr)) {
+        return MH_ERR_UNSUPPORTED;
+    }
+    MfmaArgs a{};
+    a.codes = reinterpret_cast<const char*>(w->codes);
+    a.scales = w->scales;
+    a.biases = w->biases;
+    a.x = x;
+    a.y = y;
+    a.slots = reinterpret_cast<unsigned long long*>(slots);
+    a.ids = ids;
+    a.n = w->out_features;
+    a.k = K;
+    a.groups = K / 64u;
+    a.row_bytes = K * w->bits / 8u;
+    return w->bits == 4 ? dispatch<4>(a, batch, stream) : dispatch<6>(a, batch, stream);
+}
+
+}  // namespace mh

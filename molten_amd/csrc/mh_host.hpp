@@ -48,6 +48,8 @@ int moe_decode_fused(const void* router, int router_dtype, const float* bias, in
                      const mh_quant_weights* down, uint32_t n_experts, uint32_t topk,
                      const uint16_t* x, uint16_t* out, float* logits, uint32_t* ids,
                      uint16_t* weights, uint16_t* act, uint32_t* scratch, hipStream_t stream);
+int gemv_mfma(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint64_t* slots, uint32_t* ids,
+              uint32_t batch, hipStream_t stream);
 int router_prefill_route(const uint16_t* x, const void* w, int w_dtype, float* logits,
                          const float* bias, uint32_t* ids, uint16_t* gw, uint32_t m, uint32_t k,
                          uint32_t e, uint32_t topk, int mode, float eps, mh_stream_t stream);

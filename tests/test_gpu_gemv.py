@@ -1,6 +1,10 @@
 """GPU parity of the decode GEMV family through the C ABI (BASELINE configs
-1, 2 and 5).  The kernels follow the oracle's chunk order, so logits are
-compared bit for bit and argmax ids exactly."""
+1, 2 and 5).  Batch 1 (and shapes outside the matrix-core kernel's limits)
+follows the oracle's chunk order: logits bit for bit.  Batch 2..8 on the
+matrix-core kernel sums in another order: logits within the stated
+tolerance (rel-L2 <= 5e-3, max abs err <= 2e-2 * max |ref|) and, as that
+kernel's own property, within one bf16 ulp plus 1e-4 * max |ref| of the
+oracle; argmax ids are exact on every path."""
 import numpy as np
 import pytest
 import torch
@@ -15,6 +19,32 @@ def _log(msg):
     print(msg, flush=True)
 
 
+def _mfma_path(n, k, batch, gs=64):
+    """Shapes the batched matrix-core kernel takes (gemv_mfma.hip limits)."""
+    return 2 <= batch <= 8 and gs == 64 and k % 256 == 0 and k <= 2048 and n % 16 == 0
+
+
+def _bf16_ulp(v):
+    """bf16 ulp at |v| (2^(e - 7)); the least normal's for zero and denormals."""
+    e = np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+def assert_logits(got, want, n, k, batch, gs=64):
+    if not _mfma_path(n, k, batch, gs):
+        np.testing.assert_array_equal(got, want)
+        return
+    g = layout.bf16_to_f32(got).astype(np.float64)
+    w = layout.bf16_to_f32(want).astype(np.float64)
+    assert np.isfinite(g).all()
+    rel_l2 = np.linalg.norm(g - w) / max(np.linalg.norm(w), 1e-30)
+    assert rel_l2 <= 5e-3, rel_l2
+    assert np.abs(g - w).max() <= 2e-2 * np.abs(w).max()
+    # the kernel's own accuracy: one bf16 ulp plus f32 rounding of the sums
+    # (relative to the largest logit: cancellation near zero)
+    assert (np.abs(g - w) <= _bf16_ulp(w) + 1e-4 * np.abs(w).max()).all()
+
+
 @pytest.mark.parametrize("bits", [4, 6])
 @pytest.mark.parametrize("n,k,batch", [
     (2048, 2048, 1),   # config 1 shape
@@ -26,7 +56,7 @@ def _log(msg):
     (512, 2048, 8),    # config 5 batch
     (130, 1536, 5),
 ])
-def test_gemv_bit_exact(dev, orc, bits, n, k, batch):
+def test_gemv_matches_oracle(dev, orc, bits, n, k, batch):
     _log(f"gemv bits={bits} n={n} k={k} batch={batch}")
     rng = np.random.default_rng(n * 131 + k + batch + bits)
     h = layout.synth_quant(rng, n, k, bits)
@@ -37,7 +67,7 @@ def test_gemv_bit_exact(dev, orc, bits, n, k, batch):
     y = empty_dev((batch, n), np.uint16)
     hip.gemv_quant(w, xd, y, batch)
     got = from_dev(y, np.uint16)
-    np.testing.assert_array_equal(got, want)
+    assert_logits(got, want, n, k, batch)
 
 
 def _extreme_x(rng, batch, k, huge):
@@ -56,9 +86,9 @@ def _extreme_x(rng, batch, k, huge):
 @pytest.mark.parametrize("huge", [False, True])
 @pytest.mark.parametrize("n,k,batch", [(512, 2048, 1), (96, 11776, 1), (256, 2048, 4)])
 def test_q4_extreme_activations(dev, orc, huge, n, k, batch):
-    """Denormal, signed-zero and (huge) 2^110 activations: the mix form of
-    the Q4 dot is exact for the first three, and the kernels switch to the
-    convert form when x * 2^24 would overflow; both stay bit-exact."""
+    """Denormal, signed-zero and (huge) 2^110 activations: the chunk-order
+    kernels stay bit-exact; the matrix-core kernel (batch 4 here) stays within
+    tolerance."""
     _log(f"q4 extreme x huge={huge} n={n} k={k} batch={batch}")
     rng = np.random.default_rng(5 + huge + k + batch)
     h = layout.synth_quant(rng, n, k, 4)
@@ -68,7 +98,7 @@ def test_q4_extreme_activations(dev, orc, huge, n, k, batch):
     w, keep = dev_quant(h)
     y = empty_dev((batch, n), np.uint16)
     hip.gemv_quant(w, to_dev(x), y, batch)
-    np.testing.assert_array_equal(from_dev(y, np.uint16), want)
+    assert_logits(from_dev(y, np.uint16), want, n, k, batch)
 
 
 @pytest.mark.parametrize("bits", [4, 6])
@@ -102,7 +132,7 @@ def test_argmax_paths_agree_with_oracle(dev, orc, bits, batch):
         hip.gemv_quant_argmax(w, xd, y, scratch, ids, batch)
         assert from_dev(ids, np.uint32).tolist() == want
         assert not from_dev(scratch, np.uint64).any()
-    np.testing.assert_array_equal(from_dev(y, np.uint16), logits)
+    assert_logits(from_dev(y, np.uint16), logits, n, k, batch)
     # (2) reference pair: head argmax (no logits) + token tail
     best = zeros_dev((batch,), np.uint64)
     tok = empty_dev((batch,), np.uint32)
@@ -200,8 +230,9 @@ def test_dequant_bit_exact(dev, orc, bits):
 
 @pytest.mark.parametrize("bits,batch", [(4, 1), (6, 1), (6, 8)])
 def test_lm_head_full_size(dev, orc, bits, batch):
-    """Configs 2 and 5 at their full 65536 x 2048 shape: every logit is
-    bit-exact against the oracle and the ids are the oracle's argmax."""
+    """Configs 2 and 5 at their full 65536 x 2048 shape: logits against the
+    oracle (bit-exact at batch 1, within tolerance at batch 8) and the ids
+    are the oracle's argmax."""
     _log(f"lm head full bits={bits} batch={batch}")
     rng = np.random.default_rng(2026 + bits + batch)
     n, k = 65536, 2048
@@ -215,5 +246,61 @@ def test_lm_head_full_size(dev, orc, bits, batch):
     got = from_dev(y, np.uint16)
     got_ids = from_dev(ids, np.uint32)
     want = orc.gemv_quant(h, x, batch)
-    np.testing.assert_array_equal(got, want)
+    assert_logits(got, want, n, k, batch)
     assert got_ids.tolist() == [orc.argmax_bf16(want[b]) for b in range(batch)]
+
+
+def _argmax_case(dev, orc, h, x, batch):
+    w, keep = dev_quant(h)
+    logits = orc.gemv_quant(h, x, batch)
+    want = [orc.argmax_bf16(logits[b]) for b in range(batch)]
+    y = empty_dev((batch, h.n), np.uint16)
+    scratch = zeros_dev((hip.argmax_scratch_words(batch),), np.uint64)
+    ids = empty_dev((batch,), np.uint32)
+    for _ in range(2):
+        hip.gemv_quant_argmax(w, to_dev(x), y, scratch, ids, batch)
+        assert from_dev(ids, np.uint32).tolist() == want
+        assert not from_dev(scratch, np.uint64).any()
+    assert_logits(from_dev(y, np.uint16), logits, h.n, h.k, batch)
+    return want
+
+
+@pytest.mark.parametrize("bits", [4, 6])
+def test_mfma_argmax_exact_ties(dev, orc, bits):
+    """Matrix-core argmax with exact ties: the winning row copied to a lower
+    and a higher index (equal bounds, so the finisher recomputes every row
+    in chunk order); the lowest index must win."""
+    _log(f"mfma argmax ties bits={bits}")
+    rng = np.random.default_rng(313 + bits)
+    n, k, batch = 2048, 2048, 3
+    h = layout.synth_quant(rng, n, k, bits)
+    x = layout.synth_bf16(rng, (batch, k))
+    top = orc.argmax_bf16(orc.gemv_quant(h, x, batch)[0])
+    for dst in (5, min(n - 1, top + 700)):
+        h.codes[dst] = h.codes[top]
+        h.scales[dst] = h.scales[top]
+        h.biases[dst] = h.biases[top]
+    want = _argmax_case(dev, orc, h, x, batch)
+    assert want[0] == min(5, top)
+
+
+@pytest.mark.parametrize("bits", [4, 6])
+def test_mfma_argmax_near_ties(dev, orc, bits):
+    """Rows that differ from the winner in one code: values apart by one
+    scale times one activation, often the same bf16 value, decided only by
+    the chunk-order recomputation of the candidates."""
+    _log(f"mfma argmax near ties bits={bits}")
+    rng = np.random.default_rng(919 + bits)
+    n, k, batch = 4096, 2048, 2
+    h = layout.synth_quant(rng, n, k, bits)
+    x = layout.synth_bf16(rng, (batch, k))
+    top = orc.argmax_bf16(orc.gemv_quant(h, x, batch)[1])
+    words = h.codes.shape[1]
+    for j, dst in enumerate((3, 1000, 2047, 4095)):
+        if dst == top:
+            continue
+        h.codes[dst] = h.codes[top]
+        h.scales[dst] = h.scales[top]
+        h.biases[dst] = h.biases[top]
+        h.codes[dst, (7 * j + 1) % words] ^= np.uint32(1 << (3 * j))
+    _argmax_case(dev, orc, h, x, batch)
