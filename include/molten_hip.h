@@ -108,7 +108,10 @@ int mh_dequant_q4_bf16_bulk(const mh_quant_weights* w, uint16_t* out, mh_stream_
  * src/kernels/lfm.rs:112 gemv_quant: y[b, :] = bf16(W x[b, :]), f32
  * accumulation in the chunk order, bits 4 or 6.  `batch` rows of x
  * (1..8; the reference has batch 1).  x bf16 [batch, in], y bf16
- * [batch, out]. */
+ * [batch, out].  Batch 2..8 with group size 64, in <= 2048 (a multiple of
+ * 512), out a multiple of 16 and x 16-byte aligned runs on the matrix cores:
+ * f32 sums in the MFMA's order, logits within one bf16 ulp (plus f32
+ * rounding) of the chunk order instead of bit-equal. */
 int mh_gemv_quant(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint32_t batch,
                   mh_stream_t stream);
 
@@ -120,8 +123,11 @@ int mh_gemv_head_argmax(const mh_quant_weights* w, const uint16_t* x, uint64_t* 
                         uint32_t batch, mh_stream_t stream);
 
 /* Head GEMV that stores the bf16 logits (y, may be NULL) and writes
- * ids[b] = argmax token of row b in the same launch.  Every workgroup but
- * the last publishes its key for each batch row into its own scratch slot;
+ * ids[b] = argmax token of row b in the same launch; the ids are the
+ * chunk-order argmax on every path (on the matrix-core path, candidates
+ * within a rigorous error bound are recomputed in chunk order).  Every
+ * workgroup but the last publishes its key(s) for each batch row into its
+ * own scratch slots;
  * the last-dispatched workgroup (every other one has started by then) collects
  * the slots, writes the token ids and re-zeroes the slots, so no two
  * workgroups contend on one atomic.  scratch: MH_ARGMAX_SCRATCH_WORDS(batch)

@@ -224,32 +224,36 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
             *reinterpret_cast<mh::u32x4*>(sw + (pc / SS::kRowPieces) * SS::kStrideWords + (pc % SS::kRowPieces) * 4u) = p[i];
         }
         const uint32_t* const mine = sw + static_cast<uint32_t>(lane & 15) * SS::kStrideWords + q * (PW / 4);
+        // the stage's group products first (independent: their LDS reads and
+        // matrix-core chains overlap), then the per-group scaling in order
+        f32x4 pgs[kStageGroups];
 #pragma unroll
         for (int g = 0; g < kStageGroups; ++g) {
-            {
-                const uint32_t ga = g0 + g;
-                Piece<BITS> pg_codes;
-                pg_codes.read(mine + g * PW);
-                uint32_t o[8];
-                pg_codes.widen(o);
-                const mh::u32x4 b0 = xl[(ga * 8u + q) * 16u + n];
-                const mh::u32x4 b1 = xl[(ga * 8u + 4u + q) * 16u + n];
-                const float xgv = xg[ga * 16u + n];
-                f32x4 pg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(o[0], o[1], o[2], o[3]),
-                                                                   __builtin_bit_cast(bf16x8, b0), zero, 0, 0, 0);
-                pg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(o[4], o[5], o[6], o[7]),
+            const uint32_t ga = g0 + g;
+            Piece<BITS> codes;
+            codes.read(mine + g * PW);
+            uint32_t o[8];
+            codes.widen(o);
+            const mh::u32x4 b0 = xl[(ga * 8u + q) * 16u + n];
+            const mh::u32x4 b1 = xl[(ga * 8u + 4u + q) * 16u + n];
+            f32x4 pg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(o[0], o[1], o[2], o[3]),
+                                                               __builtin_bit_cast(bf16x8, b0), zero, 0, 0, 0);
+            pgs[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(o[4], o[5], o[6], o[7]),
                                                              __builtin_bit_cast(bf16x8, b1), pg, 0, 0, 0);
-                const float4 s4 = *reinterpret_cast<const float4*>(&sbl[wave][region][0][g][4u * q]);
-                const float4 b4 = *reinterpret_cast<const float4*>(&sbl[wave][region][1][g][4u * q]);
-                acc[0] = __builtin_fmaf(s4.x, pg[0], acc[0]);
-                acc[1] = __builtin_fmaf(s4.y, pg[1], acc[1]);
-                acc[2] = __builtin_fmaf(s4.z, pg[2], acc[2]);
-                acc[3] = __builtin_fmaf(s4.w, pg[3], acc[3]);
-                acc[0] = __builtin_fmaf(b4.x, xgv, acc[0]);
-                acc[1] = __builtin_fmaf(b4.y, xgv, acc[1]);
-                acc[2] = __builtin_fmaf(b4.z, xgv, acc[2]);
-                acc[3] = __builtin_fmaf(b4.w, xgv, acc[3]);
-            }
+        }
+#pragma unroll
+        for (int g = 0; g < kStageGroups; ++g) {
+            const float xgv = xg[(g0 + g) * 16u + n];
+            const float4 s4 = *reinterpret_cast<const float4*>(&sbl[wave][region][0][g][4u * q]);
+            const float4 b4 = *reinterpret_cast<const float4*>(&sbl[wave][region][1][g][4u * q]);
+            acc[0] = __builtin_fmaf(s4.x, pgs[g][0], acc[0]);
+            acc[1] = __builtin_fmaf(s4.y, pgs[g][1], acc[1]);
+            acc[2] = __builtin_fmaf(s4.z, pgs[g][2], acc[2]);
+            acc[3] = __builtin_fmaf(s4.w, pgs[g][3], acc[3]);
+            acc[0] = __builtin_fmaf(b4.x, xgv, acc[0]);
+            acc[1] = __builtin_fmaf(b4.y, xgv, acc[1]);
+            acc[2] = __builtin_fmaf(b4.z, xgv, acc[2]);
+            acc[3] = __builtin_fmaf(b4.w, xgv, acc[3]);
         }
     };
 
