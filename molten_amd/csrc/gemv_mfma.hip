@@ -35,11 +35,12 @@ constexpr uint32_t kMaxK = 2048;
 constexpr uint32_t kMaxG = kMaxK / 64;
 constexpr int kMaxB = 8;
 constexpr int kSlotWords = 6;  // per (batch row, workgroup): lower bound, dropped bound, 4 candidates
+constexpr int kPerKind = kGrid / 64;  // a finisher lane's words of one kind (word kind * kGrid + workgroup)
 constexpr int kCand = 4;
 constexpr uint32_t kArgSlots = MH_ARGMAX_SLOTS;
 constexpr uint32_t kMaxCand = kTileRows * 68;  // finisher's candidate list (a wave's stage buffer)
 constexpr uint32_t kSpinLimit = 1u << 24;
-static_assert((kGrid - 1) * kSlotWords <= kArgSlots, "finisher slots");
+static_assert(kGrid * kSlotWords <= kArgSlots && kGrid % 64 == 0, "finisher slots");
 static_assert(kGrid * kCand <= kMaxCand, "candidate list");
 
 struct MfmaArgs {
@@ -56,6 +57,19 @@ struct MfmaArgs {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// A bf16(q + 128) pair from a field t holding the low code at bit 0 and the
+// high code at bit S: (((t << (16 - S)) | t) & M) | 0x43004300, M = the two
+// code masks.  Written as two instructions (v_lshl_or_b32, v_and_or_b32) so
+// that the compiler cannot split them into more; the exponent word lives in
+// a VGPR (a VOP3 reads at most one SGPR on this target).
+template <int SH>
+__device__ __forceinline__ uint32_t bf16_pair(uint32_t t, uint32_t m, uint32_t e) {
+    uint32_t u, o;
+    asm("v_lshl_or_b32 %0, %1, %2, %1" : "=v"(u) : "v"(t), "n"(SH));
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(o) : "v"(u), "s"(m), "v"(e));
+    return o;
+}
+
 // Codes of one lane for one group (16 codes) and their bf16(q + 128) pairs.
 template <int BITS>
 struct Piece;
@@ -67,12 +81,14 @@ struct Piece<6> {
         w[1] = l[1];
         w[2] = l[2];
     }
-    // pair j: the 12-bit field 12 j .. 12 j + 11 (codes 2j, 2j + 1)
-    __device__ __forceinline__ void widen(uint32_t (&o)[8]) const {
+    // pair j: the 12-bit field 12 j .. 12 j + 11 (codes 2j, 2j + 1); a field's
+    // bits 16..21 must be clear (they would reach the high code), the rest
+    // above bit 11 is masked off
+    __device__ __forceinline__ void widen(uint32_t (&o)[8], uint32_t e) const {
         uint32_t t[8];
         t[0] = w[0] & 0xfffu;
         t[1] = __builtin_amdgcn_ubfe(w[0], 12, 12);
-        t[2] = __builtin_amdgcn_alignbit(w[1], w[0], 24) & 0xfffu;
+        t[2] = __builtin_amdgcn_perm(w[1], w[0], 0x0c0c0403u);  // bytes w0.3, w1.0, 0, 0
         t[3] = __builtin_amdgcn_ubfe(w[1], 4, 12);
         t[4] = __builtin_amdgcn_ubfe(w[1], 16, 12);
         t[5] = __builtin_amdgcn_alignbit(w[2], w[1], 28) & 0xfffu;
@@ -80,8 +96,7 @@ struct Piece<6> {
         t[7] = w[2] >> 20;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            // low code to bits 0..5, high code to bits 16..21, exponent of 128
-            o[j] = (((t[j] << 10) | t[j]) & 0x003f003fu) | 0x43004300u;
+            o[j] = bf16_pair<10>(t[j], 0x003f003fu, e);
         }
     }
 };
@@ -93,11 +108,10 @@ struct Piece<4> {
         w[1] = l[1];
     }
     // pair j: byte j (codes 2j, 2j + 1 are its low and high nibble)
-    __device__ __forceinline__ void widen(uint32_t (&o)[8]) const {
+    __device__ __forceinline__ void widen(uint32_t (&o)[8], uint32_t e) const {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const uint32_t t = __builtin_amdgcn_ubfe(w[j >> 2], 8 * (j & 3), 8);
-            o[j] = (((t << 12) | t) & 0x000f000fu) | 0x43004300u;
+            o[j] = bf16_pair<12>(__builtin_amdgcn_ubfe(w[j >> 2], 8 * (j & 3), 8), 0x000f000fu, e);
         }
     }
 };
@@ -115,19 +129,27 @@ __device__ __forceinline__ float key_value(unsigned long long key) {
     return __uint_as_float((o & 0x7fffffffu & neg) | (~o & ~neg));
 }
 
-// Chunk-order value of one row for batch row b (the staged kernel's formula:
-// lane c owns chunk c, K <= 2048): the exact value the argmax is taken on.
-template <int BITS>
-__device__ float chunk_value(const MfmaArgs& a, uint32_t row, const float (&xr)[32], float xs, bool live,
-                             uint32_t c) {
-    mh::Chunk<BITS> ch;
-    ch.load(reinterpret_cast<const uint32_t*>(a.codes + static_cast<size_t>(row) * a.row_bytes) + c * BITS);
+// Chunk-order values of U rows for one batch row (the staged kernel's
+// formula: lane c owns chunk c, K <= 2048): the exact values the argmax is
+// taken on.  Every row's loads go out before the first dot.
+template <int BITS, int U>
+__device__ void chunk_values(const MfmaArgs& a, const uint32_t (&rows)[U], const float (&xr)[32], float xs,
+                             bool live, uint32_t c, float (&out)[U]) {
+    mh::Chunk<BITS> ch[U];
+    float s[U], b[U];
     const uint32_t g = (32u * c) / 64u;
-    const float s = mh::bf16_to_f32(a.scales[static_cast<size_t>(row) * a.groups + g]);
-    const float b = mh::bf16_to_f32(a.biases[static_cast<size_t>(row) * a.groups + g]);
-    const float p = ch.dot(xr);
-    const float acc = live ? 0.0f + __builtin_fmaf(s, p, b * xs) : 0.0f;
-    return mh::lane63(mh::wave_sum_lane63(acc));
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        ch[u].load(reinterpret_cast<const uint32_t*>(a.codes + static_cast<size_t>(rows[u]) * a.row_bytes) + c * BITS);
+        s[u] = mh::bf16_to_f32(a.scales[static_cast<size_t>(rows[u]) * a.groups + g]);
+        b[u] = mh::bf16_to_f32(a.biases[static_cast<size_t>(rows[u]) * a.groups + g]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const float p = ch[u].dot(xr);
+        const float acc = live ? 0.0f + __builtin_fmaf(s[u], p, b[u] * xs) : 0.0f;
+        out[u] = mh::lane63(mh::wave_sum_lane63(acc));
+    }
 }
 
 // A stage of a tile: 16 rows x kStageGroups groups of codes, loaded with
@@ -192,26 +214,28 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
     };
     // a stage's scales / biases into LDS as f32 (s, b - 128 s), and the
     // rows' running max |s|, |b| (restarted at a tile's first stage)
+    // a stage's scales / biases into LDS as f32 (s, b - 128 s), and the
+    // rows' running max |s|, |b| in registers (bits of non-negative floats
+    // order as integers; every lane of a row's quad holds its row's maxima),
+    // restarted at a tile's first stage
+    uint32_t rms = 0u, rmb = 0u;
     auto stage_sb = [&](int region, uint32_t st, uint32_t sv, uint32_t bv) {
-        float ms = 0.0f, mb = 0.0f;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const float s = e ? mh::bf16hi(sv) : mh::bf16lo(sv);
             const float b = e ? mh::bf16hi(bv) : mh::bf16lo(bv);
             sbl[wave][region][0][sg + e][srow] = s;
             sbl[wave][region][1][sg + e][srow] = __builtin_fmaf(-128.0f, s, b);
-            ms = fmaxf(ms, fabsf(s));
-            mb = fmaxf(mb, fabsf(b));
         }
-        // max over the row's four lanes (lanes 4 srow .. + 3)
-        ms = fmaxf(ms, __shfl_xor(ms, 1));
-        ms = fmaxf(ms, __shfl_xor(ms, 2));
-        mb = fmaxf(mb, __shfl_xor(mb, 1));
-        mb = fmaxf(mb, __shfl_xor(mb, 2));
-        if ((lane & 3) == 0) {
-            mrow[wave][0][srow] = st == 0u ? ms : fmaxf(mrow[wave][0][srow], ms);
-            mrow[wave][1][srow] = st == 0u ? mb : fmaxf(mrow[wave][1][srow], mb);
-        }
+        uint32_t ms = max((sv << 16) & 0x7fffffffu, sv & 0x7fff0000u);
+        uint32_t mb = max((bv << 16) & 0x7fffffffu, bv & 0x7fff0000u);
+        // max over the row's four lanes (lanes 4 srow .. + 3): quad_perm 1,0,3,2 and 2,3,0,1
+        ms = max(ms, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(ms), 0xB1, 0xf, 0xf, false)));
+        mb = max(mb, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mb), 0xB1, 0xf, 0xf, false)));
+        ms = max(ms, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(ms), 0x4E, 0xf, 0xf, false)));
+        mb = max(mb, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(mb), 0x4E, 0xf, 0xf, false)));
+        rms = st == 0u ? ms : max(rms, ms);
+        rmb = st == 0u ? mb : max(rmb, mb);
     };
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     auto compute = [&](int region, uint32_t st, const mh::u32x4(&p)[SS::kLoads]) {
@@ -224,6 +248,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
             *reinterpret_cast<mh::u32x4*>(sw + (pc / SS::kRowPieces) * SS::kStrideWords + (pc % SS::kRowPieces) * 4u) = p[i];
         }
         const uint32_t* const mine = sw + static_cast<uint32_t>(lane & 15) * SS::kStrideWords + q * (PW / 4);
+        const uint32_t kExp = mh::opaque(0x43004300u);  // the exponent word of bf16 128, in a VGPR
         // the stage's group products first (independent: their LDS reads and
         // matrix-core chains overlap), then the per-group scaling in order
         f32x4 pgs[kStageGroups];
@@ -233,7 +258,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
             Piece<BITS> codes;
             codes.read(mine + g * PW);
             uint32_t o[8];
-            codes.widen(o);
+            codes.widen(o, kExp);
             const mh::u32x4 b0 = xl[(ga * 8u + q) * 16u + n];
             const mh::u32x4 b1 = xl[(ga * 8u + 4u + q) * 16u + n];
             f32x4 pg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(o[0], o[1], o[2], o[3]),
@@ -324,9 +349,8 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
     const uint32_t first_c = first < n_tiles ? first : 0u;
     auto tile_c = [&](uint32_t st) { return n_stages > 0u ? tile_of(st < n_stages ? st : last_st) : first_c; };
     auto stage_c = [&](uint32_t st) { return (st < n_stages ? st : last_st) % n_st; };
-    // ---- x to LDS in operand order (columns >= B zero): every thread's x
-    // loads go out first (clamped addresses, no branches), then the first
-    // stages' code loads, then the x stores wait for the x loads only
+    // ---- x to LDS in operand order (columns >= B zero), clamped addresses,
+    // no branches
     constexpr int kXPer = kMaxG * 8 * 16 / kThreads;
     mh::u32x4 xv[kXPer];
 #pragma unroll
@@ -337,20 +361,24 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         const uint4 v = *reinterpret_cast<const uint4*>(a.x + static_cast<size_t>(nc) * K + 64u * gcl + 16u * qq + 8u * t);
         xv[j] = mh::u32x4{v.x, v.y, v.z, v.w};
     }
+    // (every entry is stored, groups >= G included: those hold group 0's x and
+    // are never read).  The first stages' code loads go out only after x has
+    // arrived: queued behind them, x would wait for tens of MB of HBM reads
+    // in flight across the chip.
+#pragma unroll
+    for (int j = 0; j < kXPer; ++j) {
+        const uint32_t u = threadIdx.x + j * kThreads;
+        const bool live_col = u % 16u < static_cast<uint32_t>(B);
+        xl[u] = live_col ? xv[j] : mh::u32x4{0u, 0u, 0u, 0u};
+    }
 #pragma unroll
     for (int u = 0; u < kDepth - 1; ++u) {
         issue(tile_c(u), stage_c(u), pbuf[u], svbuf[u], bvbuf[u]);
     }
-#pragma unroll
-    for (int j = 0; j < kXPer; ++j) {
-        const uint32_t u = threadIdx.x + j * kThreads;
-        if (u / 128u < G) {
-            const bool live_col = u % 16u < static_cast<uint32_t>(B);
-            xl[u] = live_col ? xv[j] : mh::u32x4{0u, 0u, 0u, 0u};
-        }
-    }
     __syncthreads();
-    for (uint32_t u = threadIdx.x; u < G * 16u; u += kThreads) {
+    static_assert(kMaxG * 16 == kThreads, "one group sum per thread");
+    {
+        const uint32_t u = threadIdx.x;
         const uint32_t nb = u % 16u, g = u / 16u;
         float s = 0.0f, sa = 0.0f;
 #pragma unroll
@@ -369,12 +397,21 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         xga[u] = sa;
     }
     __syncthreads();
-    if (threadIdx.x < static_cast<uint32_t>(B)) {
+    // sum |x| per batch row: wave 0, lane l sums groups l / 16 + 4 i of
+    // column l % 16, then the four partial sums are added
+    if (wave == 0) {
+        const uint32_t nb = static_cast<uint32_t>(lane) % 16u, p = static_cast<uint32_t>(lane) / 16u;
         float s = 0.0f;
-        for (uint32_t g = 0; g < G; ++g) {
-            s = s + xga[g * 16u + threadIdx.x];
+#pragma unroll
+        for (uint32_t i = 0; i < kMaxG / 4; ++i) {
+            const uint32_t g = p + 4u * i;
+            s = s + (g < G ? xga[g * 16u + nb] : 0.0f);
         }
-        xa[threadIdx.x] = s;
+        s = s + __shfl_xor(s, 16);
+        s = s + __shfl_xor(s, 32);
+        if (lane < B) {
+            xa[lane] = s;
+        }
     }
     __syncthreads();
 
@@ -389,6 +426,10 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
                 stage_sb(u & 1, st % n_st, svbuf[u], bvbuf[u]);
                 compute(u & 1, st % n_st, pbuf[u]);
                 if (st % n_st == n_st - 1u) {
+                    if ((lane & 3) == 0) {
+                        mrow[wave][0][srow] = __uint_as_float(rms);
+                        mrow[wave][1][srow] = __uint_as_float(rmb);
+                    }
                     finish_tile(tile_of(st));
                     acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                 }
@@ -424,12 +465,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         out[0] = mh::argmax_key(lb, 0u);
 #pragma unroll
         for (int c = 0; c < kCand; ++c) {
-            unsigned long long m = key;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                const unsigned long long o = __shfl_xor(m, off);
-                m = o > m ? o : m;
-            }
+            const unsigned long long m = mh::wave_max_u64(key);
             out[2 + c] = m != 0ull ? m : mh::argmax_key(-__builtin_inff(), 0xffffffffu);
             key = key == m ? 0ull : key;  // keys are distinct (distinct rows)
         }
@@ -437,6 +473,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         dmax = fmaxf(dmax, key != 0ull ? key_value(key) : -__builtin_inff());
         dmax = mh::wave_max_f32(dmax);
         out[1] = mh::argmax_key(dmax, 0u);
+        // word j of this workgroup at slot j * kGrid + workgroup
         if (blockIdx.x != last) {
             if (lane < kSlotWords) {
                 unsigned long long w = out[0];
@@ -444,7 +481,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
                 for (int j = 1; j < kSlotWords; ++j) {
                     w = lane == j ? out[j] : w;
                 }
-                __hip_atomic_store(a.slots + static_cast<size_t>(b) * kArgSlots + blockIdx.x * kSlotWords + lane, w,
+                __hip_atomic_store(a.slots + static_cast<size_t>(b) * kArgSlots + lane * kGrid + blockIdx.x, w,
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         } else if (lane == 0) {
@@ -470,16 +507,21 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         return;
     }
     const uint32_t b = static_cast<uint32_t>(wave);
-    const uint32_t words = last * kSlotWords;
-    constexpr int kPer = ((kGrid - 1) * kSlotWords + 63) / 64;  // words per lane
-    static_assert(kPer <= 32, "pending mask");
+    // word j: kind j / kPerKind, workgroup lane + 64 (j % kPerKind)
+    constexpr int kWords = kSlotWords * kPerKind;
+    static_assert(kWords <= 32, "pending mask");
     unsigned long long* const sl = a.slots + static_cast<size_t>(b) * kArgSlots;
-    unsigned long long v[kPer];
+    auto word_at = [&](int j) {
+        return static_cast<uint32_t>(j / kPerKind) * kGrid + static_cast<uint32_t>(lane) + 64u * (j % kPerKind);
+    };
+    auto word_valid = [&](int j) { return static_cast<uint32_t>(lane) + 64u * (j % kPerKind) < last; };
+    unsigned long long v[kWords];
     uint32_t pend = 0;
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        const uint32_t i = static_cast<uint32_t>(lane) + 64u * j;
-        v[j] = i < words ? __hip_atomic_load(sl + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1ull;
+    for (int j = 0; j < kWords; ++j) {
+        // missing workgroups read as 1: high word 0 (the least key), low word
+        // nonzero, never a candidate
+        v[j] = word_valid(j) ? __hip_atomic_load(sl + word_at(j), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1ull;
         pend |= (v[j] == 0ull ? 1u : 0u) << j;
     }
     uint32_t spins = 0;
@@ -487,58 +529,50 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         __builtin_amdgcn_s_sleep(1);
         // all of a round's loads in flight together, then the checks
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) {
+        for (int j = 0; j < kWords; ++j) {
             if ((pend >> j) & 1u) {
-                v[j] = __hip_atomic_load(sl + lane + 64u * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                v[j] = __hip_atomic_load(sl + word_at(j), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) {
+        for (int j = 0; j < kWords; ++j) {
             if (v[j] != 0ull) {
                 pend &= ~(1u << j);
             }
         }
     }
     const bool lost = __any(pend != 0u);
-    float lb = lane == 0 ? key_value(own[b][0]) : -__builtin_inff();
-    float dmax = lane == 0 ? key_value(own[b][1]) : -__builtin_inff();
-    // word i = lane + 64 j has kind i % 6 (64 = 4 mod 6): branch-free scan
-    uint32_t kinds[kPer];
-    {
-        uint32_t kd = static_cast<uint32_t>(lane) % kSlotWords;
+    // lower bounds (kind 0) and dropped bounds (kind 1): maxima of the keys'
+    // orderable high words
+    uint32_t olb = lane == 0 ? static_cast<uint32_t>(own[b][0] >> 32) : 0u;
+    uint32_t odu = lane == 0 ? static_cast<uint32_t>(own[b][1] >> 32) : 0u;
 #pragma unroll
-        for (int j = 0; j < kPer; ++j) {
-            kinds[j] = kd;
-            kd = kd + 4u >= kSlotWords ? kd + 4u - kSlotWords : kd + 4u;
-        }
+    for (int j = 0; j < kPerKind; ++j) {
+        olb = max(olb, static_cast<uint32_t>(v[j] >> 32));
+        odu = max(odu, static_cast<uint32_t>(v[kPerKind + j] >> 32));
     }
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        const bool valid = static_cast<uint32_t>(lane) + 64u * j < words;
-        const float val = key_value(v[j]);
-        lb = valid && kinds[j] == 0u ? fmaxf(lb, val) : lb;
-        dmax = valid && kinds[j] == 1u ? fmaxf(dmax, val) : dmax;
-    }
-    lb = mh::wave_max_f32(lb);
-    dmax = mh::wave_max_f32(dmax);
+    const float lb = key_value(static_cast<unsigned long long>(mh::wave_max_u32(olb)) << 32);
+    const float dmax = key_value(static_cast<unsigned long long>(mh::wave_max_u32(odu)) << 32);
+    // a candidate's bf16 upper bound reaches lb: one compare of the high word
+    const uint32_t thr = mh::bf16_ge_threshold(lb);
     // candidates (row ids) into this wave's stage buffer (free now)
     uint32_t* const cand = stg[wave];
     uint32_t nc = 0;
     auto collect = [&](unsigned long long key, bool valid) {
-        const uint32_t r = ~static_cast<uint32_t>(key & 0xffffffffull);
-        const bool take = valid && r != 0xffffffffu && mh::round_bf16(key_value(key)) >= lb;
+        const bool take = valid && static_cast<uint32_t>(key) != 0u && static_cast<uint32_t>(key >> 32) >= thr;
         const unsigned long long m = __ballot(take);
         if (m != 0ull) {  // uniform: most words hold no candidate
             if (take) {
                 cand[nc + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u))] = r;
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u))] =
+                    ~static_cast<uint32_t>(key);
             }
             nc += static_cast<uint32_t>(__popcll(m));
         }
     };
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        collect(v[j], static_cast<uint32_t>(lane) + 64u * j < words && kinds[j] >= 2u);
+    for (int j = 2 * kPerKind; j < kWords; ++j) {
+        collect(v[j], word_valid(j));
     }
     collect(lane < kCand ? own[b][2 + (lane < kCand ? lane : 0)] : 0ull, lane < kCand);
     const bool all_rows = !(mh::round_bf16(dmax) < lb);
@@ -546,8 +580,9 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
     if (!all_rows && nc == 1u) {
         id = cand[0];
     } else {
-        // chunk-order values of the candidates (or of every row); the staged
-        // kernel's merge: NaN never wins, with no other value (-inf, 0)
+        // chunk-order values of the candidates (or of every row), four rows'
+        // loads at a time; the staged kernel's merge: NaN never wins, with no
+        // other value (-inf, 0)
         const uint32_t C = K / 32u;
         const bool live = static_cast<uint32_t>(lane) < C;
         const uint32_t c = live ? static_cast<uint32_t>(lane) : 0u;
@@ -558,12 +593,22 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         }
         const uint32_t count = all_rows ? a.n : nc;
         unsigned long long best = mh::argmax_key(-__builtin_inff(), 0u);
-        for (uint32_t i = 0; i < count; ++i) {
-            const uint32_t row = all_rows ? i : cand[i];
-            const float val = mh::round_bf16(chunk_value<BITS>(a, row, xr, xs, live, c));
-            if (val == val) {
-                const unsigned long long key = mh::argmax_key(val, row);
-                best = key > best ? key : best;
+        for (uint32_t i0 = 0; i0 < count; i0 += 4u) {
+            uint32_t rows[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t i = i0 + u < count ? i0 + u : count - 1u;
+                rows[u] = all_rows ? i : cand[i];
+            }
+            float vals[4];
+            chunk_values<BITS, 4>(a, rows, xr, xs, live, c, vals);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float val = mh::round_bf16(vals[u]);
+                if (val == val) {
+                    const unsigned long long key = mh::argmax_key(val, rows[u]);
+                    best = key > best ? key : best;
+                }
             }
         }
         id = ~static_cast<uint32_t>(best & 0xffffffffull);
@@ -573,10 +618,9 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
     }
     // clear the words for the next launch (last: no later load waits on them)
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        const uint32_t i = static_cast<uint32_t>(lane) + 64u * j;
-        if (i < words) {
-            __hip_atomic_store(sl + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int j = 0; j < kWords; ++j) {
+        if (word_valid(j)) {
+            __hip_atomic_store(sl + word_at(j), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }

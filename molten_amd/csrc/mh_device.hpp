@@ -227,6 +227,62 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t i) {
     return (static_cast<unsigned long long>(o) << 32) | static_cast<unsigned long long>(~i);
 }
 
+// The orderable high word of argmax_key for the least f32 h whose bf16
+// rounding (nearest even) is >= lb, lb a bf16 value or -inf: for h not NaN,
+// round_bf16(h) >= lb exactly when (argmax_key(h, .) >> 32) >= the result.
+// For lb > 0 that h is the midpoint below lb (lb's mantissa even: the tie
+// rounds up to lb) or the next f32 above it; for lb <= -0 the midpoint below
+// |lb| in magnitude, bounded the other way; for +-0, -(0x8000 in bits), the
+// last negative value that still rounds to -0.  (Checked exhaustively over
+// every bf16 lb and the f32 values around its neighbours.)
+__device__ __forceinline__ uint32_t bf16_ge_threshold(float lb) {
+    const uint32_t L = __float_as_uint(lb);
+    uint32_t t;
+    if (L == 0xff800000u) {
+        t = L;
+    } else if ((L << 1) == 0u) {
+        t = 0x80008000u;
+    } else if (!(L & 0x80000000u)) {
+        t = (L - 0x8000u) + ((L >> 16) & 1u);
+    } else {
+        const uint32_t m = (L & 0x7fffffffu) + 0x8000u;
+        t = 0x80000000u | (m - ((L >> 16) & 1u));
+    }
+    return static_cast<uint32_t>(argmax_key(__uint_as_float(t), 0u) >> 32);
+}
+
+// Wave max of a u32 / u64 (0 is the identity), as a uniform value: the DPP
+// tree of wave_max_f32, both halves of a u64 moved together.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x111, 0xf, 0xf, false)));
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x112, 0xf, 0xf, false)));
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x114, 0xf, 0xf, false)));
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x118, 0xf, 0xf, false)));
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x142, 0xa, 0xf, false)));
+    v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x143, 0xc, 0xf, false)));
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ unsigned long long dpp_max_u64(unsigned long long v) {
+    const uint32_t lo = static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(v)), CTRL, ROW_MASK, 0xf, false));
+    const uint32_t hi = static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(v >> 32)), CTRL, ROW_MASK, 0xf, false));
+    const unsigned long long o = (static_cast<unsigned long long>(hi) << 32) | lo;
+    return o > v ? o : v;
+}
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+    v = dpp_max_u64<0x111, 0xf>(v);
+    v = dpp_max_u64<0x112, 0xf>(v);
+    v = dpp_max_u64<0x114, 0xf>(v);
+    v = dpp_max_u64<0x118, 0xf>(v);
+    v = dpp_max_u64<0x142, 0xa>(v);
+    v = dpp_max_u64<0x143, 0xc>(v);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), 63));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), 63));
+    return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+
 __device__ __forceinline__ void argmax_merge(float& bv, uint32_t& bi, float v, uint32_t i) {
     if (v > bv || (v == bv && i < bi)) {
         bv = v;
