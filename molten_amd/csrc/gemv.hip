@@ -37,6 +37,16 @@ __device__ __forceinline__ unsigned long long amax(unsigned long long* p, unsign
     return __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Atomic max that first reads the word and skips the atomic when it already
+// holds a key >= v (it only grows, so the result is the same).  Device-scope
+// atomics on one word serialize (~12 ns each); most workgroups finish after
+// a greater key is in and issue none.
+__device__ __forceinline__ void amax_if_greater(unsigned long long* p, unsigned long long v) {
+    if (v > __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+        amax(p, v);
+    }
+}
+
 // Argmax epilogue with the finisher.  Keys are published by "units" (waves
 // of the batch-1 kernel, workgroups of the staged kernel) into their own
 // slots, so no two units contend on one address.  The last workgroup of the
@@ -94,22 +104,19 @@ __device__ void collect_keys(const GemvArgs& a, uint32_t n_units, const unsigned
                 __hip_atomic_store(sl + j * kThreads, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const unsigned long long o = __shfl_xor(m, off);
-            m = o > m ? o : m;
-        }
+        m = mh::wave_max_u64(m);
         const bool any_lost = __syncthreads_or(lost) != 0;
         if (lane == 0) {
             sk[wave] = m;
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
-            unsigned long long t = own[b];
-            for (int w = 0; w < kWaves; ++w) {
-                t = sk[w] > t ? sk[w] : t;
+        // wave 0: the waves' maxima and the collector's own key
+        if (wave == 0) {
+            const unsigned long long t =
+                mh::wave_max_u64(lane < kWaves ? sk[lane < kWaves ? lane : 0] : (lane == kWaves ? own[b] : 0ull));
+            if (lane == 0) {
+                a.ids[b] = any_lost ? 0xffffffffu : ~static_cast<uint32_t>(t & 0xffffffffull);
             }
-            a.ids[b] = any_lost ? 0xffffffffu : ~static_cast<uint32_t>(t & 0xffffffffull);
         }
         __syncthreads();
     }
@@ -144,7 +151,7 @@ __device__ void finish_argmax(const GemvArgs& a, const float (&bv)[B], const uin
     }
     if (a.slots == nullptr) {
         if (threadIdx.x < B) {
-            amax(a.best + threadIdx.x, key);
+            amax_if_greater(a.best + threadIdx.x, key);
         }
         return;
     }
@@ -287,32 +294,29 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
     if (!ARGMAX) {
         return;
     }
+    // workgroup key: the waves' keys, maxed by wave 0 (one publication or
+    // atomic per workgroup)
     const unsigned long long key = wave_argmax_key(lbv, lbi);
-    if (a.slots == nullptr) {
-        if (lane == 0) {
-            amax(a.best, key);
-        }
-        return;
-    }
-    // workgroup key (one slot per workgroup), then publish or collect
     __shared__ unsigned long long wk[kWaves];
     __shared__ unsigned long long own[1];
     if (lane == 0) {
         wk[wave] = key;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned long long t = wk[0];
-        for (int w = 1; w < kWaves; ++w) {
-            t = wk[w] > t ? wk[w] : t;
-        }
-        own[0] = t;
-    }
     const uint32_t last = gridDim.x - 1;
-    if (blockIdx.x != last) {
-        if (threadIdx.x == 0) {
-            publish_key(a, 0, blockIdx.x, own[0]);
+    if (wave == 0) {
+        const unsigned long long t = mh::wave_max_u64(lane < kWaves ? wk[lane < kWaves ? lane : 0] : 0ull);
+        if (lane == 0) {
+            if (a.slots == nullptr) {
+                amax_if_greater(a.best, t);
+            } else if (blockIdx.x != last) {
+                publish_key(a, 0, blockIdx.x, t);
+            } else {
+                own[0] = t;
+            }
         }
+    }
+    if (a.slots == nullptr || blockIdx.x != last) {
         return;
     }
     __syncthreads();
