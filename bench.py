@@ -40,6 +40,9 @@ BYTES = {
     "config3": 21_504_000,
     "config5_b1": 109_187_076,
     "config5_b8": 110_133_280,
+    # the decode epilogue variants (proj3, conv3) at the model's shapes
+    "next_proj3_gemv_scatter": 3_549_184,  # 3072 rows x (1024 code + 128 s/b) B + x + outputs
+    "next_conv3_gemv": 7_114_752,          # 6144 rows x 1152 B + x + taps + state in/out + out
 }
 FLOPS_CONFIG4 = 309_237_645_312
 
@@ -135,6 +138,31 @@ def bench_config1(torch, hip, dev, gen, steps, warmup):
     ms = timed(torch, lambda i: hip.gemv_quant(ws[i % copies][0], x, y, 1), steps, warmup)
     del ws
     return ms
+
+
+def bench_next_rows(torch, hip, dev, gen, steps, warmup):
+    """The decode epilogue variants at the model's shapes: proj3 (Q 2048, K 512,
+    V 512 rows into a 4096-position cache) and conv3 (H 2048)."""
+    copies = 96  # 96 x 3.5 MB and 48 x 7.1 MB: beyond the 256 MB Infinity Cache
+    qs = make_quant(torch, 2048, 2048, 4, copies, dev, gen)
+    ks = make_quant(torch, 512, 2048, 4, copies, dev, gen)
+    vs = make_quant(torch, 512, 2048, 4, copies, dev, gen)
+    x = bf16_randn(torch, (2048,), dev, gen)
+    q = torch.empty(2048, dtype=torch.int16, device=dev)
+    k = torch.empty(512, dtype=torch.int16, device=dev)
+    cache = torch.empty((8, 4096, 64), dtype=torch.int16, device=dev)
+    ms_p = timed(torch, lambda i: hip.proj3_gemv_scatter(qs[i % copies][0], ks[i % copies][0], vs[i % copies][0],
+                                                         x, q, k, cache, 4096, i % 4096), steps, warmup)
+    del qs, ks, vs
+    H = 2048
+    ws = make_quant(torch, 3 * H, 2048, 4, copies // 2, dev, gen)
+    taps = bf16_randn(torch, (H, 3), dev, gen, std=0.5)
+    states = [bf16_randn(torch, (2, H), dev, gen) for _ in range(2)]
+    out = torch.empty(H, dtype=torch.int16, device=dev)
+    ms_c = timed(torch, lambda i: hip.conv3_gemv(ws[i % (copies // 2)][0], x, taps, states[i % 2], out,
+                                                 states[(i + 1) % 2]), steps, warmup)
+    del ws
+    return ms_p, ms_c
 
 
 def moe_set(torch, dev, gen, E=64, H=2048, I=1536):
@@ -288,6 +316,12 @@ def main() -> int:
         others["config1_q4_gemv_2048"] = dict(
             value=round(BYTES["config1"] / (ms1 * 1e-3) / 1e9, 1), unit="GB/s",
             ms_per_step=round(ms1, 5), frac_of_hbm_peak=round(BYTES["config1"] / (ms1 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+        log("next rows: proj3_gemv_scatter, conv3_gemv")
+        ms_p, ms_c = bench_next_rows(torch, hip, dev, gen, steps, warmup)
+        for key, ms in (("next_proj3_gemv_scatter", ms_p), ("next_conv3_gemv", ms_c)):
+            v = BYTES[key] / (ms * 1e-3) / 1e9
+            others[key] = dict(value=round(v, 1), unit="GB/s", ms_per_step=round(ms, 5),
+                               frac_of_hbm_peak=round(v / HBM_PEAK_GBS, 4))
         log("config 3: MoE decode step")
         ms3 = bench_config3(torch, hip, dev, gen, steps, warmup)
         v3 = BYTES["config3"] / (ms3 * 1e-3) / 1e9

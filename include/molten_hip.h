@@ -139,6 +139,27 @@ int mh_gemv_head_argmax(const mh_quant_weights* w, const uint16_t* x, uint64_t* 
 int mh_gemv_quant_argmax(const mh_quant_weights* w, const uint16_t* x, uint16_t* y,
                          uint64_t* scratch, uint32_t* ids, uint32_t batch, mh_stream_t stream);
 
+/* src/kernels/lfm.rs:155-218 proj3_gemv_scatter (lfm.metal:1023-1067): the
+ * Q, K and V projections of one x in one launch; q_out[NQ], k_out[NK] bf16,
+ * V row j written to v_cache[((j / 64) * max_seq + pos) * 64 + j % 64]
+ * (v_cache bf16 [NV / 64, max_seq, 64]).  Rows are mh_gemv_quant's values.
+ * Q4, group 64, in_features a multiple of 128 up to 2048 (the reference:
+ * exactly its hidden size 2048), NV a multiple of 64, pos < max_seq. */
+int mh_proj3_gemv_scatter(const mh_quant_weights* q, const mh_quant_weights* k,
+                          const mh_quant_weights* v, const uint16_t* x, uint16_t* q_out,
+                          uint16_t* k_out, uint16_t* v_cache, uint32_t max_seq, uint32_t pos,
+                          mh_stream_t stream);
+
+/* src/kernels/lfm.rs:220-256 conv3_gemv (lfm.metal:1074-1109): the decode
+ * short-conv input projection and the conv.  wproj has 3H rows (B, C, X
+ * blocks of H); taps bf16 [H, 3]; state, new_state bf16 [2, H]; out bf16 [H].
+ * Per channel c: B, C, X = bf16 rows c, H + c, 2H + c; v2 = bf16(B X);
+ * z = t0 state[c] + t1 state[H + c] + t2 v2; out[c] = bf16(C bf16(z));
+ * new_state[c] = state[H + c], new_state[H + c] = v2.  Same shape limits as
+ * mh_proj3_gemv_scatter. */
+int mh_conv3_gemv(const mh_quant_weights* wproj, const uint16_t* x, const uint16_t* taps,
+                  const uint16_t* state, uint16_t* out, uint16_t* new_state, mh_stream_t stream);
+
 /* src/kernels/lfm.rs:850 token_tail without `next`: out_tok[b] = token of
  * key best[b]; best[b] is cleared. */
 int mh_token_tail(uint64_t* best, uint32_t* out_tok, uint32_t batch, mh_stream_t stream);

@@ -81,6 +81,8 @@ _SIGNATURES = {
     "mh_gemv_quant": [_qw, _vp, _vp, _u32, _vp],
     "mh_gemv_head_argmax": [_qw, _vp, _vp, _u32, _vp],
     "mh_gemv_quant_argmax": [_qw, _vp, _vp, _vp, _vp, _u32, _vp],
+    "mh_proj3_gemv_scatter": [_qw, _qw, _qw, _vp, _vp, _vp, _vp, _u32, _u32, _vp],
+    "mh_conv3_gemv": [_qw, _vp, _vp, _vp, _vp, _vp, _vp],
     "mh_token_tail": [_vp, _vp, _u32, _vp],
     "mh_argmax_bf16": [_vp, _u32, _vp, _vp, _vp],
     "mh_gemv_f32": [_vp, _vp, _vp, _u32, _u32, _vp],
@@ -288,6 +290,20 @@ def router_route(w, x, logits, bias, ids, weights, counter, e: int, k: int, topk
     check(load().mh_router_route(_ptr(w), _dtype_of(w), _ptr(x), _ptr(logits), _ptr(bias),
                                  _ptr(ids), _ptr(weights), _ptr(counter), e, k, topk, mode, eps,
                                  _stream(stream)), "router_route")
+
+
+def proj3_gemv_scatter(q: QuantWeights, k: QuantWeights, v: QuantWeights, x, q_out, k_out, v_cache,
+                       max_seq: int, pos: int, stream=None) -> None:
+    """src/kernels/lfm.rs:155 (q_out, k_out stored; V rows into v_cache at pos)."""
+    check(load().mh_proj3_gemv_scatter(_qref(q), _qref(k), _qref(v), _ptr(x), _ptr(q_out),
+                                       _ptr(k_out), _ptr(v_cache), max_seq, pos, _stream(stream)),
+          "proj3_gemv_scatter")
+
+
+def conv3_gemv(wproj: QuantWeights, x, taps, state, out, new_state, stream=None) -> None:
+    """src/kernels/lfm.rs:220 (the decode short conv with its input projection)."""
+    check(load().mh_conv3_gemv(_qref(wproj), _ptr(x), _ptr(taps), _ptr(state), _ptr(out),
+                               _ptr(new_state), _stream(stream)), "conv3_gemv")
 
 
 def gemv_gather_act(gate: QuantWeights, up: QuantWeights, x, ids, act, topk: int, n_inter: int,

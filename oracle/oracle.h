@@ -89,6 +89,22 @@ void orc_gemv_quant(const orc_qw* w, const uint16_t* x, uint32_t batch,
 void orc_gemv_quant_rows(const orc_qw* w, const uint16_t* x, uint32_t batch,
                          const uint32_t* rows, uint32_t n_rows, uint16_t* y);
 
+/* ---- next rows: decode GEMV epilogue variants on the same row values ---
+ * proj3 (lfm.metal:1023-1067; src/kernels/lfm.rs:155-218): q_out, k_out =
+ * bf16 rows of q, k; v row j into v_cache[((j / 64) * max_seq + pos) * 64 +
+ * j % 64].  Pinned: equal to orc_gemv_quant of each matrix with the cache
+ * index computed independently in the test.
+ * conv3 (lfm.metal:1074-1109; src/kernels/lfm.rs:220-256): w has 3H rows;
+ * per channel c: B, C, X = bf16 rows c, H + c, 2H + c; v2 = bf16(B X);
+ * z = w0 state[c] + w1 state[H + c] + w2 v2; out[c] = bf16(C bf16(z));
+ * new_state = [state[H + c], v2].  Pinned: one-hot tap cases that reduce to
+ * the inputs (w = e0: out = bf16(C s0); w = e2: out = bf16(C v2)), the state
+ * shift, and B X against the GEMV rows. */
+void orc_proj3(const orc_qw* q, const orc_qw* k, const orc_qw* v, const uint16_t* x,
+               uint16_t* q_out, uint16_t* k_out, uint16_t* v_cache, uint32_t max_seq, uint32_t pos);
+void orc_conv3(const orc_qw* w, const uint16_t* x, const uint16_t* taps, const uint16_t* state,
+               uint16_t* out, uint16_t* new_state);
+
 /* ---- a6: argmax over bf16 logits (lfm.metal:1113-1282) ------------------
  * value desc, index asc; -0 == +0; NaN never taken; none -> 0.  Pinned by
  * known-answer ties and numpy argmax on tie-free rows. */

@@ -124,6 +124,31 @@ def gemv_quant(h, x: np.ndarray, batch: int = 1, want_f32: bool = False):
     return (y, yf) if want_f32 else y
 
 
+def proj3(hq, hk, hv, x: np.ndarray, max_seq: int, pos: int, v_cache: np.ndarray):
+    """q, k rows and the v rows written into v_cache (updated in place)."""
+    x = np.ascontiguousarray(x, np.uint16)
+    assert v_cache.dtype == np.uint16 and v_cache.flags.c_contiguous
+    q = np.empty(hq.n, np.uint16)
+    k = np.empty(hk.n, np.uint16)
+    wq, wk, wv = qw(hq), qw(hk), qw(hv)
+    lib().orc_proj3(ctypes.byref(wq), ctypes.byref(wk), ctypes.byref(wv), _p(x), _p(q), _p(k),
+                    _p(v_cache), ctypes.c_uint32(max_seq), ctypes.c_uint32(pos))
+    return q, k
+
+
+def conv3(h, x: np.ndarray, taps: np.ndarray, state: np.ndarray):
+    """(out [H], new_state [2, H]) of the decode short conv."""
+    x = np.ascontiguousarray(x, np.uint16)
+    taps = np.ascontiguousarray(taps, np.uint16)
+    state = np.ascontiguousarray(state, np.uint16)
+    H = h.n // 3
+    out = np.empty(H, np.uint16)
+    new_state = np.empty((2, H), np.uint16)
+    w = qw(h)
+    lib().orc_conv3(ctypes.byref(w), _p(x), _p(taps), _p(state), _p(out), _p(new_state))
+    return out, new_state
+
+
 def gemv_quant_rows(h, x: np.ndarray, rows: np.ndarray, batch: int = 1) -> np.ndarray:
     x = np.ascontiguousarray(x, np.uint16)
     rows = np.ascontiguousarray(rows, np.uint32)

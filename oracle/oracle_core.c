@@ -240,6 +240,66 @@ void orc_gemv_quant_rows(const orc_qw* w, const uint16_t* x, uint32_t batch,
     free(xf);
 }
 
+/* ----------------------------------------- decode GEMV epilogue variants --- */
+
+/* lfm.metal:1023-1067 lfm_proj3_gemv_scatter_bf16: rows of q, k and v
+ * against one x; q and k stored, v row j stored into the cache at
+ * ((j / 64) * max_seq + pos) * 64 + j % 64. */
+void orc_proj3(const orc_qw* q, const orc_qw* k, const orc_qw* v, const uint16_t* x,
+               uint16_t* q_out, uint16_t* k_out, uint16_t* v_cache, uint32_t max_seq, uint32_t pos) {
+    const uint32_t K = q->k, C = K / 32;
+    float* xf = to_f32(x, K);
+    float* xs = (float*)malloc((size_t)C * sizeof(float));
+    chunk_xsums(xf, K, xs);
+    const long total = (long)q->n + k->n + v->n;
+#pragma omp parallel for schedule(static) num_threads(ORC_THREADS)
+    for (long row = 0; row < total; ++row) {
+        if (row < (long)q->n) {
+            q_out[row] = orc_f32_to_bf16(qrow_value(q, (uint32_t)row, xf, xs));
+        } else if (row < (long)(q->n + k->n)) {
+            const uint32_t j = (uint32_t)(row - q->n);
+            k_out[j] = orc_f32_to_bf16(qrow_value(k, j, xf, xs));
+        } else {
+            const uint32_t j = (uint32_t)(row - q->n - k->n);
+            const size_t at = ((size_t)(j / 64u) * max_seq + pos) * 64u + j % 64u;
+            v_cache[at] = orc_f32_to_bf16(qrow_value(v, j, xf, xs));
+        }
+    }
+    free(xs);
+    free(xf);
+}
+
+/* lfm.metal:1074-1109 lfm_conv3_gemv_split_bf16: for channel c < H the rows
+ * c (B), H + c (C) and 2H + c (X) of w, each rounded to bf16; then
+ * v2 = bf16(B X), z = w0 s0 + w1 s1 + w2 v2 (in that order, f32),
+ * out = bf16(C bf16(z)), new_state = [s1, v2] with s0 = state[c],
+ * s1 = state[H + c], taps w_j = taps[3c + j]. */
+void orc_conv3(const orc_qw* w, const uint16_t* x, const uint16_t* taps, const uint16_t* state,
+               uint16_t* out, uint16_t* new_state) {
+    const uint32_t K = w->k, C = K / 32, H = w->n / 3;
+    float* xf = to_f32(x, K);
+    float* xs = (float*)malloc((size_t)C * sizeof(float));
+    chunk_xsums(xf, K, xs);
+#pragma omp parallel for schedule(static) num_threads(ORC_THREADS)
+    for (long cl = 0; cl < (long)H; ++cl) {
+        const uint32_t c = (uint32_t)cl;
+        const float b = bfr(qrow_value(w, c, xf, xs));
+        const float cc = bfr(qrow_value(w, H + c, xf, xs));
+        const float xv = bfr(qrow_value(w, 2u * H + c, xf, xs));
+        const uint16_t s1 = state[H + c];
+        const float v0 = orc_bf16_to_f32(state[c]);
+        const float v1 = orc_bf16_to_f32(s1);
+        const float v2 = bfr(b * xv);
+        const float z = orc_bf16_to_f32(taps[3u * c]) * v0 + orc_bf16_to_f32(taps[3u * c + 1u]) * v1 +
+                        orc_bf16_to_f32(taps[3u * c + 2u]) * v2;
+        out[c] = orc_f32_to_bf16(cc * bfr(z));
+        new_state[H + c] = orc_f32_to_bf16(v2);
+        new_state[c] = s1;
+    }
+    free(xs);
+    free(xf);
+}
+
 /* ------------------------------------------------------------- argmax --- */
 
 uint32_t orc_argmax_bf16(const uint16_t* x, size_t n) {

@@ -84,3 +84,24 @@ def test_bulk_dequant_needs_k_multiple_of_128():
 def test_memcpy_kind_checked():
     lib = hip.load()
     assert lib.mh_memcpy(None, None, 0, 7, None) == hip.MH_ERR_INVALID
+
+
+def test_proj3_and_conv3_arguments():
+    q = _qw(out_features=64)
+    with pytest.raises(hip.MoltenError) as ei:  # pos beyond the cache
+        hip.proj3_gemv_scatter(q, q, q, 0x4000, 0x5000, 0x6000, 0x7000, 8, 8, stream=0)
+    assert ei.value.code == hip.MH_ERR_INVALID
+    with pytest.raises(hip.MoltenError) as ei:  # V rows not whole heads
+        hip.proj3_gemv_scatter(q, q, _qw(out_features=96), 0x4000, 0x5000, 0x6000, 0x7000, 8, 0,
+                               stream=0)
+    assert ei.value.code == hip.MH_ERR_INVALID
+    with pytest.raises(hip.MoltenError) as ei:  # the reference's projections are 4-bit
+        hip.proj3_gemv_scatter(q, _qw(bits=6), q, 0x4000, 0x5000, 0x6000, 0x7000, 8, 0, stream=0)
+    assert ei.value.code == hip.MH_ERR_UNSUPPORTED
+    with pytest.raises(hip.MoltenError) as ei:  # 3H rows
+        hip.conv3_gemv(_qw(out_features=64), 0x4000, 0x5000, 0x6000, 0x7000, 0x8000, stream=0)
+    assert ei.value.code == hip.MH_ERR_INVALID
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.conv3_gemv(_qw(out_features=48, in_features=4096), 0x4000, 0x5000, 0x6000, 0x7000,
+                       0x8000, stream=0)
+    assert ei.value.code == hip.MH_ERR_UNSUPPORTED

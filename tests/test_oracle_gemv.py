@@ -128,3 +128,63 @@ def test_dense_gemv(orc, rng, w_f32):
     for t, e in ((0, 0), (2, 63)):
         want = exact.replay_dense_row(wf[e].astype(np.float32), bf(x[t]))
         assert y[t, e] == want
+
+
+# ---- decode GEMV epilogue variants (lfm.metal:1023-1109) -------------------
+
+def test_proj3_is_three_gemvs_and_a_cache_write(orc, rng):
+    """Pins orc_proj3: q and k equal the GEMV rows; the V rows land at
+    position pos of each 64-wide head of the cache (checked through a reshape,
+    not the index formula) and nothing else in the cache changes."""
+    k, nq, nk, nv, max_seq, pos = 512, 48, 16, 128, 6, 4
+    hq, hk, hv = (layout.synth_quant(rng, n, k, 4) for n in (nq, nk, nv))
+    x = layout.synth_bf16(rng, (1, k))[0]
+    cache = np.full((nv // 64, max_seq, 64), 0x7fc1, np.uint16)
+    q, kk = orc.proj3(hq, hk, hv, x, max_seq, pos, cache)
+    np.testing.assert_array_equal(q, orc.gemv_quant(hq, x)[0])
+    np.testing.assert_array_equal(kk, orc.gemv_quant(hk, x)[0])
+    np.testing.assert_array_equal(cache[:, pos, :], orc.gemv_quant(hv, x)[0].reshape(nv // 64, 64))
+    rest = np.delete(cache, pos, axis=1)
+    assert (rest == 0x7fc1).all()
+
+
+def _bf16_round(v):
+    return layout.bf16_to_f32(layout.f32_to_bf16(np.asarray(v, np.float32)))
+
+
+def test_conv3_reduces_to_its_inputs_for_one_hot_taps(orc, rng):
+    """Pins orc_conv3's indexing: with taps (1, 0, 0) the conv output is
+    bf16(C * state[c]); with (0, 0, 1) it is bf16(C * bf16(B X)); the state
+    shifts (new_state[0] = state[1], new_state[1] = bf16(B X)); B, C, X are
+    the GEMV row blocks 0, H, 2H."""
+    H, k = 40, 512
+    h = layout.synth_quant(rng, 3 * H, k, 4)
+    x = layout.synth_bf16(rng, (1, k))[0]
+    state = layout.synth_bf16(rng, (2, H))
+    rows = layout.bf16_to_f32(orc.gemv_quant(h, x)[0])
+    B, C, X = rows[:H], rows[H:2 * H], rows[2 * H:]
+    bx = _bf16_round(B * X)
+    one = layout.f32_to_bf16(np.float32(1.0))
+    for hot, want in ((0, _bf16_round(C * layout.bf16_to_f32(state[0]))), (2, _bf16_round(C * bx))):
+        taps = np.zeros((H, 3), np.uint16)
+        taps[:, hot] = one
+        out, ns = orc.conv3(h, x, taps, state)
+        np.testing.assert_array_equal(layout.bf16_to_f32(out), want)
+        np.testing.assert_array_equal(ns[0], state[1])
+        np.testing.assert_array_equal(layout.bf16_to_f32(ns[1]), bx)
+
+
+def test_conv3_taps_sum_in_order(orc, rng):
+    """General taps: z = t0 s0 + t1 s1 + t2 v2 in f32, left to right."""
+    H, k = 24, 256
+    h = layout.synth_quant(rng, 3 * H, k, 4)
+    x = layout.synth_bf16(rng, (1, k))[0]
+    state = layout.synth_bf16(rng, (2, H))
+    taps = layout.synth_bf16(rng, (H, 3), std=0.5)
+    out, _ = orc.conv3(h, x, taps, state)
+    rows = layout.bf16_to_f32(orc.gemv_quant(h, x)[0])
+    t = layout.bf16_to_f32(taps)
+    s = layout.bf16_to_f32(state)
+    v2 = _bf16_round(rows[:H] * rows[2 * H:])
+    z = (t[:, 0] * s[0] + t[:, 1] * s[1]).astype(np.float32) + (t[:, 2] * v2).astype(np.float32)
+    np.testing.assert_array_equal(layout.bf16_to_f32(out), _bf16_round(rows[H:2 * H] * _bf16_round(z)))
