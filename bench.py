@@ -43,6 +43,9 @@ BYTES = {
     # the decode epilogue variants (proj3, conv3) at the model's shapes
     "next_proj3_gemv_scatter": 3_549_184,  # 3072 rows x (1024 code + 128 s/b) B + x + outputs
     "next_conv3_gemv": 7_114_752,          # 6144 rows x 1152 B + x + taps + state in/out + out
+    "next_dense_down_q4_k11776": 13_593_600,  # 2048 rows x (5888 code + 736 s/b) B + x + y
+    "next_gather_rows_q6_4096": 23_609_344,   # 4096 x (1536 code + 128 s/b + 4096 out) B + ids
+    "next_token_tail_embed": 13_972,  # key read + clear, token, one Q6 row + s/b, gain, x and normed rows
 }
 FLOPS_CONFIG4 = 309_237_645_312
 
@@ -162,7 +165,32 @@ def bench_next_rows(torch, hip, dev, gen, steps, warmup):
     ms_c = timed(torch, lambda i: hip.conv3_gemv(ws[i % (copies // 2)][0], x, taps, states[i % 2], out,
                                                  states[(i + 1) % 2]), steps, warmup)
     del ws
-    return ms_p, ms_c
+    # the dense FFN down projection (lfm_gemv_q4_bf16_k11776): 2048 x 11776
+    ds = make_quant(torch, 2048, 11776, 4, 24, dev, gen)  # 24 x 13.6 MB
+    xd = bf16_randn(torch, (1, 11776), dev, gen)
+    yd = torch.empty((1, 2048), dtype=torch.int16, device=dev)
+    ms_d = timed(torch, lambda i: hip.gemv_quant(ds[i % 24][0], xd, yd, 1), steps, warmup)
+    del ds
+    # the Q6 embedding table (65536 x 2048): prefill gather of 4096 rows and
+    # the decode token tail (key -> token, its row + RMSNorm)
+    tab = make_quant(torch, 65536, 2048, 6, 1, dev, gen)[0]
+    ids = [torch.randint(0, 65536, (4096,), dtype=torch.int32, device=dev, generator=gen) for _ in range(4)]
+    gout = torch.empty((4096, 2048), dtype=torch.int16, device=dev)
+    ms_g = timed(torch, lambda i: hip.gather_rows_q6(tab[0], ids[i % 4], 4096, gout), steps, warmup)
+    keys = torch.randint(0, 65536, (steps + warmup + 8,), dtype=torch.int64, device=dev, generator=gen)
+    keys = (keys ^ 0xffffffff) | (0x40000000 << 32)  # low word ~token
+    best = torch.empty(1, dtype=torch.int64, device=dev)
+    tok = torch.empty(1, dtype=torch.int32, device=dev)
+    gain = bf16_randn(torch, (2048,), dev, gen)
+    xe = torch.empty(2048, dtype=torch.int16, device=dev)
+    ne = torch.empty(2048, dtype=torch.int16, device=dev)
+
+    def tail(i):  # (timed with the copy that refills the key the tail clears)
+        best.copy_(keys[i:i + 1])
+        hip.token_tail_embed(best, tok, tab[0], gain, xe, ne, 1e-5)
+
+    ms_t = timed(torch, tail, steps, warmup)
+    return ms_p, ms_c, ms_d, ms_g, ms_t
 
 
 def moe_set(torch, dev, gen, E=64, H=2048, I=1536):
@@ -316,9 +344,11 @@ def main() -> int:
         others["config1_q4_gemv_2048"] = dict(
             value=round(BYTES["config1"] / (ms1 * 1e-3) / 1e9, 1), unit="GB/s",
             ms_per_step=round(ms1, 5), frac_of_hbm_peak=round(BYTES["config1"] / (ms1 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
-        log("next rows: proj3_gemv_scatter, conv3_gemv")
-        ms_p, ms_c = bench_next_rows(torch, hip, dev, gen, steps, warmup)
-        for key, ms in (("next_proj3_gemv_scatter", ms_p), ("next_conv3_gemv", ms_c)):
+        log("next rows: proj3, conv3, dense down K=11776, Q6 gather, token tail")
+        ms_p, ms_c, ms_d, ms_g, ms_t = bench_next_rows(torch, hip, dev, gen, steps, warmup)
+        for key, ms in (("next_proj3_gemv_scatter", ms_p), ("next_conv3_gemv", ms_c),
+                        ("next_dense_down_q4_k11776", ms_d), ("next_gather_rows_q6_4096", ms_g),
+                        ("next_token_tail_embed", ms_t)):
             v = BYTES[key] / (ms * 1e-3) / 1e9
             others[key] = dict(value=round(v, 1), unit="GB/s", ms_per_step=round(ms, 5),
                                frac_of_hbm_peak=round(v / HBM_PEAK_GBS, 4))

@@ -164,6 +164,22 @@ int mh_conv3_gemv(const mh_quant_weights* wproj, const uint16_t* x, const uint16
  * key best[b]; best[b] is cleared. */
 int mh_token_tail(uint64_t* best, uint32_t* out_tok, uint32_t batch, mh_stream_t stream);
 
+/* src/kernels/lfm.rs:850-888 token_tail with `next` (lfm.metal:1284-1386):
+ * out_tok[0] = token of key best[0] (cleared); then the token's row of the Q6
+ * embedding table e (6-bit, group 64, width K <= 2048, a multiple of 64) is
+ * dequantized into x [K] (bf16(fma(s, q, b))) and RMSNorm'd into normed [K]:
+ * bf16((x * inv) * w), inv = 1 / sqrt(sum x^2 / K + eps).  w, x, normed
+ * 16-byte aligned.  A token outside the table (an empty key) writes no rows. */
+int mh_token_tail_embed(uint64_t* best, uint32_t* out_tok, const mh_quant_weights* e,
+                        const uint16_t* w, uint16_t* x, uint16_t* normed, float eps,
+                        mh_stream_t stream);
+
+/* src/kernels/lfm.rs:337-363 gather_rows_q6 (lfm.metal:430-462): out[t, :] =
+ * dequantized row ids[t] of the Q6 table w (6-bit, group 64), t < m.  out
+ * 16-byte aligned; an id outside the table leaves its row unwritten. */
+int mh_gather_rows_q6(const mh_quant_weights* w, const uint32_t* ids, uint32_t m, uint16_t* out,
+                      mh_stream_t stream);
+
 /* src/kernels/lfm.rs:794 argmax_bf16: two-stage argmax of a bf16 row,
  * ties to the lowest index.  partials: scratch of >= 64*8 bytes. */
 int mh_argmax_bf16(const uint16_t* x, uint32_t n, void* partials, uint32_t* out,

@@ -472,6 +472,68 @@ uint32_t grid_for(uint32_t units, uint32_t cap) {
     return want < cap ? want : cap;
 }
 
+// Batch 1 with K > 2048 (the dense FFN down, K = 11776), no argmax: R rows
+// per workgroup, the row's chunks split across the workgroup's waves in
+// slabs of 64 (slab s: chunks 64 s + lane), so every wave holds little and
+// the whole matrix is in flight at once.  Each chunk value h_c goes to LDS;
+// then wave r sums row r's lane l values h_l, h_{l+64}, ... in ascending slab
+// order from +0 and takes the xor butterfly: the chunk order exactly.
+constexpr int kSplitRows = 4;
+constexpr int kSplitSlabs = 16;  // K <= 16 * 64 * 32 = 32768
+
+constexpr int kSplitWaves = 8;
+
+template <int BITS>
+__global__ __launch_bounds__(kSplitWaves * 64) void k_gemv_splitk(GemvArgs a) {
+    constexpr int R = kSplitRows;
+    __shared__ float hs[R][kSplitSlabs][mh::kWave];
+    const int lane = threadIdx.x & (mh::kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / mh::kWave);
+    const uint32_t N = a.n, C = a.k / 32u;
+    const uint32_t S = (C + mh::kWave - 1) / mh::kWave;
+    const uint32_t row0 = blockIdx.x * R;
+    for (uint32_t sl = wave; sl < S; sl += kSplitWaves) {
+        const uint32_t c = sl * mh::kWave + lane;
+        const bool live = c < C;
+        const uint32_t cc = live ? c : 0u;
+        mh::Chunk<BITS> ch[R];
+        float sc[R], bi[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t row = min(row0 + r, N - 1u);
+            load_row_chunk<BITS>(a, row, cc, ch[r], sc[r], bi[r]);
+        }
+        float xr[32], xs;
+        mh::load_x_chunk(a.x + 32u * cc, xr, xs);
+        if (BITS == 4) {
+            mh::q4_scale_x(xr);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float p = ch[r].dot(xr);
+            hs[r][sl][lane] = live ? __builtin_fmaf(sc[r], p, bi[r] * xs) : 0.0f;
+        }
+    }
+    __syncthreads();
+    if (wave < R && row0 + wave < N) {
+        float v = 0.0f;
+        for (uint32_t sl = 0; sl < S; ++sl) {
+            v = v + hs[wave][sl][lane];
+        }
+        v = mh::lane63(mh::wave_sum_lane63(v));
+        if (lane == 0) {
+            a.y[row0 + wave] = mh::f32_to_bf16(v);
+        }
+    }
+}
+
+template <int BITS>
+int launch_splitk(const GemvArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL(k_gemv_splitk<BITS>, dim3((a.n + kSplitRows - 1) / kSplitRows), dim3(kSplitWaves * 64), 0,
+                       stream, a);
+    return mh::launch_status("k_gemv_splitk");
+}
+
 template <int BITS, int B, int R>
 int launch_staged(const GemvArgs& a, hipStream_t stream) {
     const size_t lds = static_cast<size_t>(B) * (a.k / 32u) * (kXPitch + 1) * sizeof(float);
@@ -500,6 +562,10 @@ int dispatch_gemv(const GemvArgs& a, uint32_t batch, hipStream_t stream) {
             if (a.k <= 2048u && a.groups <= static_cast<uint32_t>(kMaxGroups) && (a.groups & 1u) == 0u) {
                 return (a.best != nullptr || a.slots != nullptr) ? launch_rows<BITS, true>(a, stream)
                                                                  : launch_rows<BITS, false>(a, stream);
+            }
+            if (a.best == nullptr && a.slots == nullptr && a.y != nullptr &&
+                a.k <= 32u * mh::kWave * kSplitSlabs) {
+                return launch_splitk<BITS>(a, stream);
             }
             return launch_staged<BITS, 1, 4>(a, stream);
         case 2: return launch_staged<BITS, 2, 2>(a, stream);
@@ -580,23 +646,7 @@ __global__ __launch_bounds__(256) void k_dequant(const uint32_t* codes, const ui
         const float s = mh::bf16_to_f32(scales[static_cast<size_t>(row) * groups + g]);
         const float b = mh::bf16_to_f32(biases[static_cast<size_t>(row) * groups + g]);
         uint32_t packed[16];
-#pragma unroll
-        for (int i = 0; i < 32; i += 2) {
-            uint32_t q0, q1;
-            if constexpr (BITS == 4) {
-                q0 = (ch.w[i >> 3] >> (4 * (i & 7))) & 15u;
-                q1 = (ch.w[(i + 1) >> 3] >> (4 * ((i + 1) & 7))) & 15u;
-            } else {
-                const int b0 = 6 * i, b1 = 6 * (i + 1);
-                q0 = ((b0 & 31) + 6 <= 32) ? (ch.w[b0 >> 5] >> (b0 & 31)) & 63u
-                                           : __builtin_amdgcn_alignbit(ch.w[(b0 >> 5) + 1], ch.w[b0 >> 5], b0 & 31) & 63u;
-                q1 = ((b1 & 31) + 6 <= 32) ? (ch.w[b1 >> 5] >> (b1 & 31)) & 63u
-                                           : __builtin_amdgcn_alignbit(ch.w[(b1 >> 5) + 1], ch.w[b1 >> 5], b1 & 31) & 63u;
-            }
-            const uint16_t lo = mh::f32_to_bf16(__builtin_fmaf(s, static_cast<float>(q0), b));
-            const uint16_t hi = mh::f32_to_bf16(__builtin_fmaf(s, static_cast<float>(q1), b));
-            packed[i >> 1] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
-        }
+        mh::dequant_chunk<BITS>(ch.w, s, b, packed);
         uint4* dst = reinterpret_cast<uint4*>(out + static_cast<size_t>(row) * k + 32u * c);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {

@@ -459,6 +459,29 @@ struct Chunk<6> {
     __device__ __forceinline__ float dot(const float* xr) const { return q6_chunk_dot(w, xr); }
 };
 
+// A chunk's 32 codes dequantized to bf16 as bf16(fma(s, q, b)) (MLX
+// dequantize, quant_nax.metal:2908-2993), packed two per word in code order.
+template <int BITS>
+__device__ __forceinline__ void dequant_chunk(const uint32_t* w, float s, float b, uint32_t (&packed)[16]) {
+#pragma unroll
+    for (int i = 0; i < 32; i += 2) {
+        uint32_t q0, q1;
+        if constexpr (BITS == 4) {
+            q0 = (w[i >> 3] >> (4 * (i & 7))) & 15u;
+            q1 = (w[(i + 1) >> 3] >> (4 * ((i + 1) & 7))) & 15u;
+        } else {
+            const int b0 = 6 * i, b1 = 6 * (i + 1);
+            q0 = ((b0 & 31) + 6 <= 32) ? (w[b0 >> 5] >> (b0 & 31)) & 63u
+                                       : __builtin_amdgcn_alignbit(w[(b0 >> 5) + 1], w[b0 >> 5], b0 & 31) & 63u;
+            q1 = ((b1 & 31) + 6 <= 32) ? (w[b1 >> 5] >> (b1 & 31)) & 63u
+                                       : __builtin_amdgcn_alignbit(w[(b1 >> 5) + 1], w[b1 >> 5], b1 & 31) & 63u;
+        }
+        const uint16_t lo = f32_to_bf16(__builtin_fmaf(s, static_cast<float>(q0), b));
+        const uint16_t hi = f32_to_bf16(__builtin_fmaf(s, static_cast<float>(q1), b));
+        packed[i >> 1] = static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+    }
+}
+
 // One lane's 32-element chunk of a router row (bf16 or f32 weights), held
 // as raw words until converted.
 template <typename WT>

@@ -84,6 +84,8 @@ _SIGNATURES = {
     "mh_proj3_gemv_scatter": [_qw, _qw, _qw, _vp, _vp, _vp, _vp, _u32, _u32, _vp],
     "mh_conv3_gemv": [_qw, _vp, _vp, _vp, _vp, _vp, _vp],
     "mh_token_tail": [_vp, _vp, _u32, _vp],
+    "mh_token_tail_embed": [_vp, _vp, _qw, _vp, _vp, _vp, _f32, _vp],
+    "mh_gather_rows_q6": [_qw, _vp, _u32, _vp, _vp],
     "mh_argmax_bf16": [_vp, _u32, _vp, _vp, _vp],
     "mh_gemv_f32": [_vp, _vp, _vp, _u32, _u32, _vp],
     "mh_gemv_bf16": [_vp, _vp, _vp, _u32, _u32, _vp],
@@ -304,6 +306,19 @@ def conv3_gemv(wproj: QuantWeights, x, taps, state, out, new_state, stream=None)
     """src/kernels/lfm.rs:220 (the decode short conv with its input projection)."""
     check(load().mh_conv3_gemv(_qref(wproj), _ptr(x), _ptr(taps), _ptr(state), _ptr(out),
                                _ptr(new_state), _stream(stream)), "conv3_gemv")
+
+
+def token_tail_embed(best, out_tok, table: QuantWeights, w, x, normed, eps: float,
+                     stream=None) -> None:
+    """src/kernels/lfm.rs:850 token_tail with `next` (the token's embedding row + RMSNorm)."""
+    check(load().mh_token_tail_embed(_ptr(best), _ptr(out_tok), _qref(table), _ptr(w), _ptr(x),
+                                     _ptr(normed), eps, _stream(stream)), "token_tail_embed")
+
+
+def gather_rows_q6(table: QuantWeights, ids, m: int, out, stream=None) -> None:
+    """src/kernels/lfm.rs:337 (dequantizing embedding gather)."""
+    check(load().mh_gather_rows_q6(_qref(table), _ptr(ids), m, _ptr(out), _stream(stream)),
+          "gather_rows_q6")
 
 
 def gemv_gather_act(gate: QuantWeights, up: QuantWeights, x, ids, act, topk: int, n_inter: int,

@@ -105,6 +105,17 @@ void orc_proj3(const orc_qw* q, const orc_qw* k, const orc_qw* v, const uint16_t
 void orc_conv3(const orc_qw* w, const uint16_t* x, const uint16_t* taps, const uint16_t* state,
                uint16_t* out, uint16_t* new_state);
 
+/* ---- next row: token tail + Q6 embedding (lfm.metal:430-462, :1284-1386;
+ * src/kernels/lfm.rs:337-363, :850-888) --------------------------------------
+ * token = ~low32(key), key cleared; x = the token's table row dequantized
+ * (bf16(fma(s, q, b)), = orc_dequant_bf16's row); normed = bf16((x * inv) *
+ * w), inv = 1 / sqrt(sum x^2 / K + eps) summed in the reference's thread
+ * order.  The embedding gather is orc_dequant_bf16's rows.  Pinned: the row
+ * against orc_dequant_bf16, normed against float64 RMSNorm (tolerance) and a
+ * constant row's closed form. */
+void orc_token_tail_embed(uint64_t* best, uint32_t* out_tok, const orc_qw* e, const uint16_t* w,
+                          uint16_t* x, uint16_t* normed, float eps);
+
 /* ---- a6: argmax over bf16 logits (lfm.metal:1113-1282) ------------------
  * value desc, index asc; -0 == +0; NaN never taken; none -> 0.  Pinned by
  * known-answer ties and numpy argmax on tie-free rows. */

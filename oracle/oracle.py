@@ -149,6 +149,19 @@ def conv3(h, x: np.ndarray, taps: np.ndarray, state: np.ndarray):
     return out, new_state
 
 
+def token_tail_embed(key: int, h, w: np.ndarray, eps: float):
+    """(token, x row, normed row, key after) of the decode token tail with the Q6 table h."""
+    w = np.ascontiguousarray(w, np.uint16)
+    best = np.array([key], np.uint64)
+    tok = np.zeros(1, np.uint32)
+    x = np.empty(h.k, np.uint16)
+    normed = np.empty(h.k, np.uint16)
+    e = qw(h)
+    lib().orc_token_tail_embed(_p(best), _p(tok), ctypes.byref(e), _p(w), _p(x), _p(normed),
+                               ctypes.c_float(eps))
+    return int(tok[0]), x, normed, int(best[0])
+
+
 def gemv_quant_rows(h, x: np.ndarray, rows: np.ndarray, batch: int = 1) -> np.ndarray:
     x = np.ascontiguousarray(x, np.uint16)
     rows = np.ascontiguousarray(rows, np.uint32)

@@ -300,6 +300,41 @@ void orc_conv3(const orc_qw* w, const uint16_t* x, const uint16_t* taps, const u
     free(xf);
 }
 
+/* lfm.metal:1284-1386 lfm_token_tail with `embed`: the key's token (the key
+ * cleared), the token's row of the Q6 table dequantized as bf16(fma(s, q,
+ * b)) into x, and its RMSNorm into normed: thread t of 256 sums v^2 (fma) of
+ * elements t + 256 j in order, the threads' sums are added in thread order
+ * (the reference's simd_sum then the 8 partials), inv = 1 / sqrt(total / K +
+ * eps), normed = bf16((v * inv) * w).  K a multiple of 256; tok < rows. */
+void orc_token_tail_embed(uint64_t* best, uint32_t* out_tok, const orc_qw* e, const uint16_t* w,
+                          uint16_t* x, uint16_t* normed, float eps) {
+    const uint32_t tok = ~(uint32_t)(*best & 0xffffffffull);
+    *best = 0;
+    *out_tok = tok;
+    const uint32_t K = e->k, groups = K / e->gs;
+    uint8_t* q = (uint8_t*)malloc(K);
+    orc_unpack(e->codes + (size_t)tok * (K * e->bits / 32), e->bits, K, q);
+    for (uint32_t j = 0; j < K; ++j) {
+        const float sc = orc_bf16_to_f32(e->scales[(size_t)tok * groups + j / e->gs]);
+        const float bi = orc_bf16_to_f32(e->biases[(size_t)tok * groups + j / e->gs]);
+        x[j] = orc_f32_to_bf16(fmaf(sc, (float)q[j], bi));
+    }
+    float total = 0.0f;
+    for (uint32_t t = 0; t < 256; ++t) {
+        float acc = 0.0f;
+        for (uint32_t j = 0; j < K / 256; ++j) {
+            const float v = orc_bf16_to_f32(x[t + 256 * j]);
+            acc = fmaf(v, v, acc);
+        }
+        total += acc;
+    }
+    const float inv = 1.0f / sqrtf(total / (float)K + eps);
+    for (uint32_t j = 0; j < K; ++j) {
+        normed[j] = orc_f32_to_bf16((orc_bf16_to_f32(x[j]) * inv) * orc_bf16_to_f32(w[j]));
+    }
+    free(q);
+}
+
 /* ------------------------------------------------------------- argmax --- */
 
 uint32_t orc_argmax_bf16(const uint16_t* x, size_t n) {

@@ -105,3 +105,22 @@ def test_proj3_and_conv3_arguments():
         hip.conv3_gemv(_qw(out_features=48, in_features=4096), 0x4000, 0x5000, 0x6000, 0x7000,
                        0x8000, stream=0)
     assert ei.value.code == hip.MH_ERR_UNSUPPORTED
+
+
+def test_embedding_arguments():
+    with pytest.raises(hip.MoltenError) as ei:  # the table is 6-bit
+        hip.gather_rows_q6(_qw(), 0x4000, 4, 0x5000, stream=0)
+    assert ei.value.code == hip.MH_ERR_UNSUPPORTED
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.gather_rows_q6(_qw(bits=6), 0x4000, 4, 0x5008, stream=0)
+    assert ei.value.code == hip.MH_ERR_ALIGN
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.gather_rows_q6(_qw(bits=6), 0x4000, 0, 0x5000, stream=0)
+    assert ei.value.code == hip.MH_ERR_INVALID
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.token_tail_embed(0x6000, 0x7000, _qw(bits=6, in_features=4096), 0x4000, 0x5000, 0x8000,
+                             1e-5, stream=0)
+    assert ei.value.code == hip.MH_ERR_UNSUPPORTED
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.token_tail_embed(0x6000, 0x7000, _qw(bits=6), 0x4008, 0x5000, 0x8000, 1e-5, stream=0)
+    assert ei.value.code == hip.MH_ERR_ALIGN

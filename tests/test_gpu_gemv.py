@@ -51,7 +51,9 @@ def assert_logits(got, want, n, k, batch, gs=64):
     (1536, 2048, 1),   # expert gate/up shape
     (2048, 1536, 1),   # expert down shape (48 live lanes)
     (300, 2048, 1),    # ragged last row group
-    (96, 11776, 1),    # dense down shape: staged-x path
+    (96, 11776, 1),    # dense down width: split-K path
+    (2048, 11776, 1),  # the dense FFN down projection
+    (37, 4160, 1),     # split-K: ragged rows, 130 chunks (a partial slab)
     (512, 2048, 2),
     (512, 2048, 8),    # config 5 batch
     (130, 1536, 5),

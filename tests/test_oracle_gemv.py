@@ -188,3 +188,39 @@ def test_conv3_taps_sum_in_order(orc, rng):
     v2 = _bf16_round(rows[:H] * rows[2 * H:])
     z = (t[:, 0] * s[0] + t[:, 1] * s[1]).astype(np.float32) + (t[:, 2] * v2).astype(np.float32)
     np.testing.assert_array_equal(layout.bf16_to_f32(out), _bf16_round(rows[H:2 * H] * _bf16_round(z)))
+
+
+# ---- token tail + Q6 embedding (lfm.metal:430-462, :1284-1386) ------------
+
+def test_token_tail_embed_row_and_norm(orc, rng):
+    """Pins orc_token_tail_embed: the token is the key's, the key is cleared,
+    the row equals the dequant oracle's row, and the norm is within bf16
+    rounding of float64 RMSNorm."""
+    n, k, eps = 300, 2048, 1e-5
+    h = layout.synth_quant(rng, n, k, 6)
+    w = layout.synth_bf16(rng, (k,), std=0.3)
+    tok = 217
+    key = (0x9abc1234 << 32) | (~tok & 0xffffffff)
+    got_tok, x, normed, after = orc.token_tail_embed(key, h, w, eps)
+    assert got_tok == tok and after == 0
+    np.testing.assert_array_equal(x, orc.dequant_bf16(h)[tok])
+    xv = bf(x).astype(np.float64)
+    ref = xv / np.sqrt(np.mean(xv * xv) + eps) * bf(w).astype(np.float64)
+    got = bf(normed).astype(np.float64)
+    assert np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)) <= 2.0 ** -7
+
+
+def test_token_tail_embed_constant_row(orc):
+    """A row of one value c: normed = bf16(c / sqrt(c^2 + eps) * w) (closed form)."""
+    k, eps = 512, 1e-6
+    q = np.full((1, k), 5, np.uint8)
+    h = layout.HostQuant(codes=orc.pack(q.ravel(), 6).reshape(1, -1),
+                         scales=layout.f32_to_bf16(np.full((1, k // 64), 0.25, np.float32)),
+                         biases=layout.f32_to_bf16(np.full((1, k // 64), -2.0, np.float32)),
+                         n=1, k=k, group_size=64, bits=6)
+    w = layout.f32_to_bf16(np.linspace(-1, 1, k).astype(np.float32))
+    _, x, normed, _ = orc.token_tail_embed(~0 & 0xffffffff, h, w, eps)  # token 0
+    c = np.float32(0.25 * 5 - 2.0)
+    assert (bf(x) == c).all()
+    inv = np.float32(1.0) / np.sqrt(np.float32(c * c) + np.float32(eps), dtype=np.float32)
+    np.testing.assert_array_equal(bf(normed), bf(layout.f32_to_bf16((c * inv) * bf(w))))
