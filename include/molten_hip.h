@@ -311,6 +311,14 @@ int mh_gemm_q4_grouped(const uint16_t* a, const mh_quant_weights* w, uint16_t* c
                        const uint32_t* blocks, uint32_t n_blocks, uint32_t s_rows, uint32_t n,
                        uint32_t bm, uint32_t bn, mh_stream_t stream);
 
+/* src/lfm.rs:661-671 project (prefill): dequant_q4_bf16_bulk + gemm_bf16_nt
+ * fused: C[m, :] = A[m, :] . dequant(W)^T for every row m < M, A bf16 [M, K]
+ * (16-byte aligned), W 4-bit group 64 [N, K], C bf16 [M, N]; the grouped
+ * GEMM's kernel (bf16 dequant, f32 MFMA accumulation) over a dense tiling
+ * (128 x 256 tiles, 128 x 64 when N % 256 != 0).  N a multiple of 64. */
+int mh_gemm_q4_dense(const uint16_t* a, uint32_t m, const mh_quant_weights* w, uint16_t* c,
+                     mh_stream_t stream);
+
 /* src/kernels/quant.rs:151 gemm_q4_grouped_mlx_gu: gate and up over the
  * same map and A, stored separately.  Tiles 32x64, 128x64, 128x128. */
 int mh_gemm_q4_grouped_gu(const uint16_t* a, const mh_quant_weights* gate,

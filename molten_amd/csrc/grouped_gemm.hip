@@ -43,7 +43,7 @@ struct GemmArgs {
     const uint32_t* c1; const uint16_t* s1; const uint16_t* b1;  // up
     uint16_t* out0;          // [s_rows, n]: C, gate, or act
     uint16_t* out1;          // [s_rows, n]: up (EPI_GATE_UP)
-    const uint4* blocks;
+    const uint4* blocks;     // block map; null: a dense product (k_grouped only)
     uint32_t k, n, s_rows, a_rows, w_rows;
 };
 
@@ -185,7 +185,14 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void k_grouped(GemmArgs a
     if (ent >= n_entries) {
         return;
     }
-    const uint4 blk = a.blocks[ent];
+    uint4 blk;
+    if (a.blocks == nullptr) {  // dense: one matrix, entry = (row tile, column tile)
+        const uint32_t nt = a.n / (NW * NBW * 32u);
+        const uint32_t mr = (ent / nt) * BM, nc = (ent % nt) * (NW * NBW * 32u);
+        blk = make_uint4(mr, nc, nc, min(mr + BM, a.s_rows));
+    } else {
+        blk = a.blocks[ent];
+    }
     const uint32_t m0 = blk.x, brow = blk.y, n0 = blk.z, m_end = blk.w;
     if (m0 >= m_end) {
         return;
@@ -980,6 +987,27 @@ int mh_gemm_q4_grouped(const uint16_t* a, const mh_quant_weights* w, uint16_t* c
     MH_TRY(gemm_checks("mh_gemm_q4_grouped", a, w, c, blocks, n_blocks, s_rows, n));
     const GemmArgs g = make_args(a, nullptr, s_rows, w, nullptr, c, nullptr, blocks, s_rows, n);
     return dispatch<false, EPI_STORE>(g, n_blocks, bm, bn, mh::as_stream(stream));
+}
+
+int mh_gemm_q4_dense(const uint16_t* a, uint32_t m, const mh_quant_weights* w, uint16_t* c,
+                     mh_stream_t stream) {
+    const char* op = "mh_gemm_q4_dense";
+    MH_TRY(mh::check_quant(w, op));
+    MH_ENSURE(a && c, MH_ERR_INVALID, "%s: NULL argument", op);
+    MH_ENSURE(w->bits == 4 && w->group_size == 64 && w->in_features % 64 == 0, MH_ERR_UNSUPPORTED,
+              "%s: needs 4-bit group-64 weights and K %% 64 == 0", op);
+    MH_ENSURE(m > 0, MH_ERR_INVALID, "%s: no rows", op);
+    MH_ENSURE(w->out_features % 64 == 0, MH_ERR_UNSUPPORTED, "%s: N %u not a multiple of 64", op,
+              w->out_features);
+    MH_ENSURE(mh::aligned(a, 16) && mh::aligned(c, 4), MH_ERR_ALIGN, "%s: A 16-byte, C 4-byte alignment", op);
+    const uint32_t n = w->out_features;
+    GemmArgs g = make_args(a, nullptr, m, w, nullptr, c, nullptr, nullptr, m, n);
+    const hipStream_t s = mh::as_stream(stream);
+    const uint32_t mt = (m + 127u) / 128u;
+    if (n % 256 == 0) {
+        return launch_t<128, 2, 4, false, EPI_STORE>(g, mt * (n / 256u), s);
+    }
+    return launch_t<128, 2, 1, false, EPI_STORE>(g, mt * (n / 64u), s);
 }
 
 int mh_gemm_q4_grouped_gu(const uint16_t* a, const mh_quant_weights* gate,

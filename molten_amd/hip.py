@@ -84,6 +84,7 @@ _SIGNATURES = {
     "mh_proj3_gemv_scatter": [_qw, _qw, _qw, _vp, _vp, _vp, _vp, _u32, _u32, _vp],
     "mh_conv3_gemv": [_qw, _vp, _vp, _vp, _vp, _vp, _vp],
     "mh_token_tail": [_vp, _vp, _u32, _vp],
+    "mh_gemm_q4_dense": [_vp, _u32, _qw, _vp, _vp],
     "mh_token_tail_embed": [_vp, _vp, _qw, _vp, _vp, _vp, _f32, _vp],
     "mh_gather_rows_q6": [_qw, _vp, _u32, _vp, _vp],
     "mh_argmax_bf16": [_vp, _u32, _vp, _vp, _vp],
@@ -319,6 +320,11 @@ def gather_rows_q6(table: QuantWeights, ids, m: int, out, stream=None) -> None:
     """src/kernels/lfm.rs:337 (dequantizing embedding gather)."""
     check(load().mh_gather_rows_q6(_qref(table), _ptr(ids), m, _ptr(out), _stream(stream)),
           "gather_rows_q6")
+
+
+def gemm_q4_dense(a, m: int, w: QuantWeights, c, stream=None) -> None:
+    """src/lfm.rs:661 (prefill dense projection: dequant + bf16 GEMM, fused)."""
+    check(load().mh_gemm_q4_dense(_ptr(a), m, _qref(w), _ptr(c), _stream(stream)), "gemm_q4_dense")
 
 
 def gemv_gather_act(gate: QuantWeights, up: QuantWeights, x, ids, act, topk: int, n_inter: int,

@@ -124,3 +124,15 @@ def test_embedding_arguments():
     with pytest.raises(hip.MoltenError) as ei:
         hip.token_tail_embed(0x6000, 0x7000, _qw(bits=6), 0x4008, 0x5000, 0x8000, 1e-5, stream=0)
     assert ei.value.code == hip.MH_ERR_ALIGN
+
+
+def test_dense_gemm_arguments():
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.gemm_q4_dense(0x4000, 16, _qw(bits=6), 0x5000, stream=0)
+    assert ei.value.code == hip.MH_ERR_UNSUPPORTED
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.gemm_q4_dense(0x4008, 16, _qw(), 0x5000, stream=0)
+    assert ei.value.code == hip.MH_ERR_ALIGN
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.gemm_q4_dense(0x4000, 0, _qw(), 0x5000, stream=0)
+    assert ei.value.code == hip.MH_ERR_INVALID

@@ -246,3 +246,37 @@ def test_moe_prefill_config4_full_size(dev, orc):
         np.testing.assert_array_equal(got[key], want[key], err_msg=key)
     sel = mask == 1
     assert_close(got["out"][sel], want["out"][sel], "prefill out config 4 (sampled tokens)")
+
+
+def _dense_map(m, n, bm=128, bn=64):
+    """Block map of a dense product (one matrix): (m0, n0, n0, m_end) per tile."""
+    ents = [(m0, n0, n0, min(m0 + bm, m)) for m0 in range(0, m, bm) for n0 in range(0, n, bn)]
+    return np.array(ents, np.uint32).reshape(-1, 4), len(ents)
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 2048, 2048), (64, 576, 1024), (4096, 512, 2048)])
+def test_dense_gemm_vs_oracle(dev, orc, m, n, k):
+    """The prefill dense projection (dequant + bf16 GEMM fused) against the
+    oracle's grouped GEMM over a dense map."""
+    rng = np.random.default_rng(m + n)
+    w = layout.synth_quant(rng, n, k, 4)
+    a = layout.synth_bf16(rng, (m, k))
+    wd, keep = dev_quant(w)
+    c = zeros_dev((m, n), np.uint16)
+    hip.gemm_q4_dense(to_dev(a), m, wd, c)
+    blocks, nb = _dense_map(m, n)
+    assert_close(from_dev(c, np.uint16), orc.gemm_q4_grouped(a, w, blocks, nb, n, 64), f"dense {m}x{n}x{k}")
+
+
+def test_dense_gemm_one_hot_is_exact_dequant(dev, orc):
+    """Rows of A that are one-hot (x = 1 at column j) give dequantized column j exactly."""
+    rng = np.random.default_rng(3)
+    m, n, k = 200, 512, 1024
+    w = layout.synth_quant(rng, n, k, 4)
+    cols = rng.integers(0, k, m)
+    a = np.zeros((m, k), np.uint16)
+    a[np.arange(m), cols] = layout.f32_to_bf16(np.float32(1.0))
+    wd, keep = dev_quant(w)
+    c = zeros_dev((m, n), np.uint16)
+    hip.gemm_q4_dense(to_dev(a), m, wd, c)
+    np.testing.assert_array_equal(from_dev(c, np.uint16), orc.dequant_bf16(w)[:, cols].T)
