@@ -191,11 +191,15 @@ def bench_next_rows(torch, hip, dev, gen, steps, warmup):
 
     ms_t = timed(torch, tail, steps, warmup)
     del tab
-    # the prefill dense projection (dequant + GEMM fused): 4096 tokens x 2048 -> 2048
-    pw = make_quant(torch, 2048, 2048, 4, 4, dev, gen)
+    # the prefill dense projections (dequant + GEMM fused), 4096 tokens: an
+    # attention projection 2048 -> 2048 and the dense FFN gate 2048 -> 11776
+    ms_x = []
     pa = bf16_randn(torch, (4096, 2048), dev, gen)
-    pc = torch.empty((4096, 2048), dtype=torch.int16, device=dev)
-    ms_x = timed(torch, lambda i: hip.gemm_q4_dense(pa, 4096, pw[i % 4][0], pc), steps, warmup)
+    for n in (2048, 11776):
+        pw = make_quant(torch, n, 2048, 4, 4, dev, gen)
+        pc = torch.empty((4096, n), dtype=torch.int16, device=dev)
+        ms_x.append(timed(torch, lambda i: hip.gemm_q4_dense(pa, 4096, pw[i % 4][0], pc), steps, warmup))
+        del pw, pc
     return ms_p, ms_c, ms_d, ms_g, ms_t, ms_x
 
 
@@ -352,10 +356,11 @@ def main() -> int:
             ms_per_step=round(ms1, 5), frac_of_hbm_peak=round(BYTES["config1"] / (ms1 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
         log("next rows: proj3, conv3, dense down K=11776, Q6 gather, token tail, dense prefill")
         ms_p, ms_c, ms_d, ms_g, ms_t, ms_x = bench_next_rows(torch, hip, dev, gen, steps, warmup)
-        tf = 2.0 * 4096 * 2048 * 2048 / (ms_x * 1e-3) / 1e12
-        others["next_dense_prefill_q4_4096x2048x2048"] = dict(
-            value=round(tf, 1), unit="TFLOP/s", ms_per_step=round(ms_x, 5),
-            frac_of_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4))
+        for n, ms in zip((2048, 11776), ms_x):
+            tf = 2.0 * 4096 * n * 2048 / (ms * 1e-3) / 1e12
+            others[f"next_dense_prefill_q4_4096x{n}x2048"] = dict(
+                value=round(tf, 1), unit="TFLOP/s", ms_per_step=round(ms, 5),
+                frac_of_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4))
         for key, ms in (("next_proj3_gemv_scatter", ms_p), ("next_conv3_gemv", ms_c),
                         ("next_dense_down_q4_k11776", ms_d), ("next_gather_rows_q6_4096", ms_g),
                         ("next_token_tail_embed", ms_t)):

@@ -43,8 +43,9 @@ struct GemmArgs {
     const uint32_t* c1; const uint16_t* s1; const uint16_t* b1;  // up
     uint16_t* out0;          // [s_rows, n]: C, gate, or act
     uint16_t* out1;          // [s_rows, n]: up (EPI_GATE_UP)
-    const uint4* blocks;     // block map; null: a dense product (k_grouped only)
+    const uint4* blocks;     // block map; null: a dense product (entries computed)
     uint32_t k, n, s_rows, a_rows, w_rows;
+    uint32_t dense_bm;       // rows per entry of a dense product (k_seg)
 };
 
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
@@ -804,16 +805,21 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
 // workgroup computes the same ranking (a few hundred instructions; the
 // group weights go through the LDS, which is free before the pass starts).
 // Returns n_entries for padding workgroups.
-__device__ uint32_t balanced_entry(const uint4* blocks, uint32_t n_entries, uint32_t nt, char* lds,
+__device__ uint32_t balanced_entry(const GemmArgs& a, uint32_t n_entries, uint32_t nt, char* lds,
                                    int lane, int wave) {
+    const uint4* blocks = a.blocks;
     uint32_t* wts = reinterpret_cast<uint32_t*>(lds);  // [C] group weights
     __shared__ uint32_t s_group;
     const uint32_t C = (n_entries + nt - 1u) / nt;
     const uint32_t x = blockIdx.x % 8u, j = blockIdx.x / 8u, slot = j / nt;
     const uint32_t k_target = slot * 8u + ((slot & 1u) ? 7u - x : x);
     for (uint32_t c = threadIdx.x; c < C; c += blockDim.x) {
-        const uint4 e = blocks[c * nt];
-        wts[c] = e.x < e.w ? e.w - e.x : 0u;
+        if (blocks == nullptr) {  // dense: row segments of dense_bm, the last partial
+            wts[c] = min(a.dense_bm, a.s_rows - c * a.dense_bm);
+        } else {
+            const uint4 e = blocks[c * nt];
+            wts[c] = e.x < e.w ? e.w - e.x : 0u;
+        }
     }
     if (threadIdx.x == 0) {
         s_group = 0xffffffffu;
@@ -846,11 +852,18 @@ void k_seg(GemmArgs a, uint32_t n_entries) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lds0 = static_cast<uint32_t>((uintptr_t)((lds_ptr)lds));
-    const uint32_t ent = balanced_entry(a.blocks, n_entries, a.n / (kSegWaves * NBW * 32u), lds, lane, wave);
+    const uint32_t nt = a.n / (kSegWaves * NBW * 32u);
+    const uint32_t ent = balanced_entry(a, n_entries, nt, lds, lane, wave);
     if (ent >= n_entries) {
         return;
     }
-    const uint4 blk = a.blocks[ent];
+    uint4 blk;
+    if (a.blocks == nullptr) {  // dense: entry = (row segment, column tile)
+        const uint32_t mr = (ent / nt) * a.dense_bm, nc = (ent % nt) * (kSegWaves * NBW * 32u);
+        blk = make_uint4(mr, nc, nc, min(mr + a.dense_bm, a.s_rows));
+    } else {
+        blk = a.blocks[ent];
+    }
     const uint32_t m0 = blk.x, brow = blk.y, n0 = blk.z, m_end = blk.w;
     if (m0 >= m_end) {
         return;
@@ -1003,6 +1016,16 @@ int mh_gemm_q4_dense(const uint16_t* a, uint32_t m, const mh_quant_weights* w, u
     const uint32_t n = w->out_features;
     GemmArgs g = make_args(a, nullptr, m, w, nullptr, c, nullptr, nullptr, m, n);
     const hipStream_t s = mh::as_stream(stream);
+    // 256 x 256 segment entries when they fill the chip (>= one per CU) and
+    // the segment kernel's 32-bit offsets hold; else 128 x 256 tiles
+    const uint32_t segs = (m + 255u) / 256u * (n / 256u);
+    if (n % 256 == 0 && segs >= 256u && w->in_features % 512u == 0 &&
+        static_cast<uint64_t>(m) * w->in_features * 2u < (1ull << 32) &&
+        static_cast<uint64_t>(n) * w->in_features / 2u < (1ull << 32) &&
+        static_cast<uint64_t>(m) * n * 2u < (1ull << 32) && mh::aligned(c, 16)) {
+        g.dense_bm = 256;
+        return launch_seg<kSegRBMax, kSegStages, 2, 1, false, EPI_STORE>(g, segs, s);
+    }
     const uint32_t mt = (m + 127u) / 128u;
     if (n % 256 == 0) {
         return launch_t<128, 2, 4, false, EPI_STORE>(g, mt * (n / 256u), s);

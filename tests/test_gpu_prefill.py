@@ -280,3 +280,29 @@ def test_dense_gemm_one_hot_is_exact_dequant(dev, orc):
     c = zeros_dev((m, n), np.uint16)
     hip.gemm_q4_dense(to_dev(a), m, wd, c)
     np.testing.assert_array_equal(from_dev(c, np.uint16), orc.dequant_bf16(w)[:, cols].T)
+
+
+def test_dense_gemm_segment_path(dev, orc):
+    """A shape with >= 256 segment entries of 256 x 256 (the segment kernel in
+    dense mode): one-hot rows reproduce the dequantized columns exactly over
+    every tile, and the first and the last (partial) row segments match the
+    oracle within tolerance."""
+    rng = np.random.default_rng(11)
+    m, n, k = 1100, 13312, 512  # 5 row segments (the last 76 rows) x 52 column tiles
+    w = layout.synth_quant(rng, n, k, 4)
+    wd, keep = dev_quant(w)
+    cols = rng.integers(0, k, m)
+    a1 = np.zeros((m, k), np.uint16)
+    a1[np.arange(m), cols] = layout.f32_to_bf16(np.float32(1.0))
+    c = zeros_dev((m, n), np.uint16)
+    hip.gemm_q4_dense(to_dev(a1), m, wd, c)
+    deq = orc.dequant_bf16(w)
+    np.testing.assert_array_equal(from_dev(c, np.uint16), deq[:, cols].T)
+    a = layout.synth_bf16(rng, (m, k))
+    hip.gemm_q4_dense(to_dev(a), m, wd, c)
+    got = from_dev(c, np.uint16)
+    ents = [(m0, n0, n0, min(m0 + 128, m)) for m0 in (0, 128, 1024) for n0 in range(0, n, 64)]
+    blocks = np.array(ents, np.uint32).reshape(-1, 4)
+    want = orc.gemm_q4_grouped(a, w, blocks, len(ents), n, 64)
+    rows = np.r_[0:256, 1024:m]
+    assert_close(got[rows], want[rows], "dense segment path")
