@@ -59,7 +59,7 @@ const char* mh_version(void);
 enum { MH_ROUTE_SIGMOID_BIAS = 0, MH_ROUTE_SOFTMAX = 1 };
 
 /* Element type of a dense router matrix. */
-enum { MH_DTYPE_F32 = 0, MH_DTYPE_BF16 = 1 };
+enum { MH_DTYPE_F32 = 0, MH_DTYPE_BF16 = 1, MH_DTYPE_U32 = 2, MH_DTYPE_OTHER = 3 };
 
 typedef void* mh_stream_t; /* hipStream_t */
 typedef void* mh_event_t;  /* hipEvent_t  */
@@ -97,6 +97,34 @@ int mh_memcpy(void* dst, const void* src, size_t bytes, int kind, mh_stream_t st
 /* Stream-ordered zero fill with a kernel (no hipMemsetAsync, so it is safe
  * inside graph capture). */
 int mh_zero(void* dst, size_t bytes, mh_stream_t stream);
+
+/* ------------------------------------------------------ checkpoint ---
+ * src/safetensors.rs:85-196 Checkpoint and src/lfm.rs:261-316 load_tensor /
+ * load_quant: the MLX safetensors checkpoint, unchanged.  open() reads the
+ * shard headers (model.safetensors.index.json's shards, else
+ * model.safetensors); tensors are listed by name (sorted); read() streams a
+ * tensor into device memory through two pinned staging buffers (file reads
+ * overlap the copies) and returns once it is there; load_quant() checks and
+ * reads base.weight (U32 codes), base.scales and base.biases (BF16), infers
+ * bits = 32 * cols / K (must equal `bits`) and fills `out` with the device
+ * pointers.  Errors: MH_ERR_INVALID with the reference's messages. */
+#define MH_MAX_DIMS 8
+typedef struct mh_checkpoint mh_checkpoint;
+typedef struct {
+    int dtype; /* MH_DTYPE_F32 / BF16 / U32, or MH_DTYPE_OTHER */
+    uint32_t ndim;
+    uint64_t shape[MH_MAX_DIMS];
+    uint64_t bytes;
+} mh_tensor_meta;
+int mh_checkpoint_open(const char* dir, mh_checkpoint** out);
+void mh_checkpoint_close(mh_checkpoint* ck);
+uint32_t mh_checkpoint_count(const mh_checkpoint* ck);
+const char* mh_checkpoint_name(const mh_checkpoint* ck, uint32_t i);
+int mh_checkpoint_meta(const mh_checkpoint* ck, const char* name, mh_tensor_meta* meta);
+int mh_checkpoint_read(mh_checkpoint* ck, const char* name, void* dst, size_t bytes, mh_stream_t stream);
+int mh_load_quant(mh_checkpoint* ck, const char* base, uint32_t rows, uint32_t k, uint32_t bits,
+                  uint32_t* codes, uint16_t* scales, uint16_t* biases, mh_quant_weights* out,
+                  mh_stream_t stream);
 
 /* ------------------------------------------------------ dequantize ---
  * src/kernels/quant.rs:69 dequant_to_bf16 and :95 dequant_q4_bf16_bulk:

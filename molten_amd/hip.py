@@ -35,6 +35,8 @@ ROUTE_SIGMOID_BIAS = 0
 ROUTE_SOFTMAX = 1
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+DTYPE_U32 = 2
+DTYPE_OTHER = 3
 MH_ERR_INVALID = -1
 MH_ERR_ALIGN = -2
 MH_ERR_UNSUPPORTED = -3
@@ -84,6 +86,13 @@ _SIGNATURES = {
     "mh_proj3_gemv_scatter": [_qw, _qw, _qw, _vp, _vp, _vp, _vp, _u32, _u32, _vp],
     "mh_conv3_gemv": [_qw, _vp, _vp, _vp, _vp, _vp, _vp],
     "mh_token_tail": [_vp, _vp, _u32, _vp],
+    "mh_checkpoint_open": [ctypes.c_char_p, ctypes.POINTER(_vp)],
+    "mh_checkpoint_close": [_vp],
+    "mh_checkpoint_count": [_vp],
+    "mh_checkpoint_name": [_vp, _u32],
+    "mh_checkpoint_meta": [_vp, ctypes.c_char_p, _vp],
+    "mh_checkpoint_read": [_vp, ctypes.c_char_p, _vp, _sz, _vp],
+    "mh_load_quant": [_vp, ctypes.c_char_p, _u32, _u32, _u32, _vp, _vp, _vp, _qw, _vp],
     "mh_gemm_q4_dense": [_vp, _u32, _qw, _vp, _vp],
     "mh_token_tail_embed": [_vp, _vp, _qw, _vp, _vp, _vp, _f32, _vp],
     "mh_gather_rows_q6": [_qw, _vp, _u32, _vp, _vp],
@@ -120,7 +129,8 @@ _SIGNATURES = {
                        _vp, _sz, _vp],
 }
 _RESTYPES = {"mh_last_error": ctypes.c_char_p, "mh_version": ctypes.c_char_p,
-             "mh_moe_prefill_workspace": ctypes.c_size_t}
+             "mh_moe_prefill_workspace": ctypes.c_size_t, "mh_checkpoint_close": None,
+             "mh_checkpoint_count": ctypes.c_uint32, "mh_checkpoint_name": ctypes.c_char_p}
 
 _lib: Optional[ctypes.CDLL] = None
 
@@ -138,7 +148,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     for name, argtypes in _SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
-        fn.restype = _RESTYPES.get(name, ctypes.c_int)
+        fn.restype = _RESTYPES[name] if name in _RESTYPES else ctypes.c_int
     _lib = lib
     return lib
 
@@ -325,6 +335,52 @@ def gather_rows_q6(table: QuantWeights, ids, m: int, out, stream=None) -> None:
 def gemm_q4_dense(a, m: int, w: QuantWeights, c, stream=None) -> None:
     """src/lfm.rs:661 (prefill dense projection: dequant + bf16 GEMM, fused)."""
     check(load().mh_gemm_q4_dense(_ptr(a), m, _qref(w), _ptr(c), _stream(stream)), "gemm_q4_dense")
+
+
+class TensorMeta(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int), ("ndim", ctypes.c_uint32), ("shape", ctypes.c_uint64 * 8),
+                ("bytes", ctypes.c_uint64)]
+
+
+class Checkpoint:
+    """src/safetensors.rs Checkpoint over the C ABI: names, metadata, staged reads to device memory."""
+
+    def __init__(self, directory: str):
+        h = _vp()
+        check(load().mh_checkpoint_open(os.fsencode(directory), ctypes.byref(h)), "checkpoint_open")
+        self._h = h
+
+    def close(self) -> None:
+        if self._h:
+            load().mh_checkpoint_close(self._h)
+            self._h = _vp()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def names(self) -> list[str]:
+        lib = load()
+        return [lib.mh_checkpoint_name(self._h, i).decode() for i in range(lib.mh_checkpoint_count(self._h))]
+
+    def meta(self, name: str):
+        """(dtype, shape, bytes) with dtype one of MH_DTYPE_*."""
+        m = TensorMeta()
+        check(load().mh_checkpoint_meta(self._h, name.encode(), ctypes.byref(m)), "checkpoint_meta")
+        return m.dtype, tuple(m.shape[i] for i in range(m.ndim)), m.bytes
+
+    def read(self, name: str, dst, nbytes: int, stream=None) -> None:
+        check(load().mh_checkpoint_read(self._h, name.encode(), _ptr(dst), nbytes, _stream(stream)),
+              "checkpoint_read")
+
+    def load_quant(self, base: str, rows: int, k: int, bits: int, codes, scales, biases,
+                   stream=None) -> "QuantWeights":
+        out = CQuantWeights()
+        check(load().mh_load_quant(self._h, base.encode(), rows, k, bits, _ptr(codes), _ptr(scales),
+                                   _ptr(biases), ctypes.byref(out), _stream(stream)), "load_quant")
+        return QuantWeights(codes, scales, biases, rows, k, 64, bits)
 
 
 def gemv_gather_act(gate: QuantWeights, up: QuantWeights, x, ids, act, topk: int, n_inter: int,
