@@ -30,7 +30,8 @@ constexpr int kThreads = kWaves * 64;
 constexpr uint32_t kGrid = 256;
 constexpr int kTileRows = 16;
 constexpr int kStageGroups = 8;  // groups of 64 codes per pipeline stage
-constexpr int kDepth = 4;        // stages whose loads are in flight (even: LDS regions alternate)
+constexpr int kDepth = 2;        // stages in the pipeline (even: LDS regions alternate); one ahead
+                                 // measured fastest: more loads in flight only queue behind each other
 constexpr uint32_t kMaxK = 2048;
 constexpr uint32_t kMaxG = kMaxK / 64;
 constexpr int kMaxB = 8;
