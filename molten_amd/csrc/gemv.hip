@@ -20,6 +20,11 @@ constexpr int kWaves = kThreads / mh::kWave;
 constexpr int kXPitch = 36;  // LDS floats per staged x chunk (32 + 4: no bank conflicts)
 constexpr uint32_t kArgSlots = MH_ARGMAX_SLOTS;
 constexpr uint32_t kSpinLimit = 1u << 24;  // bound of the collector's wait for one slot
+#ifndef MH_ROWS_GRID_CAP
+#define MH_ROWS_GRID_CAP MH_ARGMAX_SLOTS
+#endif
+constexpr uint32_t kRowsGridCap = MH_ROWS_GRID_CAP;  // batch-1 GEMV workgroups (<= the finisher's slots)
+static_assert(kRowsGridCap <= kArgSlots, "one finisher slot per workgroup");
 
 struct GemvArgs {
     const uint32_t* codes;
@@ -548,7 +553,7 @@ int launch_rows(const GemvArgs& a, hipStream_t stream) {
     // one block per wave while the finisher has a slot for every workgroup
     // (the hardware keeps as many workgroups resident as registers allow);
     // beyond that the waves loop over blocks
-    const uint32_t grid = grid_for((a.n + kBlockRows - 1) / kBlockRows, kArgSlots);
+    const uint32_t grid = grid_for((a.n + kBlockRows - 1) / kBlockRows, kRowsGridCap);
     if (a.k == 2048u && a.gs == 64u && a.n % kBlockRows == 0u) {
         return launch(k_gemv_rows<BITS, true, ARGMAX>, a, grid, 0, stream, "k_gemv_rows");
     }
