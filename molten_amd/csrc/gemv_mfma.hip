@@ -43,6 +43,9 @@ constexpr uint32_t kMaxCand = kTileRows * 68;  // finisher's candidate list (a w
 constexpr uint32_t kSpinLimit = 1u << 24;
 static_assert(kGrid * kSlotWords <= kArgSlots && kGrid % 64 == 0, "finisher slots");
 static_assert(kGrid * kCand <= kMaxCand, "candidate list");
+// a stage's scales / biases are read by all 64 lanes: row l / 4, groups
+// 2 (l % 4) and 2 (l % 4) + 1 -- exactly 16 rows x 8 groups
+static_assert(kStageGroups == 8 && kTileRows == 16, "scale / bias staging covers 16 rows x 8 groups");
 
 struct MfmaArgs {
     const char* codes;
