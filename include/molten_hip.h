@@ -107,7 +107,9 @@ int mh_zero(void* dst, size_t bytes, mh_stream_t stream);
  * overlap the copies) and returns once it is there; load_quant() checks and
  * reads base.weight (U32 codes), base.scales and base.biases (BF16), infers
  * bits = 32 * cols / K (must equal `bits`) and fills `out` with the device
- * pointers.  Errors: MH_ERR_INVALID with the reference's messages. */
+ * pointers.  Errors: MH_ERR_INVALID with the reference's messages.  Names
+ * stay valid until close(); reads on one checkpoint share its staging buffers,
+ * so concurrent calls on one checkpoint from several threads race. */
 #define MH_MAX_DIMS 8
 typedef struct mh_checkpoint mh_checkpoint;
 typedef struct {
