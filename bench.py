@@ -45,6 +45,7 @@ BYTES = {
     "next_conv3_gemv": 7_114_752,          # 6144 rows x 1152 B + x + taps + state in/out + out
     "next_dense_down_q4_k11776": 13_593_600,  # 2048 rows x (5888 code + 736 s/b) B + x + y
     "next_gather_rows_q6_4096": 23_609_344,   # 4096 x (1536 code + 128 s/b + 4096 out) B + ids
+    "next_sample_gumbel_128000": 272_008,  # 128000 bf16 logits + the seen bits + the key
     "next_token_tail_embed": 13_972,  # key read + clear, token, one Q6 row + s/b, gain, x and normed rows
 }
 FLOPS_CONFIG4 = 309_237_645_312
@@ -191,6 +192,13 @@ def bench_next_rows(torch, hip, dev, gen, steps, warmup):
 
     ms_t = timed(torch, tail, steps, warmup)
     del tab
+    # the temperature-only Gumbel draw over a stored 128000-logit row
+    from molten_amd.hip import sample_params
+    rows = [bf16_randn(torch, (128000,), dev, gen, std=3.0) for _ in range(4)]
+    seen = torch.randint(-2**31, 2**31 - 1, (4000,), dtype=torch.int32, device=dev, generator=gen)
+    key = torch.zeros(1, dtype=torch.int64, device=dev)
+    prm = [sample_params(0.8, 1234, i, 1.1) for i in range(8)]
+    ms_s = timed(torch, lambda i: hip.sample_gumbel(rows[i % 4], 128000, seen, prm[i % 8], key), steps, warmup)
     # the prefill dense projections (dequant + GEMM fused), 4096 tokens: an
     # attention projection 2048 -> 2048 and the dense FFN gate 2048 -> 11776
     ms_x = []
@@ -200,7 +208,7 @@ def bench_next_rows(torch, hip, dev, gen, steps, warmup):
         pc = torch.empty((4096, n), dtype=torch.int16, device=dev)
         ms_x.append(timed(torch, lambda i: hip.gemm_q4_dense(pa, 4096, pw[i % 4][0], pc), steps, warmup))
         del pw, pc
-    return ms_p, ms_c, ms_d, ms_g, ms_t, ms_x
+    return ms_p, ms_c, ms_d, ms_g, ms_t, ms_x, ms_s
 
 
 def moe_set(torch, dev, gen, E=64, H=2048, I=1536):
@@ -354,8 +362,8 @@ def main() -> int:
         others["config1_q4_gemv_2048"] = dict(
             value=round(BYTES["config1"] / (ms1 * 1e-3) / 1e9, 1), unit="GB/s",
             ms_per_step=round(ms1, 5), frac_of_hbm_peak=round(BYTES["config1"] / (ms1 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
-        log("next rows: proj3, conv3, dense down K=11776, Q6 gather, token tail, dense prefill")
-        ms_p, ms_c, ms_d, ms_g, ms_t, ms_x = bench_next_rows(torch, hip, dev, gen, steps, warmup)
+        log("next rows: proj3, conv3, dense down K=11776, Q6 gather, token tail, Gumbel draw, dense prefill")
+        ms_p, ms_c, ms_d, ms_g, ms_t, ms_x, ms_s = bench_next_rows(torch, hip, dev, gen, steps, warmup)
         for n, ms in zip((2048, 11776), ms_x):
             tf = 2.0 * 4096 * n * 2048 / (ms * 1e-3) / 1e12
             others[f"next_dense_prefill_q4_4096x{n}x2048"] = dict(
@@ -363,7 +371,7 @@ def main() -> int:
                 frac_of_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4))
         for key, ms in (("next_proj3_gemv_scatter", ms_p), ("next_conv3_gemv", ms_c),
                         ("next_dense_down_q4_k11776", ms_d), ("next_gather_rows_q6_4096", ms_g),
-                        ("next_token_tail_embed", ms_t)):
+                        ("next_token_tail_embed", ms_t), ("next_sample_gumbel_128000", ms_s)):
             v = BYTES[key] / (ms * 1e-3) / 1e9
             others[key] = dict(value=round(v, 1), unit="GB/s", ms_per_step=round(ms, 5),
                                frac_of_hbm_peak=round(v / HBM_PEAK_GBS, 4))

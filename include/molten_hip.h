@@ -210,6 +210,30 @@ int mh_token_tail_embed(uint64_t* best, uint32_t* out_tok, const mh_quant_weight
 int mh_gather_rows_q6(const mh_quant_weights* w, const uint32_t* ids, uint32_t m, uint16_t* out,
                       mh_stream_t stream);
 
+/* src/lfm/sample.rs:264-285 encode_draw without top-k / top-p
+ * (lfm_sample.metal:157-190 lfm_sample_gumbel): the temperature draw from the
+ * bf16 logits row [n] folded into the greedy key word *best (zero or an
+ * earlier key; mh_token_tail reads and clears it): token = argmax_i w_i + G_i,
+ * w_i = v_i / p (v_i > 0) or v_i p (v_i <= 0) for seen tokens (bit i of seen
+ * [n / 32] words; only read when use_penalty), then times inv_temp, -0 folded
+ * to +0; G_i = -log(-log(1 - V)), V = (x_i + 0.5) 2^-32, x_i word i % 4 of
+ * Philox4x32-10(counter (i / 4, pos, 0x53414D50, 0), key (seed_lo, seed_hi));
+ * ties to the lower id.  The layout is the reference's SmpParams head.
+ * top_k != 0 or top_p < 1 (the kept-set path) -> MH_ERR_UNSUPPORTED. */
+typedef struct {
+    float inv_temp;
+    float penalty;
+    float inv_penalty;
+    uint32_t use_penalty;
+    uint32_t top_k;
+    float top_p;
+    uint32_t seed_lo, seed_hi;
+    uint32_t pos;
+    uint32_t pad0;
+} mh_sample_params;
+int mh_sample_gumbel(const uint16_t* logits, uint32_t n, const uint32_t* seen,
+                     const mh_sample_params* params, uint64_t* best, mh_stream_t stream);
+
 /* src/kernels/lfm.rs:794 argmax_bf16: two-stage argmax of a bf16 row,
  * ties to the lowest index.  partials: scratch of >= 64*8 bytes. */
 int mh_argmax_bf16(const uint16_t* x, uint32_t n, void* partials, uint32_t* out,

@@ -115,6 +115,64 @@ __device__ __forceinline__ float expf_fixed(float x) {
     return (p * pow2i(n1)) * pow2i(n2);
 }
 
+// log(x) in f32 for finite x > 0 (the sampler's Gumbel transform): x =
+// m 2^k with m in [sqrt(1/2), sqrt(2)), log m = 2 atanh(s), s = (m - 1) /
+// (m + 1), as the odd series 2 s (1 + s^2/3 + s^4/5 + ... + s^10/11) in
+// Horner form with fma, plus k ln2 with ln2 split into a 16-bit head and a
+// tail.  Written out so the CPU restatement reproduces it bit for bit.
+__device__ __forceinline__ float logf_fixed(float x) {
+    uint32_t u = __float_as_uint(x);
+    int k = static_cast<int>(u >> 23) - 127;
+    if ((u >> 23) == 0u) {  // denormal: scale into the normal range
+        u = __float_as_uint(x * 0x1p25f);
+        k = static_cast<int>(u >> 23) - 127 - 25;
+    }
+    float m = __uint_as_float((u & 0x007fffffu) | 0x3f800000u);  // [1, 2)
+    if (m > 1.41421356f) {
+        m = m * 0.5f;
+        k += 1;
+    }
+    const float s = (m - 1.0f) / (m + 1.0f);
+    const float s2 = s * s;
+    float p = 0x1.745d18p-4f;                  // 1/11
+    p = __builtin_fmaf(p, s2, 0x1.c71c72p-4f);  // 1/9
+    p = __builtin_fmaf(p, s2, 0x1.24924ap-3f);  // 1/7
+    p = __builtin_fmaf(p, s2, 0x1.99999ap-3f);  // 1/5
+    p = __builtin_fmaf(p, s2, 0x1.555556p-2f);  // 1/3
+    p = __builtin_fmaf(p, s2, 1.0f);
+    const float lm = (2.0f * s) * p;
+    const float kf = static_cast<float>(k);
+    return __builtin_fmaf(kf, 0x1.62e400p-1f, __builtin_fmaf(kf, 0x1.7f7d1cp-20f, lm));
+}
+
+// Philox4x32-10 (Salmon et al., SC 2011): ten rounds of the two 32x32->64
+// multiplies, the key bumped by the Weyl constants after each round.
+__device__ __forceinline__ u32x4 philox4x32_10(u32x4 c, uint32_t k0, uint32_t k1) {
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        const uint64_t p0 = static_cast<uint64_t>(0xD2511F53u) * c.x;
+        const uint64_t p1 = static_cast<uint64_t>(0xCD9E8D57u) * c.z;
+        c = u32x4{static_cast<uint32_t>(p1 >> 32) ^ c.y ^ k0, static_cast<uint32_t>(p1),
+                  static_cast<uint32_t>(p0 >> 32) ^ c.w ^ k1, static_cast<uint32_t>(p0)};
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    return c;
+}
+
+// Gumbel(0, 1) from a 32-bit uniform word (lfm_sample.metal:141-155): V =
+// (x + 0.5) 2^-32, E = -log(1 - V) (its series below V = 1/64), G = -log E.
+__device__ __forceinline__ float gumbel_of(uint32_t x) {
+    const float v = (static_cast<float>(x) + 0.5f) * 2.3283064365386963e-10f;
+    float e;
+    if (v < 0.015625f) {
+        e = v * (1.0f + v * (0.5f + v * (0.33333334f + v * 0.25f)));
+    } else {
+        e = -logf_fixed(fmaxf(1.0f - v, 2.9802322387695312e-08f));
+    }
+    return -logf_fixed(e);
+}
+
 // bf16(silu(g)) with silu(g) = g / (1 + exp(-g)), IEEE division.
 __device__ __forceinline__ float silu_bf16(float g) {
     return round_bf16(g / (1.0f + expf_fixed(-g)));

@@ -86,6 +86,7 @@ _SIGNATURES = {
     "mh_proj3_gemv_scatter": [_qw, _qw, _qw, _vp, _vp, _vp, _vp, _u32, _u32, _vp],
     "mh_conv3_gemv": [_qw, _vp, _vp, _vp, _vp, _vp, _vp],
     "mh_token_tail": [_vp, _vp, _u32, _vp],
+    "mh_sample_gumbel": [_vp, _u32, _vp, _vp, _vp, _vp],
     "mh_checkpoint_open": [ctypes.c_char_p, ctypes.POINTER(_vp)],
     "mh_checkpoint_close": [_vp],
     "mh_checkpoint_count": [_vp],
@@ -335,6 +336,28 @@ def gather_rows_q6(table: QuantWeights, ids, m: int, out, stream=None) -> None:
 def gemm_q4_dense(a, m: int, w: QuantWeights, c, stream=None) -> None:
     """src/lfm.rs:661 (prefill dense projection: dequant + bf16 GEMM, fused)."""
     check(load().mh_gemm_q4_dense(_ptr(a), m, _qref(w), _ptr(c), _stream(stream)), "gemm_q4_dense")
+
+
+class SampleParams(ctypes.Structure):
+    """The reference's SmpParams head (src/lfm/sample.rs:175-192)."""
+    _fields_ = [("inv_temp", ctypes.c_float), ("penalty", ctypes.c_float), ("inv_penalty", ctypes.c_float),
+                ("use_penalty", ctypes.c_uint32), ("top_k", ctypes.c_uint32), ("top_p", ctypes.c_float),
+                ("seed_lo", ctypes.c_uint32), ("seed_hi", ctypes.c_uint32), ("pos", ctypes.c_uint32),
+                ("pad0", ctypes.c_uint32)]
+
+
+def sample_params(temperature: float, seed: int, pos: int, penalty: float = 1.0, top_k: int = 0,
+                  top_p: float = 1.0) -> SampleParams:
+    import numpy as np
+    return SampleParams(float(np.float32(1.0) / np.float32(temperature)), penalty,
+                        float(np.float32(1.0) / np.float32(penalty)), int(penalty != 1.0), top_k, top_p,
+                        seed & 0xffffffff, seed >> 32, pos, 0)
+
+
+def sample_gumbel(logits, n: int, seen, params: SampleParams, best, stream=None) -> None:
+    """src/lfm/sample.rs:264 encode_draw, temperature only (the key folds into best)."""
+    check(load().mh_sample_gumbel(_ptr(logits), n, _ptr(seen), ctypes.byref(params), _ptr(best),
+                                  _stream(stream)), "sample_gumbel")
 
 
 class TensorMeta(ctypes.Structure):

@@ -116,6 +116,22 @@ void orc_conv3(const orc_qw* w, const uint16_t* x, const uint16_t* taps, const u
 void orc_token_tail_embed(uint64_t* best, uint32_t* out_tok, const orc_qw* e, const uint16_t* w,
                           uint16_t* x, uint16_t* normed, float eps);
 
+/* ---- next row: the temperature-only Gumbel draw (lfm_sample.metal:124-190;
+ * src/lfm/sample.rs:264-285) ---------------------------------------------------
+ * orc_philox: Philox4x32-10.  Pinned: Random123's published known-answer
+ * vectors.  orc_logf: the device's own log.  Pinned: <= 2 ulp vs float64 over
+ * a dense sweep, exact powers of two.  orc_gumbel: -log(-log(1 - V)).  Pinned:
+ * vs float64 within tolerance on both branches.  orc_sample_gumbel: the draw's
+ * key.  Pinned: the empirical token frequencies over many positions match
+ * softmax(w) (chi-square), the penalty and temperature closed forms.  Parity
+ * with the reference's own bits is unpinned where Metal's log decides them. */
+float orc_logf(float x);
+void orc_philox(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+float orc_gumbel(uint32_t x);
+uint64_t orc_sample_gumbel(const uint16_t* logits, uint32_t n, const uint32_t* seen, float inv_temp, float penalty,
+                           float inv_penalty, int use_penalty, uint32_t seed_lo, uint32_t seed_hi, uint32_t pos,
+                           uint64_t best);
+
 /* ---- a6: argmax over bf16 logits (lfm.metal:1113-1282) ------------------
  * value desc, index asc; -0 == +0; NaN never taken; none -> 0.  Pinned by
  * known-answer ties and numpy argmax on tie-free rows. */

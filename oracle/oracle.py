@@ -51,6 +51,11 @@ def lib() -> ctypes.CDLL:
         _lib.orc_argmax_bf16.restype = ctypes.c_uint32
         _lib.orc_argmax_key.restype = ctypes.c_uint64
         _lib.orc_argmax_key.argtypes = [ctypes.c_float, ctypes.c_uint32]
+        _lib.orc_logf.restype = ctypes.c_float
+        _lib.orc_logf.argtypes = [ctypes.c_float]
+        _lib.orc_gumbel.restype = ctypes.c_float
+        _lib.orc_gumbel.argtypes = [ctypes.c_uint32]
+        _lib.orc_sample_gumbel.restype = ctypes.c_uint64
         _lib.orc_get_threads.restype = ctypes.c_int
     return _lib
 
@@ -160,6 +165,35 @@ def token_tail_embed(key: int, h, w: np.ndarray, eps: float):
     lib().orc_token_tail_embed(_p(best), _p(tok), ctypes.byref(e), _p(w), _p(x), _p(normed),
                                ctypes.c_float(eps))
     return int(tok[0]), x, normed, int(best[0])
+
+
+def philox(ctr, key) -> np.ndarray:
+    c = np.array(ctr, np.uint32)
+    k = np.array(key, np.uint32)
+    out = np.empty(4, np.uint32)
+    lib().orc_philox(_p(c), _p(k), _p(out))
+    return out
+
+
+def logf(x: float) -> float:
+    return lib().orc_logf(ctypes.c_float(x))
+
+
+def gumbel(x: int) -> float:
+    return lib().orc_gumbel(ctypes.c_uint32(x))
+
+
+def sample_gumbel(logits: np.ndarray, seen, inv_temp: float, penalty: float, use_penalty: bool,
+                  seed: int, pos: int, best: int = 0) -> int:
+    """The key of the temperature-only draw (lfm_sample_gumbel), folded with best."""
+    logits = np.ascontiguousarray(logits, np.uint16)
+    seen = None if seen is None else np.ascontiguousarray(seen, np.uint32)
+    inv_pen = np.float32(1.0) / np.float32(penalty)
+    return int(lib().orc_sample_gumbel(_p(logits), ctypes.c_uint32(logits.size), _p(seen),
+                                       ctypes.c_float(inv_temp), ctypes.c_float(penalty),
+                                       ctypes.c_float(inv_pen), ctypes.c_int(int(use_penalty)),
+                                       ctypes.c_uint32(seed & 0xffffffff), ctypes.c_uint32(seed >> 32),
+                                       ctypes.c_uint32(pos), ctypes.c_uint64(best)))
 
 
 def gemv_quant_rows(h, x: np.ndarray, rows: np.ndarray, batch: int = 1) -> np.ndarray:

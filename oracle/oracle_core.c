@@ -335,6 +335,97 @@ void orc_token_tail_embed(uint64_t* best, uint32_t* out_tok, const orc_qw* e, co
     free(q);
 }
 
+/* ------------------------------------------------------------ sampling --- */
+
+/* log(x), x finite > 0: the device's logf_fixed step for step (m 2^k, m in
+ * [sqrt(1/2), sqrt(2)), 2 atanh((m-1)/(m+1)) as an odd series to s^11, k ln2
+ * split). */
+float orc_logf(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    int k = (int)(u >> 23) - 127;
+    if ((u >> 23) == 0u) {
+        const float xs = x * 0x1p25f;
+        memcpy(&u, &xs, 4);
+        k = (int)(u >> 23) - 127 - 25;
+    }
+    const uint32_t mu = (u & 0x007fffffu) | 0x3f800000u;
+    float m;
+    memcpy(&m, &mu, 4);
+    if (m > 1.41421356f) {
+        m = m * 0.5f;
+        k += 1;
+    }
+    const float s = (m - 1.0f) / (m + 1.0f);
+    const float s2 = s * s;
+    float p = 0x1.745d18p-4f;
+    p = fmaf(p, s2, 0x1.c71c72p-4f);
+    p = fmaf(p, s2, 0x1.24924ap-3f);
+    p = fmaf(p, s2, 0x1.99999ap-3f);
+    p = fmaf(p, s2, 0x1.555556p-2f);
+    p = fmaf(p, s2, 1.0f);
+    const float lm = (2.0f * s) * p;
+    const float kf = (float)k;
+    return fmaf(kf, 0x1.62e400p-1f, fmaf(kf, 0x1.7f7d1cp-20f, lm));
+}
+
+/* Philox4x32-10 (Salmon et al., SC 2011), as lfm_sample.metal:124-135. */
+void orc_philox(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3], k0 = key[0], k1 = key[1];
+    for (int r = 0; r < 10; ++r) {
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+        const uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0, n1 = (uint32_t)p1;
+        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1, n3 = (uint32_t)p0;
+        c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+/* lfm_sample.metal:141-155 smp_gumbel. */
+float orc_gumbel(uint32_t x) {
+    const float v = ((float)x + 0.5f) * 2.3283064365386963e-10f;
+    float e;
+    if (v < 0.015625f) {
+        e = v * (1.0f + v * (0.5f + v * (0.33333334f + v * 0.25f)));
+    } else {
+        const float a = 1.0f - v;
+        e = -orc_logf(a > 2.9802322387695312e-08f ? a : 2.9802322387695312e-08f);
+    }
+    return -orc_logf(e);
+}
+
+/* lfm_sample.metal:157-190 lfm_sample_gumbel over the whole row: the key of
+ * argmax_i (w_i + G_i), folded with *best. */
+uint64_t orc_sample_gumbel(const uint16_t* logits, uint32_t n, const uint32_t* seen, float inv_temp, float penalty,
+                           float inv_penalty, int use_penalty, uint32_t seed_lo, uint32_t seed_hi, uint32_t pos,
+                           uint64_t best) {
+    const uint32_t key[2] = {seed_lo, seed_hi};
+    for (uint32_t q = 0; q < n / 4; ++q) {
+        const uint32_t ctr[4] = {q, pos, 0x53414D50u, 0u};
+        uint32_t r[4];
+        orc_philox(ctr, key, r);
+        for (uint32_t j = 0; j < 4; ++j) {
+            const uint32_t i = 4 * q + j;
+            float v = orc_bf16_to_f32(logits[i]);
+            if (use_penalty && ((seen[i >> 5] >> (i & 31u)) & 1u)) {
+                v = v > 0.0f ? v * inv_penalty : v * penalty;
+            }
+            float w = v * inv_temp;
+            uint32_t u;
+            memcpy(&u, &w, 4);
+            if ((u << 1) == 0u) {
+                w = 0.0f;
+            }
+            const uint64_t k = orc_argmax_key(w + orc_gumbel(r[j]), i);
+            best = k > best ? k : best;
+        }
+    }
+    return best;
+}
+
 /* ------------------------------------------------------------- argmax --- */
 
 uint32_t orc_argmax_bf16(const uint16_t* x, size_t n) {

@@ -136,3 +136,16 @@ def test_dense_gemm_arguments():
     with pytest.raises(hip.MoltenError) as ei:
         hip.gemm_q4_dense(0x4000, 0, _qw(), 0x5000, stream=0)
     assert ei.value.code == hip.MH_ERR_INVALID
+
+
+def test_sample_arguments():
+    p = hip.sample_params(1.0, 1, 0)
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.sample_gumbel(0x4000, 128000, 0x5000, hip.sample_params(1.0, 1, 0, top_k=40), 0x6000, stream=0)
+    assert ei.value.code == hip.MH_ERR_UNSUPPORTED
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.sample_gumbel(0x4000, 128002, 0x5000, p, 0x6000, stream=0)
+    assert ei.value.code == hip.MH_ERR_INVALID
+    with pytest.raises(hip.MoltenError) as ei:  # the penalty reads the seen set
+        hip.sample_gumbel(0x4000, 128000, None, hip.sample_params(1.0, 1, 0, penalty=1.2), 0x6000, stream=0)
+    assert ei.value.code == hip.MH_ERR_INVALID
