@@ -273,6 +273,151 @@ def bench_config4(torch, hip, dev, gen, steps, warmup):
     return ms_step, ms_gemm
 
 
+def measure_ceilings(torch, dev, steps, warmup):
+    """What this part reaches with nothing but the bound resource in use
+    (libmolten_ceiling.so): a streaming read of the LM heads' byte counts
+    (config 2 75.6 MB, config 5 109 MB; rotated over 5 copies, as the GEMVs
+    are) and of 1 GiB, and the bf16 matrix cores with independent MFMAs
+    only.  The read is the best of a small sweep of launch shapes."""
+    import ctypes
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "molten_amd", "libmolten_ceiling.so"))
+    vp, u32 = ctypes.c_void_p, ctypes.c_uint32
+    lib.mhc_read.argtypes = [vp, ctypes.c_size_t, u32, u32, ctypes.c_int, vp, vp]
+    lib.mhc_mfma.argtypes = [vp, u32, u32, vp]
+    lib.mhc_mfma_flops.argtypes = [u32, u32]
+    lib.mhc_mfma_flops.restype = ctypes.c_uint64
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    out = {}
+
+    def stream():
+        return vp(torch.cuda.current_stream().cuda_stream)
+
+    for key, nbytes, copies in (("hbm_read_75.6MB", 75_632_640, 5), ("hbm_read_109MB", 109_187_072, 5),
+                                ("hbm_read_1GiB", 1 << 30, 1)):
+        bufs = [torch.empty(nbytes // 4, dtype=torch.int32, device=dev).random_() for _ in range(copies)]
+        best = None
+        for unroll, grid in ((1, 2048), (1, 4096), (4, 512), (8, 256)):
+            def fn(i, unroll=unroll, grid=grid):
+                rc = lib.mhc_read(bufs[i % copies].data_ptr(), nbytes, grid, unroll, 1, sink.data_ptr(), stream())
+                assert rc == 0, rc
+            ms = timed(torch, fn, steps, warmup)
+            if best is None or ms < best[0]:
+                best = (ms, unroll, grid)
+        ms, unroll, grid = best
+        out[key] = dict(value=round(nbytes / (ms * 1e-3) / 1e9, 1), unit="GB/s", us=round(ms * 1e3, 2),
+                        frac_of_hbm_peak=round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                        launch=f"{grid} x 256 threads, {unroll} x 16-byte non-temporal loads in flight")
+        del bufs
+    fo = torch.empty(1024 * 256, dtype=torch.float32, device=dev)
+    wg, iters = 512, 1000
+
+    def mf(i):
+        assert lib.mhc_mfma(fo.data_ptr(), wg, iters, stream()) == 0
+
+    ms = timed(torch, mf, max(4, steps // 20), 2)
+    tf = lib.mhc_mfma_flops(wg, iters) / (ms * 1e-3) / 1e12
+    out["bf16_mfma_32x32x16"] = dict(value=round(tf, 1), unit="TFLOP/s", us=round(ms * 1e3, 1),
+                                     frac_of_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4),
+                                     launch=f"{wg} x 4 waves, 8 independent accumulators per wave")
+    return out
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _repeat(fn, budget_s: float, max_reps: int = 1000):
+    """Seconds per call of fn() over about budget_s seconds (after one warm call)."""
+    fn()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= max_reps:
+            return el / reps, reps, el
+
+
+def cpu_baselines(budget_s: float, threads_all: int):
+    """The C oracle (the same code the parity tests check against: MLX
+    affine dequant semantics, f32 accumulation, OpenMP over output rows /
+    expert rows) on the host cores, every BASELINE config at 1 thread and at
+    `threads_all` threads, each timed for about budget_s seconds.  Config 4
+    runs the whole prefill step (router, sort, gate/up + SwiGLU, down,
+    combine) for a stated subset of tokens (their expert rows only) and is
+    reported in FLOP/s of the rows computed."""
+    import numpy as np
+
+    from molten_amd import layout
+    from oracle import oracle as orc
+
+    rng = np.random.default_rng(0)
+    h4 = layout.synth_quant(rng, 65536, 2048, 4)
+    h6 = layout.synth_quant(rng, 65536, 2048, 6)
+    h1 = layout.synth_quant(rng, 2048, 2048, 4)
+    x1 = layout.synth_bf16(rng, (1, 2048))
+    x8 = layout.synth_bf16(rng, (8, 2048))
+    E, H, I, topk, m = 64, 2048, 1536, 4, 4096
+    gate = layout.synth_quant(rng, E * I, H, 4)
+    up = layout.synth_quant(rng, E * I, H, 4)
+    down = layout.synth_quant(rng, E * H, I, 4)
+    router = layout.f32_to_bf16((rng.normal(0, 0.02, (E, H))).astype(np.float32))
+    xm = layout.synth_bf16(rng, (m, H))
+
+    def head(h, x, b):
+        def f():
+            y = orc.gemv_quant(h, x, b)
+            for r in range(b):
+                orc.argmax_bf16(y[r])
+        return f
+
+    out = {"cpu_model": _cpu_model(), "nproc": os.cpu_count()}
+    for threads in (1, threads_all):
+        orc.set_threads(threads)
+        res = {}
+        for key, fn, unit_work in (
+                ("config1", lambda: orc.gemv_quant(h1, x1, 1), BYTES["config1"]),
+                ("config2", head(h4, x1, 1), BYTES["config2"]),
+                ("config5_b1", head(h6, x1, 1), BYTES["config5_b1"]),
+                ("config5_b8", head(h6, x8, 8), BYTES["config5_b8"]),
+                ("config3", lambda: orc.moe_decode(router, None, 1, gate, up, down, E, topk, H, I,
+                                                   xm[len(res) % m]), BYTES["config3"])):
+            per, reps, el = _repeat(fn, budget_s)
+            res[key] = dict(value=round(unit_work / per / 1e9, 3), unit="GB/s", ms_per_step=round(per * 1e3, 3),
+                            reps=reps)
+        # config 4: the grouped GEMMs (gate, up, down) of `ne` experts with
+        # 256 rows each (the config's mean rows per expert), one block-map
+        # entry per expert covering all its columns
+        ne = 1 if threads == 1 else threads
+        rows = 256
+        a_gu = xm[:ne * rows]
+        a_dn = layout.synth_bf16(rng, (ne * rows, I))
+        mg = np.array([[e * rows, e * I, 0, (e + 1) * rows] for e in range(ne)], np.uint32)
+        md = np.array([[e * rows, e * H, 0, (e + 1) * rows] for e in range(ne)], np.uint32)
+
+        def grouped():
+            orc.gemm_q4_grouped(a_gu, gate, mg, ne, I, I)
+            orc.gemm_q4_grouped(a_gu, up, mg, ne, I, I)
+            orc.gemm_q4_grouped(a_dn, down, md, ne, H, H)
+
+        per, reps, el = _repeat(grouped, budget_s, max_reps=50)
+        flops = 3.0 * 2 * ne * rows * I * H
+        res["config4"] = dict(value=round(flops / per / 1e9, 2), unit="GFLOP/s", ms_per_step=round(per * 1e3, 1),
+                              reps=reps, sample=f"gate, up and down grouped GEMMs of {ne} expert(s) x {rows} rows "
+                                                f"(the config's mean rows per expert); the full config is 64 experts")
+        out[f"threads_{threads}"] = res
+    orc.set_threads(threads_all)
+    return out
+
+
 def cpu_baseline_config2(budget_s: float):
     """The C oracle's Q4 LM-head GEMV (65536 x 2048, batch 1) + argmax on the
     host cores, repeated for about `budget_s` seconds."""
@@ -284,16 +429,7 @@ def cpu_baseline_config2(budget_s: float):
     rng = np.random.default_rng(0)
     h = layout.synth_quant(rng, 65536, 2048, 4)
     x = layout.synth_bf16(rng, (1, 2048))
-    orc.gemv_quant(h, x, 1)  # warm
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        y = orc.gemv_quant(h, x, 1)
-        orc.argmax_bf16(y[0])
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 1000:
-            break
-    per = el / reps
+    per, reps, el = _repeat(lambda: orc.argmax_bf16(orc.gemv_quant(h, x, 1)[0]), budget_s)
     return dict(value=round(BYTES["config2"] / per / 1e9, 3), unit="GB/s", cores=orc.get_threads(),
                 kind="port",
                 sample=f"full config 2 workload (65536x2048 Q4 GEMV + argmax) x {reps} reps, "
@@ -318,6 +454,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="time budget of the CPU baseline sample (0 = skip)")
+    ap.add_argument("--cpu-all-seconds", type=float, default=1.5,
+                    help="time budget of each per-config CPU baseline sample (0 = skip)")
     ap.add_argument("--only-headline", action="store_true", help="skip configs 1, 3, 4, 5")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="also run a plain elementwise copy (f32 negate) of this many MiB "
@@ -397,10 +535,17 @@ def main() -> int:
             grouped_gemm_only_ms=round(ms4g, 4),
             frac_of_bf16_peak=round(FLOPS_CONFIG4 / (ms4g * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
 
+    log("ceilings: streaming read, bf16 matrix cores")
+    ceilings = measure_ceilings(torch, dev, min(steps, 100), min(warmup, 5))
+
     cpu = None
     if args.cpu_seconds > 0:
         log("CPU baseline (oracle, config 2)")
         cpu = cpu_baseline_config2(args.cpu_seconds)
+        if not args.only_headline and args.cpu_all_seconds > 0:
+            log("CPU baseline (oracle, every config, 1 thread and all threads)")
+            from oracle import oracle as orc
+            cpu["per_config"] = cpu_baselines(args.cpu_all_seconds, orc.get_threads())
 
     line = {
         "metric": "Q4 LM-head GEMV + argmax HBM GB/s (config 2; MoE decode / prefill under others)",
@@ -422,6 +567,7 @@ def main() -> int:
                      "traffic": read_traffic()},
         "cpu_baseline": cpu,
         "others": others,
+        "ceilings": ceilings,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -1,0 +1,144 @@
+// ceiling.hip -- measurement kernels that frame the hot path's rooflines on
+// this part: what a plain streaming read of HBM reaches, and what the bf16
+// matrix cores reach with nothing but independent MFMAs in flight.  They
+// have no counterpart in the reference (which publishes its own ceiling as
+// a measured streaming read, docs/ARCHITECTURE.md:48); they are not part of
+// the operator boundary and live in their own library.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "molten_ceiling.h"
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// Streaming read: every thread loads U 16-byte pieces per round (all in
+// flight before any is used), rounds stride over the grid.  The xor of the
+// data is stored only when it equals a value the data never produces in
+// practice, so the loads stay live and almost nothing is written.
+template <int U, bool NT>
+__global__ __launch_bounds__(256) void k_read(const uint4* __restrict__ p, uint64_t n16, uint32_t* sink) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256u;
+    uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;
+    uint32_t acc = 0;
+    for (; i + (U - 1) * stride < n16; i += U * stride) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if constexpr (NT) {
+                const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p + i + u * stride));
+                v[u] = make_uint4(t.x, t.y, t.z, t.w);
+            } else {
+                v[u] = p[i + u * stride];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < n16; i += stride) {
+        const uint4 v = p[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9e3779b9u) {
+        sink[0] = acc;
+    }
+}
+
+// Copy (read + write of the same byte count), for the counter calibration.
+__global__ __launch_bounds__(256) void k_copy(const uint4* __restrict__ src, uint4* __restrict__ dst, uint64_t n16) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256u;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x; i < n16; i += stride) {
+        dst[i] = src[i];
+    }
+}
+
+// bf16 matrix-core rate: each wave keeps 8 independent 32x32 accumulators
+// and issues v_mfma_f32_32x32x16_bf16 back to back, `iters` rounds of 8.
+__global__ __launch_bounds__(256) void k_mfma(float* out, uint32_t iters) {
+    const int lane = threadIdx.x & 63;
+    bf16x8_t a, b;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        a[j] = static_cast<__bf16>(0.001f * static_cast<float>(lane + j));
+        b[j] = static_cast<__bf16>(0.002f * static_cast<float>(lane - j));
+    }
+    f32x16_t acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) acc[c][q] = 0.0f;
+    for (uint32_t it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[c], 0, 0, 0);
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) s += acc[c][q];
+    if (s == 1234.5f) {  // keeps the chain live; practically never stored
+        out[blockIdx.x * 256 + threadIdx.x] = s;
+    }
+}
+
+template <int U, bool NT>
+void launch_read(const void* p, uint64_t n16, uint32_t grid, uint32_t* sink, hipStream_t s) {
+    hipLaunchKernelGGL((k_read<U, NT>), dim3(grid), dim3(256), 0, s, static_cast<const uint4*>(p), n16, sink);
+}
+
+int status() {
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : static_cast<int>(e);
+}
+
+}  // namespace
+
+extern "C" {
+
+int mhc_read(const void* src, size_t bytes, uint32_t grid, uint32_t unroll, int nontemporal, uint32_t* sink,
+             void* stream) {
+    if (src == nullptr || sink == nullptr || bytes % 16 != 0 || grid == 0 ||
+        reinterpret_cast<uintptr_t>(src) % 16 != 0) {
+        return -1;
+    }
+    const uint64_t n16 = bytes / 16;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool nt = nontemporal != 0;
+    switch (unroll) {
+        case 1: nt ? launch_read<1, true>(src, n16, grid, sink, s) : launch_read<1, false>(src, n16, grid, sink, s); break;
+        case 2: nt ? launch_read<2, true>(src, n16, grid, sink, s) : launch_read<2, false>(src, n16, grid, sink, s); break;
+        case 4: nt ? launch_read<4, true>(src, n16, grid, sink, s) : launch_read<4, false>(src, n16, grid, sink, s); break;
+        case 8: nt ? launch_read<8, true>(src, n16, grid, sink, s) : launch_read<8, false>(src, n16, grid, sink, s); break;
+        default: return -1;
+    }
+    return status();
+}
+
+int mhc_copy(const void* src, void* dst, size_t bytes, uint32_t grid, void* stream) {
+    if (src == nullptr || dst == nullptr || bytes % 16 != 0 || grid == 0 ||
+        reinterpret_cast<uintptr_t>(src) % 16 != 0 || reinterpret_cast<uintptr_t>(dst) % 16 != 0) {
+        return -1;
+    }
+    hipLaunchKernelGGL(k_copy, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint4*>(src), static_cast<uint4*>(dst), static_cast<uint64_t>(bytes / 16));
+    return status();
+}
+
+int mhc_mfma(float* out, uint32_t workgroups, uint32_t iters, void* stream) {
+    if (out == nullptr || workgroups == 0) {
+        return -1;
+    }
+    hipLaunchKernelGGL(k_mfma, dim3(workgroups), dim3(256), 0, static_cast<hipStream_t>(stream), out, iters);
+    return status();
+}
+
+uint64_t mhc_mfma_flops(uint32_t workgroups, uint32_t iters) {
+    return static_cast<uint64_t>(workgroups) * 4u * iters * 8u * (32u * 32u * 16u * 2u);
+}
+
+}  // extern "C"

@@ -352,8 +352,23 @@ int parse_shard(mh_checkpoint* ck, int shard) {
                   kv.first.c_str(), m.shape.size());
         const uint64_t a = off->arr[0].u, b = off->arr[1].u;
         MH_ENSURE(b >= a, MH_ERR_INVALID, "checkpoint: tensor %s has reversed data offsets", kv.first.c_str());
-        MH_ENSURE(data + b <= static_cast<uint64_t>(fsize), MH_ERR_INVALID,
+        // data <= fsize holds (hlen <= fsize - 8), so the subtraction cannot wrap
+        MH_ENSURE(b <= static_cast<uint64_t>(fsize) - data, MH_ERR_INVALID,
                   "checkpoint: tensor %s extends past the end of %s", kv.first.c_str(), path.c_str());
+        // the byte range must be exactly the shape's elements (known dtypes):
+        // reads copy end - start bytes into buffers sized from the shape
+        if (dtype_size(m.dtype) != 0) {
+            uint64_t elems = 1;
+            bool fits = true;
+            for (uint64_t d : m.shape) {
+                fits = fits && (d == 0 || elems <= UINT64_MAX / d);
+                elems = fits ? elems * d : 0;
+            }
+            fits = fits && elems <= UINT64_MAX / dtype_size(m.dtype);
+            MH_ENSURE(fits && b - a == elems * dtype_size(m.dtype), MH_ERR_INVALID,
+                      "checkpoint: tensor %s holds %llu bytes, its shape needs a different count", kv.first.c_str(),
+                      static_cast<unsigned long long>(b - a));
+        }
         m.start = data + a;
         m.end = data + b;
         m.shard = shard;
@@ -522,7 +537,10 @@ int mh_load_quant(mh_checkpoint* ck, const char* base, uint32_t rows, uint32_t k
     MH_ENSURE(wm, MH_ERR_INVALID, "missing %s.weight", base);
     MH_ENSURE(wm->dtype == MH_DTYPE_U32, MH_ERR_INVALID, "%s codes must be U32", base);
     MH_ENSURE(!wm->shape.empty(), MH_ERR_INVALID, "%s: empty shape", base);
+    MH_ENSURE(bits == 4u || bits == 6u || bits == 8u, MH_ERR_UNSUPPORTED, "%s: unsupported bit width %u", base, bits);
+    MH_ENSURE(k > 0u && rows > 0u, MH_ERR_INVALID, "%s: empty matrix (%u x %u)", base, rows, k);
     const uint64_t cols = wm->shape.back();
+    MH_ENSURE(cols > 0u, MH_ERR_INVALID, "%s: codes have no columns", base);
     MH_ENSURE(k % 64u == 0 && !sm->shape.empty() && sm->shape.back() == k / 64u, MH_ERR_INVALID,
               "%s: scales group count mismatch", base);
     const uint64_t found = 32u * cols / k;
@@ -536,6 +554,13 @@ int mh_load_quant(mh_checkpoint* ck, const char* base, uint32_t rows, uint32_t k
               rows);
     MH_ENSURE(ns / (k / 64u) == rows && nb / (k / 64u) == rows, MH_ERR_INVALID, "%s: scale rows mismatch", base);
     MH_ENSURE(sm->dtype == MH_DTYPE_BF16 && bm->dtype == MH_DTYPE_BF16, MH_ERR_INVALID, "%s: scales dtype", base);
+    // the caller's buffers hold exactly rows x k codes and rows x k/64 scale /
+    // bias pairs: every byte range read must be that size
+    const uint64_t code_bytes = static_cast<uint64_t>(rows) * k * bits / 8u;
+    const uint64_t sb_bytes = static_cast<uint64_t>(rows) * (k / 64u) * 2u;
+    MH_ENSURE(wm->end - wm->start == code_bytes && sm->end - sm->start == sb_bytes &&
+                  bm->end - bm->start == sb_bytes,
+              MH_ERR_INVALID, "%s: tensor byte counts do not match %u x %u at %u bits", base, rows, k, bits);
     MH_TRY(mh_checkpoint_read(ck, (b + ".weight").c_str(), codes, wm->end - wm->start, stream));
     MH_TRY(mh_checkpoint_read(ck, (b + ".scales").c_str(), scales, sm->end - sm->start, stream));
     MH_TRY(mh_checkpoint_read(ck, (b + ".biases").c_str(), biases, bm->end - bm->start, stream));

@@ -136,6 +136,30 @@ _RESTYPES = {"mh_last_error": ctypes.c_char_p, "mh_version": ctypes.c_char_p,
 _lib: Optional[ctypes.CDLL] = None
 
 
+def _one_runtime() -> None:
+    """Load torch's HIP runtime first when torch is installed.
+
+    torch ships its own libamdhip64.so with the same soname
+    (libamdhip64.so.7) as the ROCm copy this library is linked against.  The
+    dynamic linker resolves a DT_NEEDED entry against the sonames of the
+    objects already loaded, so with torch imported first the library binds
+    to torch's runtime and the process holds one HIP runtime, whose streams
+    torch hands to the launchers.  Loaded the other way round, the process
+    would hold two runtimes, and a stream or event of one passed to the
+    other.  Without torch (the Rust host, a torch-free worker) the library
+    loads the ROCm runtime on its own: again one runtime."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
+def hip_runtimes() -> list[str]:
+    """Paths of the HIP runtime libraries mapped into this process."""
+    with open("/proc/self/maps") as f:
+        return sorted({ln.split()[-1] for ln in f if "libamdhip64" in ln and "/" in ln})
+
+
 def load(path: str = LIB_PATH) -> ctypes.CDLL:
     """Load the native library (once).  Raises if it has not been built."""
     global _lib
@@ -145,7 +169,10 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         raise ImportError(
             f"{path} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()')"
         )
+    _one_runtime()
     lib = ctypes.CDLL(path)
+    if len(hip_runtimes()) != 1:
+        raise ImportError(f"{path}: more than one HIP runtime in the process: {hip_runtimes()}")
     for name, argtypes in _SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes

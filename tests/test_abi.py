@@ -17,6 +17,40 @@ def test_library_exports_every_declared_symbol():
     assert sorted(set(names) - set(hip._SIGNATURES)) == []
 
 
+def test_one_hip_runtime():
+    """The library and torch share one HIP runtime: torch's runtime carries
+    the soname the library needs, and hip.load() imports torch first."""
+    import torch  # noqa: F401
+
+    hip.load()
+    rts = hip.hip_runtimes()
+    assert len(rts) == 1, rts
+    assert "torch" in rts[0], rts
+
+
+def test_ceiling_library_exports():
+    """The measurement kernels' library (bench.py --ceilings) exports what
+    include/molten_ceiling.h declares and rejects bad arguments on the host."""
+    import os
+    import re
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    text = open(os.path.join(root, "include", "molten_ceiling.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = sorted(set(re.findall(r"\b(mhc_[a-z0-9_]+)\s*\(", text)))
+    assert names == ["mhc_copy", "mhc_mfma", "mhc_mfma_flops", "mhc_read"]
+    hip.load()
+    lib = ctypes.CDLL(os.path.join(root, "molten_amd", "libmolten_ceiling.so"))
+    for n in names:
+        assert hasattr(lib, n), n
+    lib.mhc_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_uint32,
+                             ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    assert lib.mhc_read(0x1000, 100, 8, 1, 0, 0x2000, None) == -1   # not a multiple of 16
+    assert lib.mhc_read(0x1000, 1024, 8, 3, 0, 0x2000, None) == -1  # unroll 3
+    lib.mhc_mfma_flops.restype = ctypes.c_uint64
+    assert lib.mhc_mfma_flops(2, 3) == 2 * 4 * 3 * 8 * 32 * 32 * 16 * 2
+
+
 def test_version():
     assert b"gfx950" in hip.load().mh_version()
 

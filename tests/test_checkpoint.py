@@ -70,7 +70,8 @@ def test_duplicate_tensor_across_shards(tmp_path, rng):
         hip.Checkpoint(str(tmp_path))
 
 
-@pytest.mark.parametrize("corrupt", ["truncated", "not_json", "past_end", "reversed"])
+@pytest.mark.parametrize("corrupt", ["truncated", "not_json", "past_end", "reversed", "inflated",
+                                     "wrapping"])
 def test_bad_headers(tmp_path, rng, corrupt):
     h = layout.synth_quant(rng, 16, 256, 4)
     p = tmp_path / "model.safetensors"
@@ -86,8 +87,16 @@ def test_bad_headers(tmp_path, rng, corrupt):
         p.write_bytes(raw[:8] + hdr[:i] + b"!" + hdr[i + 1:] + raw[8 + n:])
     else:
         ent = header["a.weight"]
-        ent["data_offsets"] = ([0, 1 << 40] if corrupt == "past_end" else
-                               [ent["data_offsets"][1], ent["data_offsets"][0]])
+        a, b = ent["data_offsets"]
+        ent["data_offsets"] = {
+            "past_end": [0, 1 << 40],
+            "reversed": [b, a],
+            # inside the file but more bytes than the shape holds: a read would
+            # overrun a buffer sized from the shape
+            "inflated": [a, b + 8],
+            # b near 2^64: data + b wraps around to a small number
+            "wrapping": [a, (1 << 64) - 8],
+        }[corrupt]
         text = json.dumps(header).encode()
         text += b" " * (-len(text) % 8)
         p.write_bytes(struct.pack("<Q", len(text)) + text + raw[8 + n:])
@@ -114,6 +123,25 @@ def test_load_quant_shape_checks(tmp_path, rng):
             ck.load_quant("w", 64, 1024, 4, 0x1000, 0x2000, 0x3000)
         with pytest.raises(hip.MoltenError, match="missing v.scales"):
             ck.load_quant("v", 64, 512, 4, 0x1000, 0x2000, 0x3000)
+        with pytest.raises(hip.MoltenError, match="empty matrix"):
+            ck.load_quant("w", 64, 0, 4, 0x1000, 0x2000, 0x3000)
+        with pytest.raises(hip.MoltenError, match="unsupported bit width"):
+            ck.load_quant("w", 64, 512, 5, 0x1000, 0x2000, 0x3000)
+
+
+def test_load_quant_zero_group_scales(tmp_path, rng):
+    """A scales tensor whose last dimension is 0 and k = 0 are rejected
+    before any arithmetic divides by them."""
+    h = layout.synth_quant(rng, 64, 512, 4)
+    _write_quant(tmp_path / "model.safetensors", "w", h,
+                 {"z.weight": np.zeros((64, 0), np.uint32), "z.scales": np.zeros((64, 0), np.uint16),
+                  "z.biases": np.zeros((64, 0), np.uint16)})
+    with hip.Checkpoint(str(tmp_path)) as ck:
+        with pytest.raises(hip.MoltenError) as ei:
+            ck.load_quant("z", 64, 0, 4, 0x1000, 0x2000, 0x3000)
+        assert ei.value.code == hip.MH_ERR_INVALID
+        with pytest.raises(hip.MoltenError, match="no columns"):
+            ck.load_quant("z", 64, 512, 4, 0x1000, 0x2000, 0x3000)
 
 
 @pytest.mark.gpu
@@ -128,3 +156,31 @@ def test_load_quant_to_device_and_gemv(dev, bits):
     worker = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ckpt_worker.py")
     r = subprocess.run([sys.executable, worker, str(bits)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and r.stdout.startswith("OK"), r.stdout + r.stderr
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bits", [4, 6])
+def test_load_quant_in_torch_process(dev, tmp_path, rng, orc, bits):
+    """The same load in a process that also runs torch: one HIP runtime is
+    mapped (torch's, which the library binds to), and the staged reads, the
+    pinned staging buffers and their events work there too."""
+    import torch
+
+    from tests.devutil import dev_quant, empty_dev, from_dev, to_dev
+
+    assert len(hip.hip_runtimes()) == 1
+    h = layout.synth_quant(rng, 256, 2048, bits)
+    _write_quant(tmp_path / "model.safetensors", "w", h)
+    codes = torch.empty(h.codes.size, dtype=torch.int32, device=dev)
+    scales = torch.empty(h.scales.size, dtype=torch.int16, device=dev)
+    biases = torch.empty(h.biases.size, dtype=torch.int16, device=dev)
+    with hip.Checkpoint(str(tmp_path)) as ck:
+        w = ck.load_quant("w", 256, 2048, bits, codes, scales, biases)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_dev(codes, np.uint32).reshape(h.codes.shape), h.codes)
+    assert np.array_equal(from_dev(scales, np.uint16).reshape(h.scales.shape), h.scales)
+    assert np.array_equal(from_dev(biases, np.uint16).reshape(h.biases.shape), h.biases)
+    x = layout.synth_bf16(rng, (1, 2048))
+    y = empty_dev((1, 256), np.uint16)
+    hip.gemv_quant(w, to_dev(x), y, 1)
+    assert np.array_equal(from_dev(y, np.uint16), orc.gemv_quant(h, x, 1))

@@ -21,7 +21,7 @@ def _log(msg):
 
 def _mfma_path(n, k, batch, gs=64):
     """Shapes the batched matrix-core kernel takes (gemv_mfma.hip limits)."""
-    return 2 <= batch <= 8 and gs == 64 and k % 256 == 0 and k <= 2048 and n % 16 == 0
+    return 2 <= batch <= 8 and gs == 64 and k % 512 == 0 and k <= 2048 and n % 16 == 0
 
 
 def _bf16_ulp(v):
