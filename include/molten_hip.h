@@ -98,6 +98,16 @@ int mh_memcpy(void* dst, const void* src, size_t bytes, int kind, mh_stream_t st
  * inside graph capture). */
 int mh_zero(void* dst, size_t bytes, mh_stream_t stream);
 
+/* Device status word: kernels that wait on other workgroups bound every
+ * wait, and when one expires they finish with a defined result (token id
+ * 0xffffffff, NaN outputs) and set a bit here.  mh_status waits for `stream`,
+ * reads the current device's word into *status and, when `clear` != 0,
+ * resets it; the counterpart of the reference surfacing a failed command
+ * buffer at commit_wait (src/metal.rs:385-399).  Not for graph capture. */
+#define MH_STATUS_ARGMAX_WAIT 1u /* a head GEMV's argmax collector gave up  */
+#define MH_STATUS_DECODE_WAIT 2u /* the fused MoE decode step's exchange wait expired */
+int mh_status(uint32_t* status, int clear, mh_stream_t stream);
+
 /* ------------------------------------------------------ checkpoint ---
  * src/safetensors.rs:85-196 Checkpoint and src/lfm.rs:261-316 load_tensor /
  * load_quant: the MLX safetensors checkpoint, unchanged.  open() reads the
@@ -161,11 +171,16 @@ int mh_gemv_head_argmax(const mh_quant_weights* w, const uint16_t* x, uint64_t* 
  * the last-dispatched workgroup (every other one has started by then) collects
  * the slots, writes the token ids and re-zeroes the slots, so no two
  * workgroups contend on one atomic.  scratch: MH_ARGMAX_SCRATCH_WORDS(batch)
- * u64 words, zero on entry and left zero; calls that overlap on one scratch
- * buffer race.  No reference counterpart (BASELINE configs 2 and 5 store the
- * logits; molten's head stores none). */
+ * u64 words, zeroed before the first call; the slots are left zero and the
+ * last word counts the launches of the chunk-order kernels' finisher (their
+ * keys carry a tag of the count, so a key written late after an expired
+ * wait is never taken for a later launch's; the matrix-core path keeps no
+ * count); calls that overlap on one scratch buffer race.  When the
+ * collector's bounded wait expires the ids are 0xffffffff and
+ * MH_STATUS_ARGMAX_WAIT is set.  No reference counterpart (BASELINE configs
+ * 2 and 5 store the logits; molten's head stores none). */
 #define MH_ARGMAX_SLOTS 2048u
-#define MH_ARGMAX_SCRATCH_WORDS(batch) (MH_ARGMAX_SLOTS * (batch))
+#define MH_ARGMAX_SCRATCH_WORDS(batch) (MH_ARGMAX_SLOTS * (batch) + 1u)
 int mh_gemv_quant_argmax(const mh_quant_weights* w, const uint16_t* x, uint16_t* y,
                          uint64_t* scratch, uint32_t* ids, uint32_t batch, mh_stream_t stream);
 

@@ -35,6 +35,8 @@ struct GemvArgs {
     unsigned long long* best;   // [batch] keys (reference head argmax), or null
     unsigned long long* slots;  // [batch][kArgSlots] finisher scratch, or null
     uint32_t* ids;              // [batch] tokens written by the finisher
+    unsigned long long* launches;  // the finisher's launch count (after the slots), or null
+    uint32_t* status;           // device status word (MH_STATUS_*), or null
     uint32_t n, k, gs, row_words, groups;
 };
 
@@ -57,23 +59,51 @@ __device__ __forceinline__ void amax_if_greater(unsigned long long* p, unsigned 
 // slots, so no two units contend on one address.  The last workgroup of the
 // grid is dispatched after all others have started, so its wait for their
 // slots ends; it reduces the slots with its own units' keys, writes the token
-// ids and re-zeroes the slots.  Keys are never zero (the orderable value of
-// any non-NaN float, -inf included, is nonzero), so zero marks an empty slot.
-__device__ __forceinline__ void publish_key(const GemvArgs& a, uint32_t b, uint32_t unit,
+// ids, re-zeroes the slots and counts the launch.
+//
+// A slot holds the unit's key for this launch as a 48-bit key (the bf16
+// logit's 16-bit orderable value above ~index: the argmax runs over bf16
+// values, whose orderable f32 word has a constant low half) under a 16-bit
+// tag derived from the launch count (the scratch word after the slots, read
+// at kernel start and bumped by the collector at its end).  The collector
+// accepts only slots that carry this launch's tag, so a key that a unit of an
+// earlier launch wrote late (after that launch's collector gave up waiting)
+// is never taken for a later launch's, and a zero slot (tag 0) is never a
+// key.
+__device__ __forceinline__ unsigned long long launch_tag(unsigned long long launches) {
+    return (launches % 0xffffull + 1ull) << 48;
+}
+
+__device__ __forceinline__ unsigned long long key48(unsigned long long key64) {
+    return ((key64 >> 48) << 32) | (key64 & 0xffffffffull);
+}
+
+constexpr unsigned long long kTagMask = 0xffff000000000000ull;
+
+__device__ __forceinline__ void publish_key(const GemvArgs& a, uint32_t b, uint32_t unit, unsigned long long tag,
                                             unsigned long long key) {
-    __hip_atomic_store(a.slots + static_cast<size_t>(b) * kArgSlots + unit, key, __ATOMIC_RELAXED,
+    __hip_atomic_store(a.slots + static_cast<size_t>(b) * kArgSlots + unit, tag | key48(key), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The launch count, read at kernel start by every workgroup of a finisher
+// launch (the collector only bumps it after every unit has published).
+__device__ __forceinline__ unsigned long long read_launches(const GemvArgs& a) {
+    return a.launches != nullptr ? __hip_atomic_load(a.launches, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+}
+
 // Run by the whole collector workgroup.  own[b]: the collector's own key.
-// Each thread reads its slots together; the ones still empty (their unit has
-// not published yet) are read again together until they fill.
+// Each thread reads its slots together; the ones without this launch's tag
+// (their unit has not published yet) are read again together until they
+// carry it.
 template <int B>
-__device__ void collect_keys(const GemvArgs& a, uint32_t n_units, const unsigned long long* own) {
+__device__ void collect_keys(const GemvArgs& a, uint32_t n_units, const unsigned long long* own,
+                             unsigned long long launches) {
     __shared__ unsigned long long sk[kWaves];
     constexpr int kPer = kArgSlots / kThreads;  // slots per collector thread
     static_assert(kPer <= 32, "pending mask is 32 bits");
     const int lane = threadIdx.x & (mh::kWave - 1), wave = threadIdx.x / mh::kWave;
+    const unsigned long long tag = launch_tag(launches);
     for (int b = 0; b < B; ++b) {
         unsigned long long* sl = a.slots + static_cast<size_t>(b) * kArgSlots + threadIdx.x;
         unsigned long long v[kPer];
@@ -81,8 +111,8 @@ __device__ void collect_keys(const GemvArgs& a, uint32_t n_units, const unsigned
 #pragma unroll
         for (int j = 0; j < kPer; ++j) {
             const bool mine = threadIdx.x + j * kThreads < n_units;
-            v[j] = mine ? __hip_atomic_load(sl + j * kThreads, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1ull;
-            pend |= (v[j] == 0ull ? 1u : 0u) << j;
+            v[j] = mine ? __hip_atomic_load(sl + j * kThreads, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : tag;
+            pend |= ((v[j] & kTagMask) != tag ? 1u : 0u) << j;
         }
         uint32_t spins = 0;
         while (pend != 0u && ++spins < kSpinLimit) {
@@ -95,7 +125,7 @@ __device__ void collect_keys(const GemvArgs& a, uint32_t n_units, const unsigned
             }
 #pragma unroll
             for (int j = 0; j < kPer; ++j) {
-                if (v[j] != 0ull) {
+                if ((v[j] & kTagMask) == tag) {
                     pend &= ~(1u << j);
                 }
             }
@@ -105,25 +135,32 @@ __device__ void collect_keys(const GemvArgs& a, uint32_t n_units, const unsigned
 #pragma unroll
         for (int j = 0; j < kPer; ++j) {
             if (threadIdx.x + j * kThreads < n_units) {
-                m = v[j] > m ? v[j] : m;
+                const unsigned long long k = (v[j] & kTagMask) == tag ? v[j] & ~kTagMask : 0ull;
+                m = k > m ? k : m;
                 __hip_atomic_store(sl + j * kThreads, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
         m = mh::wave_max_u64(m);
         const bool any_lost = __syncthreads_or(lost) != 0;
+        if (any_lost && threadIdx.x == 0 && a.status != nullptr) {
+            __hip_atomic_fetch_or(a.status, MH_STATUS_ARGMAX_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         if (lane == 0) {
             sk[wave] = m;
         }
         __syncthreads();
         // wave 0: the waves' maxima and the collector's own key
         if (wave == 0) {
-            const unsigned long long t =
-                mh::wave_max_u64(lane < kWaves ? sk[lane < kWaves ? lane : 0] : (lane == kWaves ? own[b] : 0ull));
+            const unsigned long long t = mh::wave_max_u64(
+                lane < kWaves ? sk[lane < kWaves ? lane : 0] : (lane == kWaves ? key48(own[b]) : 0ull));
             if (lane == 0) {
                 a.ids[b] = any_lost ? 0xffffffffu : ~static_cast<uint32_t>(t & 0xffffffffull);
             }
         }
         __syncthreads();
+    }
+    if (threadIdx.x == 0 && a.launches != nullptr) {
+        __hip_atomic_store(a.launches, launches + 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -132,7 +169,7 @@ __device__ void collect_keys(const GemvArgs& a, uint32_t n_units, const unsigned
 // gemv_head_argmax) or the finisher's slots.
 template <int B>
 __device__ void finish_argmax(const GemvArgs& a, const float (&bv)[B], const uint32_t (&bi)[B],
-                              int lane, int wave) {
+                              int lane, int wave, unsigned long long launches) {
     __shared__ float sv[kWaves][B];
     __shared__ uint32_t si[kWaves][B];
     __shared__ unsigned long long own[B];
@@ -163,7 +200,7 @@ __device__ void finish_argmax(const GemvArgs& a, const float (&bv)[B], const uin
     const uint32_t last = gridDim.x - 1;
     if (blockIdx.x != last) {
         if (threadIdx.x < B) {
-            publish_key(a, threadIdx.x, blockIdx.x, key);
+            publish_key(a, threadIdx.x, blockIdx.x, launch_tag(launches), key);
         }
         return;
     }
@@ -171,7 +208,7 @@ __device__ void finish_argmax(const GemvArgs& a, const float (&bv)[B], const uin
         own[threadIdx.x] = key;
     }
     __syncthreads();
-    collect_keys<B>(a, last, own);
+    collect_keys<B>(a, last, own, launches);
 }
 
 // Key of the wave's argmax over per-lane bests (bv, bi) kept by argmax_merge:
@@ -214,6 +251,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
     const uint32_t G = FAST ? 32u : a.groups;
     const bool live = FAST || lane < static_cast<int>(C);
     const uint32_t c = live ? lane : 0u;
+    const unsigned long long launches = ARGMAX ? read_launches(a) : 0ull;
 
     // x is converted after the first block's loads are issued
     uint32_t xw[16];
@@ -315,7 +353,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
             if (a.slots == nullptr) {
                 amax_if_greater(a.best, t);
             } else if (blockIdx.x != last) {
-                publish_key(a, 0, blockIdx.x, t);
+                publish_key(a, 0, blockIdx.x, launch_tag(launches), t);
             } else {
                 own[0] = t;
             }
@@ -325,7 +363,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
         return;
     }
     __syncthreads();
-    collect_keys<1>(a, last, own);
+    collect_keys<1>(a, last, own, launches);
 }
 
 // Row values (wave-uniform) of one row group of the staged kernel: store and
@@ -375,6 +413,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_staged(GemvArgs a) {
     const uint32_t N = a.n;
     float* xl = lds;                                          // [B*C][kXPitch]
     float* xsl = lds + static_cast<size_t>(B) * C * kXPitch;  // [B*C]
+    const unsigned long long launches = read_launches(a);
 
     for (uint32_t t = threadIdx.x; t < B * C; t += kThreads) {
         const uint32_t b = t / C, c = t % C;
@@ -450,7 +489,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_staged(GemvArgs a) {
         emit_rows<B, R>(a, rg, v, bv, bi, lane);
     }
     if (a.best != nullptr || a.slots != nullptr) {
-        finish_argmax<B>(a, bv, bi, lane, wave);
+        finish_argmax<B>(a, bv, bi, lane, wave, launches);
     }
 }
 
@@ -619,6 +658,9 @@ int gemv_common(const char* op, const mh_quant_weights* w, const uint16_t* x, ui
     a.gs = w->group_size;
     a.row_words = w->in_features * w->bits / 32u;
     a.groups = w->in_features / w->group_size;
+    a.launches = finisher ? reinterpret_cast<unsigned long long*>(best) + static_cast<size_t>(batch) * kArgSlots
+                          : nullptr;
+    a.status = mh::status_word();
     const hipStream_t s = mh::as_stream(stream);
     // batch > 1 without the reference's atomic-max key: the matrix-core
     // kernel where its shape limits allow

@@ -55,6 +55,7 @@ struct MfmaArgs {
     uint16_t* y;                // [batch, N] bf16, or null
     unsigned long long* slots;  // [batch][kArgSlots] finisher scratch, or null (no argmax)
     uint32_t* ids;              // [batch]
+    uint32_t* status;           // device status word (MH_STATUS_*), or null
     uint32_t n, k, groups, row_bytes;
 };
 
@@ -619,6 +620,9 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
     }
     if (lane == 0) {
         a.ids[b] = lost ? 0xffffffffu : id;
+        if (lost && a.status != nullptr) {
+            __hip_atomic_fetch_or(a.status, MH_STATUS_ARGMAX_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
     // clear the words for the next launch (last: no later load waits on them)
 #pragma unroll
@@ -675,6 +679,7 @@ int gemv_mfma(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint64_
     a.k = K;
     a.groups = K / 64u;
     a.row_bytes = K * w->bits / 8u;
+    a.status = mh::status_word();
     return w->bits == 4 ? dispatch<4>(a, batch, stream) : dispatch<6>(a, batch, stream);
 }
 

@@ -25,6 +25,11 @@ int hip_error(hipError_t e, const char* what);
 // Number of compute units of the current device (cached per device).
 int cu_count();
 
+// The current device's status word (MH_STATUS_* bits; kernels set bits with
+// a device-scope atomic or when a bounded wait expires), or NULL when it
+// cannot be resolved.  Cached per device after the first call.
+uint32_t* status_word();
+
 inline hipStream_t as_stream(mh_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline bool aligned(const void* p, uintptr_t a) {

@@ -15,7 +15,39 @@ thread_local std::string g_last_error;
 
 constexpr int kMaxDevices = 64;
 std::atomic<int> g_cu_count[kMaxDevices];
+
+// The device status word (MH_STATUS_* bits, set by kernels whose bounded
+// waits expire).  Each device holds its own copy; host code uses the address
+// hipGetSymbolAddress returns for the current device, never the name.
+__device__ __align__(256) uint32_t g_status[64];
+std::atomic<uint32_t*> g_status_ptr[kMaxDevices];
 }  // namespace
+
+int current_device() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        return -1;
+    }
+    return dev;
+}
+
+uint32_t* status_word() {
+    const int dev = current_device();
+    if (dev < 0) {
+        return nullptr;
+    }
+    uint32_t* p = g_status_ptr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        void* q = nullptr;
+        if (hipGetSymbolAddress(&q, HIP_SYMBOL(g_status)) != hipSuccess || q == nullptr) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        p = static_cast<uint32_t*>(q);
+        g_status_ptr[dev].store(p, std::memory_order_release);
+    }
+    return p;
+}
 
 int set_error(int code, const char* fmt, ...) {
     char buf[512];
@@ -173,6 +205,24 @@ int mh_memcpy(void* dst, const void* src, size_t bytes, int kind, mh_stream_t st
         e = hipStreamSynchronize(mh::as_stream(stream));
     }
     return e == hipSuccess ? MH_OK : mh::hip_error(e, "hipMemcpyAsync");
+}
+
+int mh_status(uint32_t* status, int clear, mh_stream_t stream) {
+    MH_ENSURE(status != nullptr, MH_ERR_INVALID, "mh_status: status is NULL");
+    uint32_t* w = mh::status_word();
+    MH_ENSURE(w != nullptr, MH_ERR_RUNTIME, "mh_status: no device status word on this device");
+    const hipStream_t s = mh::as_stream(stream);
+    hipError_t e = hipMemcpyAsync(status, w, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) {
+        e = hipStreamSynchronize(s);
+    }
+    if (e == hipSuccess && clear && *status != 0u) {
+        e = hipMemsetAsync(w, 0, sizeof(uint32_t), s);
+        if (e == hipSuccess) {
+            e = hipStreamSynchronize(s);
+        }
+    }
+    return e == hipSuccess ? MH_OK : mh::hip_error(e, "mh_status");
 }
 
 int mh_zero(void* dst, size_t bytes, mh_stream_t stream) {

@@ -78,6 +78,7 @@ _SIGNATURES = {
     "mh_free": [_vp],
     "mh_memcpy": [_vp, _vp, _sz, _i32, _vp],
     "mh_zero": [_vp, _sz, _vp],
+    "mh_status": [ctypes.POINTER(_u32), _i32, _vp],
     "mh_dequant_to_bf16": [_qw, _vp, _vp],
     "mh_dequant_q4_bf16_bulk": [_qw, _vp, _vp],
     "mh_gemv_quant": [_qw, _vp, _vp, _u32, _vp],
@@ -211,6 +212,18 @@ def _stream(stream) -> Optional[int]:
     return None
 
 
+STATUS_ARGMAX_WAIT = 1
+STATUS_DECODE_WAIT = 2
+
+
+def device_status(clear: bool = True, stream=None) -> int:
+    """The device status word (MH_STATUS_* bits): waits for the stream, reads
+    the word and (clear) resets it."""
+    v = _u32()
+    check(load().mh_status(ctypes.byref(v), 1 if clear else 0, _stream(stream)), "status")
+    return v.value
+
+
 def check(rc: int, op: str) -> None:
     if rc != MH_OK:
         msg = load().mh_last_error().decode(errors="replace")
@@ -275,7 +288,7 @@ MOE_DECODE_SCRATCH_WORDS = 10240  # MH_MOE_DECODE_SCRATCH_WORDS
 
 def argmax_scratch_words(batch: int) -> int:
     """MH_ARGMAX_SCRATCH_WORDS(batch): u64 words of gemv_quant_argmax scratch."""
-    return ARGMAX_SLOTS * batch
+    return ARGMAX_SLOTS * batch + 1
 
 
 def gemv_quant_argmax(w: QuantWeights, x, y, scratch, ids, batch: int = 1, stream=None) -> None:

@@ -30,6 +30,15 @@ def _bf16_ulp(v):
     return 2.0 ** (e - 7)
 
 
+def assert_scratch(scratch, n, k, batch, launches):
+    """The finisher's slots are left zero; the last word counts the
+    chunk-order kernels' finisher launches (the matrix-core kernel's
+    finisher keeps no count)."""
+    sc = from_dev(scratch, np.uint64)
+    assert not sc[:-1].any()
+    assert int(sc[-1]) == (0 if _mfma_path(n, k, batch) else launches)
+
+
 def assert_logits(got, want, n, k, batch, gs=64):
     if not _mfma_path(n, k, batch, gs):
         np.testing.assert_array_equal(got, want)
@@ -130,10 +139,10 @@ def test_argmax_paths_agree_with_oracle(dev, orc, bits, batch):
     y = empty_dev((batch, n), np.uint16)
     scratch = zeros_dev((hip.argmax_scratch_words(batch),), np.uint64)
     ids = empty_dev((batch,), np.uint32)
-    for _ in range(3):
+    for call in range(3):
         hip.gemv_quant_argmax(w, xd, y, scratch, ids, batch)
         assert from_dev(ids, np.uint32).tolist() == want
-        assert not from_dev(scratch, np.uint64).any()
+        assert_scratch(scratch, n, k, batch, call + 1)
     assert_logits(from_dev(y, np.uint16), logits, n, k, batch)
     # (2) reference pair: head argmax (no logits) + token tail
     best = zeros_dev((batch,), np.uint64)
@@ -170,19 +179,50 @@ def test_lm_head_argmax_graph_replays(dev, orc):
             hip.gemv_quant_argmax(w, xd, y, scratch, i, 1)
     other_y = empty_dev((1, n), np.uint16)
     other_id = empty_dev((1,), np.uint32)
+    launches = 3  # the eager warm-up calls (capture runs nothing)
     for rep in range(4):
         for y, i in zip(ys, ids):
             y.zero_()
             i.zero_()
         graph.replay()
         torch.cuda.synchronize()
+        launches += 3
         for c in range(3):
             np.testing.assert_array_equal(from_dev(ys[c], np.uint16), want[c])
             assert int(from_dev(ids[c], np.uint32)[0]) == want_ids[c]
-        assert not from_dev(scratch, np.uint64).any()
+        assert_scratch(scratch, n, k, 1, launches)
+        launches += 1
         hip.gemv_quant_argmax(devw[rep % 3][0], xd, other_y, scratch, other_id, 1)  # eager, same scratch
         torch.cuda.synchronize()
         assert int(from_dev(other_id, np.uint32)[0]) == want_ids[rep % 3]
+
+
+def test_argmax_ignores_keys_of_earlier_launches(dev, orc):
+    """A key that a late unit of an earlier launch left in its slot (planted
+    here from the host: the largest possible key, tagged with the previous
+    launch's tag) is never taken for this launch's: the ids stay the
+    oracle's, the slot is re-zeroed and no wait expired."""
+    rng = np.random.default_rng(4242)
+    n, k = 8192, 2048
+    h = layout.synth_quant(rng, n, k, 4)
+    x = layout.synth_bf16(rng, (1, k))
+    want = orc.argmax_bf16(orc.gemv_quant(h, x, 1)[0])
+    w, keep = dev_quant(h)
+    xd = to_dev(x)
+    scratch = zeros_dev((hip.argmax_scratch_words(1),), np.uint64)
+    ids = empty_dev((1,), np.uint32)
+    hip.device_status(clear=True)
+    for launch in range(3):
+        sc = from_dev(scratch, np.uint64).copy()
+        assert int(sc[-1]) == launch
+        if launch > 0:
+            stale_tag = (launch - 1) % 0xFFFF + 1
+            sc[5] = np.uint64((stale_tag << 48) | 0xFFFFFFFFFFFF)
+            scratch.copy_(to_dev(sc))
+        hip.gemv_quant_argmax(w, xd, None, scratch, ids, 1)
+        assert int(from_dev(ids, np.uint32)[0]) == want
+        assert_scratch(scratch, n, k, 1, launch + 1)
+    assert hip.device_status(clear=True) == 0
 
 
 def test_argmax_ties_take_lowest_index(dev, orc):
@@ -259,10 +299,10 @@ def _argmax_case(dev, orc, h, x, batch):
     y = empty_dev((batch, h.n), np.uint16)
     scratch = zeros_dev((hip.argmax_scratch_words(batch),), np.uint64)
     ids = empty_dev((batch,), np.uint32)
-    for _ in range(2):
+    for call in range(2):
         hip.gemv_quant_argmax(w, to_dev(x), y, scratch, ids, batch)
         assert from_dev(ids, np.uint32).tolist() == want
-        assert not from_dev(scratch, np.uint64).any()
+        assert_scratch(scratch, h.n, h.k, batch, call + 1)
     assert_logits(from_dev(y, np.uint16), logits, h.n, h.k, batch)
     return want
 
