@@ -184,6 +184,20 @@ int mh_gemv_head_argmax(const mh_quant_weights* w, const uint16_t* x, uint64_t* 
 int mh_gemv_quant_argmax(const mh_quant_weights* w, const uint16_t* x, uint16_t* y,
                          uint64_t* scratch, uint32_t* ids, uint32_t batch, mh_stream_t stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): mh_gemv_quant_argmax with its finisher scratch held by
+ * the library in a file-scope device array of MH_ARGMAX_SCRATCH_WORDS(8) u64
+ * words (128 KiB + 8 B on each device it runs on, held until the process
+ * ends), resolved and zeroed on the first call on each device.  batch must
+ * be 1..8 (the array's size; larger is MH_ERR_INVALID).  The caller passes
+ * the weights, x, y (may be NULL) and ids as for mh_gemv_quant_argmax;
+ * nothing is allocated.  Every call on a device shares that device's array
+ * and keeps it in the state the kernels leave (slots zero, a launch count):
+ * calls that overlap on one device race, so issue them on one stream. */
+int mh_gemv_quant_argmax_noalloc(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint32_t* ids,
+                                 uint32_t batch, mh_stream_t stream);
+
 /* src/kernels/lfm.rs:155-218 proj3_gemv_scatter (lfm.metal:1023-1067): the
  * Q, K and V projections of one x in one launch; q_out[NQ], k_out[NK] bf16,
  * V row j written to v_cache[((j / 64) * max_seq + pos) * 64 + j % 64]

@@ -10,6 +10,8 @@
 //
 // Replaces lfm.metal:100-297 (GEMV_Q4_BODY, lfm_gemv_q4_bf16[_k*],
 // lfm_gemv_q6_bf16[_x4]) and :1113-1386 (argmax, head argmax, token tail).
+#include <mutex>
+
 #include "mh_device.hpp"
 #include "mh_host.hpp"
 
@@ -791,9 +793,61 @@ __global__ __launch_bounds__(256) void k_argmax_final(const ArgPair* partials, u
     }
 }
 
+// ------------------------------------------------------ no-alloc head ---
+// The finisher scratch of mh_gemv_quant_argmax_noalloc: one array per device
+// (each device holds its own copy until the process ends).  Host code never
+// uses this name as an address: it uses the pointer hipGetSymbolAddress
+// returns for the current device (the name is a host-side stand-in).
+constexpr uint32_t kNoAllocMaxBatch = 8;
+static __device__ __align__(256) unsigned long long scratch[MH_ARGMAX_SCRATCH_WORDS(kNoAllocMaxBatch)];
+
+constexpr int kNoAllocDevices = 64;
+std::mutex g_noalloc_mu;
+unsigned long long* g_noalloc_ptr[kNoAllocDevices];  // per device, under g_noalloc_mu
+
+// The current device's scratch address; on the first call on a device it is
+// resolved and zeroed (a fill kernel on `stream`, ordered before the call's
+// own launch).  Nothing is allocated.
+int noalloc_scratch(unsigned long long** out, mh_stream_t stream) {
+    int dev = 0;
+    const hipError_t ge = hipGetDevice(&dev);
+    if (ge != hipSuccess) {
+        return mh::hip_error(ge, "hipGetDevice");
+    }
+    MH_ENSURE(dev >= 0 && dev < kNoAllocDevices, MH_ERR_UNSUPPORTED,
+              "mh_gemv_quant_argmax_noalloc: device %d beyond the %d this library tracks", dev, kNoAllocDevices);
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (g_noalloc_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) {
+            return mh::hip_error(e, "hipGetSymbolAddress(scratch)");
+        }
+        MH_ENSURE(p != nullptr, MH_ERR_RUNTIME, "hipGetSymbolAddress(scratch) returned NULL");
+        MH_TRY(mh_zero(p, sizeof(scratch), stream));
+        g_noalloc_ptr[dev] = static_cast<unsigned long long*>(p);
+    }
+    *out = g_noalloc_ptr[dev];
+    return MH_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int mh_gemv_quant_argmax_noalloc(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint32_t* ids,
+                                 uint32_t batch, mh_stream_t stream) {
+    MH_ENSURE(ids != nullptr, MH_ERR_INVALID, "mh_gemv_quant_argmax_noalloc: ids is NULL");
+    MH_ENSURE(batch >= 1 && batch <= kNoAllocMaxBatch, MH_ERR_INVALID,
+              "mh_gemv_quant_argmax_noalloc: batch %u exceeds the library's scratch (batch 1..%u)", batch,
+              kNoAllocMaxBatch);
+    MH_TRY(mh::check_quant(w, "mh_gemv_quant_argmax_noalloc"));
+    MH_ENSURE(x != nullptr, MH_ERR_INVALID, "mh_gemv_quant_argmax_noalloc: x is NULL");
+    unsigned long long* ws = nullptr;
+    MH_TRY(noalloc_scratch(&ws, stream));
+    return gemv_common("mh_gemv_quant_argmax_noalloc", w, x, y, reinterpret_cast<uint64_t*>(ws), true, ids, batch,
+                       stream);
+}
 
 int mh_gemv_quant(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint32_t batch,
                   mh_stream_t stream) {

@@ -84,6 +84,7 @@ _SIGNATURES = {
     "mh_gemv_quant": [_qw, _vp, _vp, _u32, _vp],
     "mh_gemv_head_argmax": [_qw, _vp, _vp, _u32, _vp],
     "mh_gemv_quant_argmax": [_qw, _vp, _vp, _vp, _vp, _u32, _vp],
+    "mh_gemv_quant_argmax_noalloc": [_qw, _vp, _vp, _vp, _u32, _vp],
     "mh_proj3_gemv_scatter": [_qw, _qw, _qw, _vp, _vp, _vp, _vp, _u32, _u32, _vp],
     "mh_conv3_gemv": [_qw, _vp, _vp, _vp, _vp, _vp, _vp],
     "mh_token_tail": [_vp, _vp, _u32, _vp],
@@ -270,6 +271,13 @@ def dequant_q4_bf16_bulk(w: QuantWeights, out, stream=None) -> None:
 
 
 # ------------------------------------------------------------------ GEMVs --
+
+def gemv_quant_argmax_noalloc(w: "QuantWeights", x, y, ids, batch: int = 1, stream=None) -> None:
+    """gemv_quant_argmax with the library's own per-device finisher scratch
+    (no device memory is allocated; batch 1..8)."""
+    check(load().mh_gemv_quant_argmax_noalloc(_qref(w), _ptr(x), _ptr(y), _ptr(ids), batch, _stream(stream)),
+          "gemv_quant_argmax_noalloc")
+
 
 def gemv_quant(w: QuantWeights, x, y, batch: int = 1, stream=None) -> None:
     """src/kernels/lfm.rs:112 (batch > 1 is this build's extension)."""
