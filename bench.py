@@ -208,6 +208,17 @@ def bench_next_rows(torch, hip, dev, gen, steps, warmup):
         pc = torch.empty((4096, n), dtype=torch.int16, device=dev)
         ms_x.append(timed(torch, lambda i: hip.gemm_q4_dense(pa, 4096, pw[i % 4][0], pc), steps, warmup))
         del pw, pc
+    # the unfused pair the reference's project() runs for weights the fused
+    # path does not take: a dense bf16 GEMM over an already dequantized W,
+    # and the generic quantized GEMM (dequantize into scratch + that GEMM)
+    pb = [bf16_randn(torch, (2048, 2048), dev, gen, std=0.05) for _ in range(4)]
+    pc = torch.empty((4096, 2048), dtype=torch.int16, device=dev)
+    ms_x.append(timed(torch, lambda i: hip.gemm_bf16_nt(pa, pb[i % 4], pc, 4096, 2048, 2048), steps, warmup))
+    pw = make_quant(torch, 2048, 2048, 4, 4, dev, gen)
+    scr = torch.empty(2048 * 2048, dtype=torch.int16, device=dev)
+    ms_x.append(timed(torch, lambda i: hip.gemm_quant_bf16_nt(pa, 4096, pw[i % 4][0], pc, scr, 2048 * 2048),
+                      steps, warmup))
+    del pb, pc, pw, scr
     return ms_p, ms_c, ms_d, ms_g, ms_t, ms_x, ms_s
 
 
@@ -502,9 +513,11 @@ def main() -> int:
             ms_per_step=round(ms1, 5), frac_of_hbm_peak=round(BYTES["config1"] / (ms1 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
         log("next rows: proj3, conv3, dense down K=11776, Q6 gather, token tail, Gumbel draw, dense prefill")
         ms_p, ms_c, ms_d, ms_g, ms_t, ms_x, ms_s = bench_next_rows(torch, hip, dev, gen, steps, warmup)
-        for n, ms in zip((2048, 11776), ms_x):
+        for key, n, ms in zip(("next_dense_prefill_q4_4096x2048x2048", "next_dense_prefill_q4_4096x11776x2048",
+                               "next_gemm_bf16_nt_4096x2048x2048", "next_gemm_quant_bf16_nt_q4_4096x2048x2048"),
+                              (2048, 11776, 2048, 2048), ms_x):
             tf = 2.0 * 4096 * n * 2048 / (ms * 1e-3) / 1e12
-            others[f"next_dense_prefill_q4_4096x{n}x2048"] = dict(
+            others[key] = dict(
                 value=round(tf, 1), unit="TFLOP/s", ms_per_step=round(ms, 5),
                 frac_of_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4))
         for key, ms in (("next_proj3_gemv_scatter", ms_p), ("next_conv3_gemv", ms_c),

@@ -140,7 +140,10 @@ int mh_load_quant(mh_checkpoint* ck, const char* base, uint32_t rows, uint32_t k
 
 /* ------------------------------------------------------ dequantize ---
  * src/kernels/quant.rs:69 dequant_to_bf16 and :95 dequant_q4_bf16_bulk:
- * out[r, j] = bf16(fma(scale, q, bias)), out bf16 [out, in]. */
+ * out[r, j] = bf16(fma(scale, q, bias)), out bf16 [out, in] (16-byte
+ * aligned).  dequant_to_bf16 takes 4-, 6- and 8-bit weights (the reference's
+ * check_quant, quant.rs:42-66, takes 4 and 8: dequant_q4_bf16 /
+ * dequant_q8_bf16, quant.metal:10-67); the bulk form 4-bit with K % 128 == 0. */
 int mh_dequant_to_bf16(const mh_quant_weights* w, uint16_t* out, mh_stream_t stream);
 int mh_dequant_q4_bf16_bulk(const mh_quant_weights* w, uint16_t* out, mh_stream_t stream);
 
@@ -393,6 +396,22 @@ int mh_moe_combine_rows(const uint16_t* sorted, const uint32_t* slotpos, const u
 int mh_gemm_q4_grouped(const uint16_t* a, const mh_quant_weights* w, uint16_t* c,
                        const uint32_t* blocks, uint32_t n_blocks, uint32_t s_rows, uint32_t n,
                        uint32_t bm, uint32_t bn, mh_stream_t stream);
+
+/* src/kernels/gemm.rs:33-60 gemm_bf16_nt (gemm.metal's gemm_bf16_nt_nax /
+ * _wide): C[M, N] = A[M, K] . B[N, K]^T, bf16 operands, f32 accumulation on
+ * the matrix cores (128 x 128 tiles), bf16 store (round to nearest even).
+ * Any M, N, K: K a multiple of 64 with 16-byte aligned A and B (each under
+ * 4 GiB) runs the tile kernel, other shapes a per-element kernel (f32 fma in
+ * ascending k).  M or N of 0 is a no-op. */
+int mh_gemm_bf16_nt(const uint16_t* a, const uint16_t* b, uint16_t* c, uint32_t m, uint32_t n, uint32_t k,
+                    mh_stream_t stream);
+
+/* src/kernels/quant.rs:126-146 gemm_quant_bf16_nt: W (4, 6 or 8 bits, [N,
+ * K]) dequantized into `scratch` (bf16, at least N * K elements, 16-byte
+ * aligned; the reference's error text when it is too small), then
+ * mh_gemm_bf16_nt(A [M, K], scratch, C [M, N]). */
+int mh_gemm_quant_bf16_nt(const uint16_t* a, uint32_t m, const mh_quant_weights* w, uint16_t* c, uint16_t* scratch,
+                          size_t scratch_elems, mh_stream_t stream);
 
 /* src/lfm.rs:661-671 project (prefill): dequant_q4_bf16_bulk + gemm_bf16_nt
  * fused: C[m, :] = A[m, :] . dequant(W)^T for every row m < M, A bf16 [M, K]

@@ -705,7 +705,7 @@ __global__ __launch_bounds__(256) void k_dequant(const uint32_t* codes, const ui
 }
 
 int dequant_common(const char* op, const mh_quant_weights* w, uint16_t* out, mh_stream_t stream) {
-    MH_TRY(mh::check_quant(w, op));
+    MH_TRY(mh::check_quant_dequant(w, op));
     MH_ENSURE(out != nullptr, MH_ERR_INVALID, "%s: out is NULL", op);
     MH_ENSURE(mh::aligned(out, 16), MH_ERR_ALIGN, "%s: out not 16-byte aligned", op);
     const size_t total = static_cast<size_t>(w->out_features) * (w->in_features / 32u);
@@ -715,6 +715,9 @@ int dequant_common(const char* op, const mh_quant_weights* w, uint16_t* out, mh_
     const hipStream_t s = mh::as_stream(stream);
     if (w->bits == 4) {
         hipLaunchKernelGGL(k_dequant<4>, dim3(grid), dim3(256), 0, s, w->codes, w->scales,
+                           w->biases, out, w->out_features, w->in_features, w->group_size);
+    } else if (w->bits == 8) {
+        hipLaunchKernelGGL(k_dequant<8>, dim3(grid), dim3(256), 0, s, w->codes, w->scales,
                            w->biases, out, w->out_features, w->in_features, w->group_size);
     } else {
         hipLaunchKernelGGL(k_dequant<6>, dim3(grid), dim3(256), 0, s, w->codes, w->scales,

@@ -24,13 +24,27 @@
 
 #include "mh_device.hpp"
 #include "mh_host.hpp"
+#include "mh_mfma.hpp"
 
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+using mh::bf16x2_t;
+using mh::bf16x8_t;
+using mh::dma16;
+using mh::dma16s;
+using mh::dma4;
+using mh::f32x16_t;
+using mh::f32x2_t;
+using mh::glb_ptr;
+using mh::lgkm_wait;
+using mh::tie_regs;
+using mh::lds_ptr;
+using mh::lds_read16;
+using mh::lds_read16_at;
+using mh::lds_read4;
+using mh::lds_read4_at;
+using mh::pack_bf16;
+using mh::wait_vmcnt;
 
 constexpr int kBK = 64;
 
@@ -47,11 +61,6 @@ struct GemmArgs {
     uint32_t k, n, s_rows, a_rows, w_rows;
     uint32_t dense_bm;       // rows per entry of a dense product (k_seg)
 };
-
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-    const f32x2_t v = {lo, hi};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
-}
 
 // One Q4 word (8 codes, low nibble first) -> bf16(fma(s, q, b)) x 8.  High
 // nibbles are converted as 16q and scaled by s/16: the product is exactly
@@ -70,8 +79,6 @@ __device__ __forceinline__ bf16x8_t deq_word(uint32_t w, float s, float s16, flo
     return __builtin_bit_cast(bf16x8_t, u);
 }
 
-typedef __attribute__((address_space(3))) void* lds_ptr;
-
 // Workgroup -> block-map entry.  Entries come in groups of nt = n / bn (the
 // column tiles of one expert row tile, which read the same A rows); groups
 // are dealt round-robin to the 8 XCDs (workgroup i runs on XCD i % 8), so
@@ -87,71 +94,7 @@ inline uint32_t grid_for_map(uint32_t n_blocks, uint32_t nt) {
     const uint32_t unit = 8u * nt;
     return (n_blocks + unit - 1u) / unit * unit;
 }
-typedef const __attribute__((address_space(1))) void* glb_ptr;
-
 constexpr int kStages = 3;  // LDS ring depth: two K-blocks in flight while one is consumed
-
-// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-}
-
-// 16-byte LDS read issued without a wait: the caller waits with lds_wait.
-// (Written as asm so the compiler does not wait for every outstanding
-// direct-to-LDS load before it.)
-__device__ __forceinline__ uint4 lds_read16(uint32_t addr) {
-    uint4 v;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
-    return v;
-}
-
-// Direct-to-LDS 16-byte load: lane l's data lands at lds_base + 16 l.
-__device__ __forceinline__ void dma16(mh::gbytes src, uint32_t lds_base) {
-    __builtin_amdgcn_global_load_lds((glb_ptr)src, (lds_ptr)(uintptr_t)lds_base, 16, 0, 0);
-}
-// The same 16-byte load in the scalar-base form: base (uniform) + a 32-bit
-// per-lane offset, LDS destination lds_base (uniform) + 16 l.  M0 carries
-// the LDS address; it is saved and restored around the load, so the
-// compiler's own use of M0 is unaffected.  The compiler does not count this
-// load for its vmcnt waits (those can then only wait longer, never less);
-// the kernel waits for it explicitly.
-__device__ __forceinline__ void dma16s(mh::gbytes base, uint32_t voff, uint32_t lds_base) {
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %3\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, %2\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(voff), "s"(base), "s"(lds_base)
-        : "memory");
-}
-// Direct-to-LDS 4-byte load: lane l's dword lands at lds_base + 4 l.
-__device__ __forceinline__ void dma4(mh::gbytes src, uint32_t lds_base) {
-    __builtin_amdgcn_global_load_lds((glb_ptr)src, (lds_ptr)(uintptr_t)lds_base, 4, 0, 0);
-}
-__device__ __forceinline__ uint32_t lds_read4(uint32_t addr) {
-    uint32_t v;
-    asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
-    return v;
-}
-// The same reads with a constant byte offset in the instruction (no address add).
-template <int OFF>
-__device__ __forceinline__ uint4 lds_read16_at(uint32_t addr) {
-    static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
-    uint4 v;
-    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
-    return v;
-}
-template <int OFF>
-__device__ __forceinline__ uint32_t lds_read4_at(uint32_t addr) {
-    static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
-    uint32_t v;
-    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
-    return v;
-}
 
 // Tile of BM rows x (NW * NBW * 32) columns per matrix; NW waves, wave w owns
 // column blocks [w * NBW, (w + 1) * NBW) of every matrix and all BM rows.
@@ -311,7 +254,9 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void k_grouped(GemmArgs a
                 sw[t] = lds_read4(sbl);
                 bw[t] = lds_read4(sbl + 128u);
             }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            lgkm_wait<0>(bcode);
+            tie_regs(sw);
+            tie_regs(bw);
             const uint32_t half = (kb & 1u) ? 0u : 16u;  // bf16 of group kb in the high half
             float sf[NB], s16[NB], bf[NB];
 #pragma unroll
@@ -335,7 +280,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void k_grouped(GemmArgs a
                         av[rb] = lds_read16(base + rb * 4096u + aoff[j]);
                     }
                 }
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                lgkm_wait<0>(av);
 #pragma unroll
                 for (int rb = 0; rb < RB; ++rb) {
                     if (static_cast<uint32_t>(rb) < live_rb) {
@@ -408,31 +353,6 @@ __device__ __forceinline__ void static_for_impl(F&& f) {
 template <int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
     static_for_impl<0, N>(f);
-}
-
-// s_waitcnt lgkmcnt(N), tied to the registers it guards so that no use of
-// them can be scheduled above it.
-template <int N, int M>
-__device__ __forceinline__ void lgkm_wait(uint4 (&v)[M]) {
-    static_assert(N >= 0 && N <= 15, "lgkmcnt field");
-    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
-#pragma unroll
-    for (int i = 0; i < M; ++i) {
-        mh::u32x4 t = {v[i].x, v[i].y, v[i].z, v[i].w};
-        asm volatile("" : "+v"(t));
-        v[i] = make_uint4(t.x, t.y, t.z, t.w);
-    }
-}
-template <int N, int M>
-__device__ __forceinline__ void lgkm_wait(uint32_t (&v)[M]) {
-    static_assert(N >= 0 && N <= 15, "lgkmcnt field");
-    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
-#pragma unroll
-    for (int i = 0; i < M; ++i) {
-        auto t = v[i];
-        asm volatile("" : "+v"(t));
-        v[i] = t;
-    }
 }
 
 // Fast SiLU for the GEMM epilogue (the gate/up values it sees already

@@ -517,6 +517,16 @@ struct Chunk<6> {
     __device__ __forceinline__ float dot(const float* xr) const { return q6_chunk_dot(w, xr); }
 };
 
+template <>
+struct Chunk<8> {  // 32 byte codes in eight words (dequantization only)
+    uint32_t w[8];
+    __device__ __forceinline__ void load(const uint32_t* p) {  // 16-byte aligned
+        const uint4* q = reinterpret_cast<const uint4*>(p);
+        const uint4 a = q[0], b = q[1];
+        w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+    }
+};
+
 // A chunk's 32 codes dequantized to bf16 as bf16(fma(s, q, b)) (MLX
 // dequantize, quant_nax.metal:2908-2993), packed two per word in code order.
 template <int BITS>
@@ -527,6 +537,9 @@ __device__ __forceinline__ void dequant_chunk(const uint32_t* w, float s, float 
         if constexpr (BITS == 4) {
             q0 = (w[i >> 3] >> (4 * (i & 7))) & 15u;
             q1 = (w[(i + 1) >> 3] >> (4 * ((i + 1) & 7))) & 15u;
+        } else if constexpr (BITS == 8) {
+            q0 = (w[i >> 2] >> (8 * (i & 3))) & 255u;
+            q1 = (w[(i + 1) >> 2] >> (8 * ((i + 1) & 3))) & 255u;
         } else {
             const int b0 = 6 * i, b1 = 6 * (i + 1);
             q0 = ((b0 & 31) + 6 <= 32) ? (w[b0 >> 5] >> (b0 & 31)) & 63u

@@ -40,6 +40,9 @@ inline bool aligned(const void* p, uintptr_t a) {
 // bits in {4, 6}; group size a multiple of 32 that divides K (a 32-code chunk
 // never crosses a group); codes aligned for the vector loads.
 int check_quant(const mh_quant_weights* w, const char* op);
+// The same for the dequantizing operators, which also take 8-bit weights
+// (src/kernels/quant.rs:42-66 accepts bits 4 and 8; this build adds 6).
+int check_quant_dequant(const mh_quant_weights* w, const char* op);
 
 // Launch status after hipLaunchKernelGGL.
 // Internal launches of the prefill MoE step (moe_prefill.hip, moe_decode.hip).

@@ -101,6 +101,27 @@ int check_quant(const mh_quant_weights* w, const char* op) {
     return MH_OK;
 }
 
+int check_quant_dequant(const mh_quant_weights* w, const char* op) {
+    MH_ENSURE(w != nullptr, MH_ERR_INVALID, "%s: weights are NULL", op);
+    if (w->bits != 8u) {
+        return check_quant(w, op);
+    }
+    MH_ENSURE(w->codes && w->scales && w->biases, MH_ERR_INVALID,
+              "%s: codes/scales/biases must be non-NULL", op);
+    MH_ENSURE(w->out_features > 0 && w->in_features > 0, MH_ERR_INVALID,
+              "%s: empty weight matrix [%u, %u]", op, w->out_features, w->in_features);
+    MH_ENSURE(w->group_size >= 32 && w->group_size % 32 == 0, MH_ERR_UNSUPPORTED,
+              "%s: group size %u is not a multiple of 32", op, w->group_size);
+    MH_ENSURE(w->in_features % w->group_size == 0, MH_ERR_INVALID,
+              "%s: in_features %u not a multiple of the group size %u", op, w->in_features,
+              w->group_size);
+    MH_ENSURE(aligned(w->codes, 16), MH_ERR_ALIGN,
+              "%s: codes pointer not 16-byte aligned; the kernels read codes as vectors", op);
+    MH_ENSURE(aligned(w->scales, 2) && aligned(w->biases, 2), MH_ERR_ALIGN,
+              "%s: scales/biases not 2-byte aligned", op);
+    return MH_OK;
+}
+
 namespace {
 __global__ void k_zero(uint32_t* p, size_t words, uint8_t* tail, size_t tail_bytes) {
     const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;

@@ -97,6 +97,8 @@ _SIGNATURES = {
     "mh_checkpoint_read": [_vp, ctypes.c_char_p, _vp, _sz, _vp],
     "mh_load_quant": [_vp, ctypes.c_char_p, _u32, _u32, _u32, _vp, _vp, _vp, _qw, _vp],
     "mh_gemm_q4_dense": [_vp, _u32, _qw, _vp, _vp],
+    "mh_gemm_bf16_nt": [_vp, _vp, _vp, _u32, _u32, _u32, _vp],
+    "mh_gemm_quant_bf16_nt": [_vp, _u32, _qw, _vp, _vp, _sz, _vp],
     "mh_token_tail_embed": [_vp, _vp, _qw, _vp, _vp, _vp, _f32, _vp],
     "mh_gather_rows_q6": [_qw, _vp, _u32, _vp, _vp],
     "mh_argmax_bf16": [_vp, _u32, _vp, _vp, _vp],
@@ -384,6 +386,17 @@ def gather_rows_q6(table: QuantWeights, ids, m: int, out, stream=None) -> None:
 def gemm_q4_dense(a, m: int, w: QuantWeights, c, stream=None) -> None:
     """src/lfm.rs:661 (prefill dense projection: dequant + bf16 GEMM, fused)."""
     check(load().mh_gemm_q4_dense(_ptr(a), m, _qref(w), _ptr(c), _stream(stream)), "gemm_q4_dense")
+
+
+def gemm_bf16_nt(a, b, c, m: int, n: int, k: int, stream=None) -> None:
+    """src/kernels/gemm.rs:33: C[m, n] = A[m, k] . B[n, k]^T (bf16, f32 accumulation)."""
+    check(load().mh_gemm_bf16_nt(_ptr(a), _ptr(b), _ptr(c), m, n, k, _stream(stream)), "gemm_bf16_nt")
+
+
+def gemm_quant_bf16_nt(a, m: int, w: QuantWeights, c, scratch, scratch_elems: int, stream=None) -> None:
+    """src/kernels/quant.rs:126: W dequantized into scratch, then gemm_bf16_nt."""
+    check(load().mh_gemm_quant_bf16_nt(_ptr(a), m, _qref(w), _ptr(c), _ptr(scratch), scratch_elems,
+                                       _stream(stream)), "gemm_quant_bf16_nt")
 
 
 class SampleParams(ctypes.Structure):

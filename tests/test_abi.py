@@ -65,7 +65,7 @@ def _qw(**kw):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(bits=3), hip.MH_ERR_UNSUPPORTED),
-    (dict(bits=8), hip.MH_ERR_UNSUPPORTED),
+    (dict(bits=8), hip.MH_ERR_UNSUPPORTED),  # the GEMVs read 4- and 6-bit codes only
     (dict(group_size=48), hip.MH_ERR_UNSUPPORTED),
     (dict(in_features=2000), hip.MH_ERR_INVALID),
     (dict(out_features=0), hip.MH_ERR_INVALID),
@@ -170,6 +170,27 @@ def test_dense_gemm_arguments():
     with pytest.raises(hip.MoltenError) as ei:
         hip.gemm_q4_dense(0x4000, 0, _qw(), 0x5000, stream=0)
     assert ei.value.code == hip.MH_ERR_INVALID
+
+
+def test_bf16_and_quant_gemm_arguments():
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.gemm_bf16_nt(None, 0x5000, 0x6000, 4, 4, 64, stream=0)
+    assert ei.value.code == hip.MH_ERR_INVALID
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.gemm_bf16_nt(0x4001, 0x5000, 0x6000, 4, 4, 64, stream=0)
+    assert ei.value.code == hip.MH_ERR_ALIGN
+    hip.gemm_bf16_nt(0x4000, 0x5000, 0x6000, 0, 4, 64, stream=0)  # M = 0: nothing to do
+    with pytest.raises(hip.MoltenError, match="dequant scratch holds 100 bf16 elements, needs 131072"):
+        hip.gemm_quant_bf16_nt(0x4000, 8, _qw(), 0x6000, 0x7000, 100, stream=0)
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.gemm_quant_bf16_nt(0x4000, 8, _qw(bits=3), 0x6000, 0x7000, 1 << 20, stream=0)
+    assert ei.value.code == hip.MH_ERR_UNSUPPORTED
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.gemm_quant_bf16_nt(0x4000, 8, _qw(bits=8), 0x6000, 0x7008, 1 << 20, stream=0)
+    assert ei.value.code == hip.MH_ERR_ALIGN
+    with pytest.raises(hip.MoltenError) as ei:  # 8-bit codes are read 16 bytes at a time
+        hip.dequant_to_bf16(_qw(bits=8, codes=0x1008), 0x6000, stream=0)
+    assert ei.value.code == hip.MH_ERR_ALIGN
 
 
 def test_sample_arguments():
