@@ -251,6 +251,58 @@ def bench_config3(torch, hip, dev, gen, steps, warmup):
     return ms
 
 
+TIMELINE_PHASES = ("start", "logit_stored", "routed", "gate_up_issued", "first_act_published",
+                   "last_act_published", "down_issued", "acts_exchanged", "out_stored")
+
+
+def timeline_config3(torch, hip, dev, gen, launches):
+    """Config 3's decode step run `launches` times on the single-launch path
+    with per-wave phase timestamps (100 MHz clock), each launch separately
+    synchronized.  Per phase: the 10th / 50th / 90th percentile and the
+    maximum over the 2048 waves of (stamp - the launch's earliest start), in
+    us, each the median over launches; and the share of workgroups whose XCD
+    equals their index mod 8 (the round-robin dispatch the step assumes)."""
+    import numpy as np
+
+    E, H, I, topk = 64, 2048, 1536, 4
+    sets = [moe_set(torch, dev, gen) for _ in range(4)]
+    xs = [bf16_randn(torch, (H,), dev, gen) for _ in range(16)]
+    out = torch.empty(H, dtype=torch.int16, device=dev)
+    logits = torch.empty(E, dtype=torch.float32, device=dev)
+    ids = torch.empty(topk, dtype=torch.int32, device=dev)
+    wt = torch.empty(topk, dtype=torch.int16, device=dev)
+    act = torch.empty((topk, I), dtype=torch.int16, device=dev)
+    scratch = torch.zeros(hip.MOE_DECODE_SCRATCH_WORDS, dtype=torch.int32, device=dev)
+    nwaves = 256 * 8
+    stamps = torch.zeros(nwaves * hip.MOE_DECODE_STAMPS, dtype=torch.int64, device=dev)
+    per = []
+    xcc_ok = []
+    for i in range(launches + 3):
+        g, u, d, r = sets[i % len(sets)]
+        stamps.zero_()
+        hip.moe_decode_stamped(r, None, g[0], u[0], d[0], E, topk, xs[i % len(xs)], out, logits, ids, wt, act,
+                               scratch, stamps, mode=hip.ROUTE_SOFTMAX)
+        torch.cuda.synchronize()
+        if i < 3:
+            continue
+        st = stamps.cpu().numpy().reshape(nwaves, hip.MOE_DECODE_STAMPS)
+        t0 = st[:, 0].min()
+        rel = (st[:, :9].astype(np.float64) - t0) / 100.0  # 100 MHz ticks -> us
+        rows = []
+        for ph in range(9):
+            v = rel[:, ph][st[:, ph] != 0]
+            rows.append([float(np.percentile(v, 10)), float(np.percentile(v, 50)), float(np.percentile(v, 90)),
+                         float(v.max())] if v.size else [float("nan")] * 4)
+        per.append(rows)
+        wg_xcc = st[::8, 9]
+        xcc_ok.append(float(np.mean(wg_xcc == (np.arange(256) % 8))))
+    med = np.median(np.array(per), axis=0)
+    del sets
+    return {"phases_us_p10_p50_p90_max": {name: [round(x, 2) for x in med[i]]
+                                          for i, name in enumerate(TIMELINE_PHASES)},
+            "launches": launches, "xcd_round_robin_share": round(float(np.mean(xcc_ok)), 4)}
+
+
 def bench_config4(torch, hip, dev, gen, steps, warmup):
     E, H, I, topk, m = 64, 2048, 1536, 4, 4096
     sets = [moe_set(torch, dev, gen) for _ in range(2)]
@@ -471,6 +523,9 @@ def main() -> int:
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="also run a plain elementwise copy (f32 negate) of this many MiB "
                          "(PMC byte calibration)")
+    ap.add_argument("--timeline", type=int, default=0,
+                    help="only print the per-phase timeline of config 3's decode step over this many "
+                         "launches (device timestamps), then exit")
     ap.add_argument("--eager", action="store_true",
                     help="launch the timed steps directly instead of replaying a graph "
                          "(for counter collection; host launch overhead is then timed)")
@@ -492,6 +547,10 @@ def main() -> int:
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
     steps, warmup = args.steps, args.warmup
+    if args.timeline > 0:
+        print(json.dumps({"timeline": "config3_moe_decode_step",
+                          **timeline_config3(torch, hip, dev, gen, args.timeline)}), flush=True)
+        return 0
 
     log("config 2: Q4 LM head + argmax")
     ms2 = bench_lm_head(torch, hip, dev, gen, 4, 1, steps, warmup, copies=5)

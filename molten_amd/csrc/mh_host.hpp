@@ -55,7 +55,10 @@ int moe_decode_fused(const void* router, int router_dtype, const float* bias, in
                      const mh_quant_weights* gate, const mh_quant_weights* up,
                      const mh_quant_weights* down, uint32_t n_experts, uint32_t topk,
                      const uint16_t* x, uint16_t* out, float* logits, uint32_t* ids,
-                     uint16_t* weights, uint16_t* act, uint32_t* scratch, hipStream_t stream);
+                     uint16_t* weights, uint16_t* act, uint32_t* scratch, uint64_t* stamps, hipStream_t stream);
+// Workgroups x waves of the fused decode step (the stamp buffer holds
+// kGrid * kWaves * MH_MOE_DECODE_STAMPS words).
+uint32_t moe_decode_fused_waves();
 int gemv_mfma(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint64_t* slots, uint32_t* ids,
               uint32_t batch, hipStream_t stream);
 int router_prefill_route(const uint16_t* x, const void* w, int w_dtype, float* logits,

@@ -1024,7 +1024,7 @@ int mh_moe_decode(const void* router, int router_dtype, const float* bias, int m
     MH_TRY(down_common(op, down, act, ids, weights, out, topk, d_model, da));
     const hipStream_t s = mh::as_stream(stream);
     const int fused = mh::moe_decode_fused(router, router_dtype, bias, mode, eps, gate, up, down, n_experts,
-                                           topk, x, out, logits, ids, weights, act, scratch, s);
+                                           topk, x, out, logits, ids, weights, act, scratch, nullptr, s);
     if (fused != MH_ERR_UNSUPPORTED) {
         return fused;
     }
@@ -1058,6 +1058,34 @@ int mh_moe_decode(const void* router, int router_dtype, const float* bias, int m
     MH_TRY(rc);
     MH_TRY(launch_gather_act(aa, s));
     return launch_down(da, topk, s);
+}
+
+int mh_moe_decode_stamped(const void* router, int router_dtype, const float* bias, int mode, float eps,
+                          const mh_quant_weights* gate, const mh_quant_weights* up, const mh_quant_weights* down,
+                          uint32_t n_experts, uint32_t topk, const uint16_t* x, uint16_t* out, float* logits,
+                          uint32_t* ids, uint16_t* weights, uint16_t* act, uint32_t* scratch, uint64_t* stamps,
+                          mh_stream_t stream) {
+    const char* op = "mh_moe_decode_stamped";
+    MH_ENSURE(stamps != nullptr && mh::aligned(stamps, 8), MH_ERR_INVALID, "%s: stamps NULL or not 8-byte aligned",
+              op);
+    MH_ENSURE(gate && up && down && scratch, MH_ERR_INVALID, "%s: NULL argument", op);
+    MH_ENSURE(n_experts > 0 && gate->out_features % n_experts == 0 && down->out_features % n_experts == 0,
+              MH_ERR_INVALID, "%s: stacked rows not divisible by %u experts", op, n_experts);
+    const uint32_t n_inter = gate->out_features / n_experts;
+    const uint32_t d_model = down->out_features / n_experts;
+    MH_ENSURE(gate->in_features == d_model && down->in_features == n_inter, MH_ERR_INVALID,
+              "%s: gate / down do not chain", op);
+    DenseArgs ra;
+    MH_TRY(route_checks(op, logits, ids, weights, 1, n_experts, topk, mode));
+    MH_TRY(dense_common(op, router, router_dtype == MH_DTYPE_F32, x, logits, 1, n_experts, d_model, ra));
+    ActArgs aa;
+    MH_TRY(act_common(op, gate, up, x, ids, act, topk, n_inter, aa));
+    DownArgs da;
+    MH_TRY(down_common(op, down, act, ids, weights, out, topk, d_model, da));
+    const int rc = mh::moe_decode_fused(router, router_dtype, bias, mode, eps, gate, up, down, n_experts, topk, x,
+                                        out, logits, ids, weights, act, scratch, stamps, mh::as_stream(stream));
+    MH_ENSURE(rc != MH_ERR_UNSUPPORTED, MH_ERR_UNSUPPORTED, "%s: the shape runs as three launches (no timeline)", op);
+    return rc;
 }
 
 }  // extern "C"

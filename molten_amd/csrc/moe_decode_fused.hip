@@ -71,8 +71,37 @@ struct FusedArgs {
     uint16_t* act;         // [topk, NI]
     uint16_t* out;         // [K]
     uint32_t* scratch;     // launch counts, tagged logits, tagged activation triples
+    uint64_t* stamps;      // per wave kStamps words of phase timestamps (STAMPS kernels only)
     uint32_t E, K, NI, gs;
 };
+
+// Phase timestamps (the 100 MHz constant clock) of one launch, written by
+// lane 0 of every wave in the STAMPS instantiation only (the product
+// instantiation carries no stamp code: even disabled, it measurably changed
+// the kernel's schedule): the timeline of the step, summarized by bench.py
+// --timeline.
+constexpr int kStamps = 10;
+enum Stamp {
+    ST_START = 0,      // the wave began
+    ST_LOGIT = 1,      // router row stored (router waves), the epoch known (others)
+    ST_ROUTED = 2,     // the experts chosen
+    ST_GU_ISSUED = 3,  // the first triple's gate/up loads issued
+    ST_ACT = 4,        // the first triple's activations published
+    ST_ACT_LAST = 5,   // the wave's last triple published (waves with two)
+    ST_DOWN_ISSUED = 6,
+    ST_EXCHANGED = 7,  // the workgroup holds every activation
+    ST_OUT = 8,        // the wave's output stored
+    ST_XCC = 9         // (a value, not a time) the XCD this workgroup ran on
+};
+
+template <bool STAMPS>
+__device__ __forceinline__ void stamp(const FusedArgs& a, uint32_t gw, int lane, int which) {
+    if constexpr (STAMPS) {
+        if (lane == 0) {
+            a.stamps[static_cast<size_t>(gw) * kStamps + which] = wall_clock64();
+        }
+    }
+}
 
 __device__ __forceinline__ void put_tagged(uint32_t* scratch, uint32_t word, uint64_t v) {
     __hip_atomic_store(reinterpret_cast<uint64_t*>(scratch) + word, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -98,7 +127,7 @@ __device__ __forceinline__ void load3_coherent(const uint32_t* p0, const uint32_
         : "memory");
 }
 
-template <typename WT, int TK, int EB>
+template <typename WT, int TK, int EB, bool STAMPS>
 __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
     static_assert(kReadsPerThread == 3, "load3_coherent covers a thread's share");
     __shared__ __attribute__((aligned(16))) uint16_t act_l[kMaxAct];
@@ -121,6 +150,14 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
     // count first and waits for it with the router's loads (loads complete
     // in order), so the two round trips overlap.
     const uint32_t re = blockIdx.x;
+    stamp<STAMPS>(a, gw, lane, ST_START);
+    if constexpr (STAMPS) {
+        if (lane == 0) {
+            uint32_t xcc;
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+            a.stamps[static_cast<size_t>(gw) * kStamps + ST_XCC] = xcc & 0xfu;
+        }
+    }
     uint32_t xw[16];
     mh::load_x_words(a.x + 32u * c, xw);
     float bias_r[EB];
@@ -176,6 +213,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
         }
         a.logits[re] = logit;
     }
+    stamp<STAMPS>(a, gw, lane, ST_LOGIT);
 
     // ---- routing: one wave polls this XCD's copy of the tagged logits into
     // LDS, then every wave chooses the experts itself
@@ -228,6 +266,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
             exv = lane == r ? ex[r] : exv;
         }
     }
+    stamp<STAMPS>(a, gw, lane, ST_ROUTED);
 
     // ---- phase 2: gate/up + SwiGLU on triples of activations: triple t is
     // activations 3t .. 3t+2 of the flattened [TK, NI] block (its six rows'
@@ -267,6 +306,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
     if (t < triples) {
         load_triple(t);
     }
+    stamp<STAMPS>(a, gw, lane, ST_GU_ISSUED);
 
     // routing weights, off the gate/up loads' path
     uint32_t wb[TK];
@@ -318,6 +358,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
                     a.act[3u * t + 2u] = static_cast<uint16_t>(a2);
                 }
             }
+            stamp<STAMPS>(a, gw, lane, t == gw ? ST_ACT : ST_ACT_LAST);
             t += nw;
             if (t < triples) {
                 load_triple(t);
@@ -345,6 +386,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
             dbr[r] = a.dbi[row * GD + gcd];
         }
     }
+    stamp<STAMPS>(a, gw, lane, ST_DOWN_ISSUED);
 
     // ---- phase 3: once the workgroup's own activations are out, every
     // thread polls its share of the activation words (16 bytes at a time)
@@ -429,6 +471,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
             xs_l[j] = xs;
         }
         __syncthreads();
+        stamp<STAMPS>(a, gw, lane, ST_EXCHANGED);
         ok = ok && bad_l == 0u;
         if (has_out) {
             float h[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -457,6 +500,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
                 a.out[gw] = ok ? mh::f32_to_bf16(total) : static_cast<uint16_t>(0x7fc0);
             }
         }
+        stamp<STAMPS>(a, gw, lane, ST_OUT);
     }
 }
 
@@ -464,13 +508,15 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
 
 namespace mh {
 
+uint32_t moe_decode_fused_waves() { return kGrid * kWaves; }
+
 // Fused decode step; MH_ERR_UNSUPPORTED when the shapes or the device need
 // the three-launch path (the caller then uses it).
 int moe_decode_fused(const void* router, int router_dtype, const float* bias, int mode, float eps,
                      const mh_quant_weights* gate, const mh_quant_weights* up,
                      const mh_quant_weights* down, uint32_t n_experts, uint32_t topk,
                      const uint16_t* x, uint16_t* out, float* logits, uint32_t* ids,
-                     uint16_t* weights, uint16_t* act, uint32_t* scratch, hipStream_t stream) {
+                     uint16_t* weights, uint16_t* act, uint32_t* scratch, uint64_t* stamps, hipStream_t stream) {
     const uint32_t NI = gate->out_features / n_experts;
     const uint32_t K = gate->in_features;
     // all kGrid workgroups resident (one per CU), one wave per output and
@@ -489,12 +535,16 @@ int moe_decode_fused(const void* router, int router_dtype, const float* bias, in
     a.uc = up->codes; a.usc = up->scales; a.ubi = up->biases;
     a.dc = down->codes; a.dsc = down->scales; a.dbi = down->biases;
     a.logits = logits; a.ids = ids; a.weights = weights; a.act = act; a.out = out; a.scratch = scratch;
+    a.stamps = stamps;
     a.E = n_experts; a.K = K; a.NI = NI; a.gs = gate->group_size;
     const bool f32 = router_dtype == MH_DTYPE_F32;
     const bool eb1 = n_experts <= 64u;  // one expert per lane in the routing
-#define MH_FUSED_LAUNCH_EB(TK, EB)                                                                               \
-    if (f32) hipLaunchKernelGGL((k_moe_decode_fused<float, TK, EB>), dim3(kGrid), dim3(kThreads), 0, stream, a); \
-    else hipLaunchKernelGGL((k_moe_decode_fused<uint16_t, TK, EB>), dim3(kGrid), dim3(kThreads), 0, stream, a);
+#define MH_FUSED_LAUNCH_ST(TK, EB, ST)                                                                            \
+    if (f32) hipLaunchKernelGGL((k_moe_decode_fused<float, TK, EB, ST>), dim3(kGrid), dim3(kThreads), 0, stream, a); \
+    else hipLaunchKernelGGL((k_moe_decode_fused<uint16_t, TK, EB, ST>), dim3(kGrid), dim3(kThreads), 0, stream, a);
+#define MH_FUSED_LAUNCH_EB(TK, EB)          \
+    if (stamps) { MH_FUSED_LAUNCH_ST(TK, EB, true) } \
+    else { MH_FUSED_LAUNCH_ST(TK, EB, false) }
 #define MH_FUSED_LAUNCH(TK)            \
     if (eb1) { MH_FUSED_LAUNCH_EB(TK, 1) } \
     else { MH_FUSED_LAUNCH_EB(TK, 4) }
@@ -504,6 +554,7 @@ int moe_decode_fused(const void* router, int router_dtype, const float* bias, in
         case 3: MH_FUSED_LAUNCH(3) break;
         default: MH_FUSED_LAUNCH(4) break;
     }
+#undef MH_FUSED_LAUNCH_ST
 #undef MH_FUSED_LAUNCH_EB
 #undef MH_FUSED_LAUNCH
     return mh::launch_status("k_moe_decode_fused");

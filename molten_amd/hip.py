@@ -112,6 +112,8 @@ _SIGNATURES = {
     "mh_gemv_gather_down_combine": [_qw, _vp, _vp, _vp, _vp, _u32, _u32, _vp],
     "mh_moe_decode": [_vp, _i32, _vp, _i32, _f32, _qw, _qw, _qw, _u32, _u32, _vp, _vp, _vp, _vp,
                       _vp, _vp, _vp, _vp],
+    "mh_moe_decode_stamped": [_vp, _i32, _vp, _i32, _f32, _qw, _qw, _qw, _u32, _u32, _vp, _vp, _vp, _vp,
+                              _vp, _vp, _vp, _vp, _vp],
     "mh_router_prefill": [_vp, _vp, _i32, _vp, _u32, _u32, _u32, _vp],
     "mh_moe_route_batch": [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _i32, _f32, _vp],
     "mh_moe_zero_counts": [_vp, _u32, _vp],
@@ -497,6 +499,20 @@ def moe_decode(router, bias, gate: QuantWeights, up: QuantWeights, down: QuantWe
                                _qref(gate), _qref(up), _qref(down), n_experts, topk, _ptr(x),
                                _ptr(out), _ptr(logits), _ptr(ids), _ptr(weights), _ptr(act),
                                _ptr(scratch), _stream(stream)), "moe_decode")
+
+
+MOE_DECODE_STAMPS = 10  # MH_MOE_DECODE_STAMPS
+
+
+def moe_decode_stamped(router, bias, gate: QuantWeights, up: QuantWeights, down: QuantWeights,
+                       n_experts: int, topk: int, x, out, logits, ids, weights, act, scratch, stamps,
+                       mode: int = ROUTE_SIGMOID_BIAS, eps: float = 1e-6, stream=None) -> None:
+    """moe_decode on the single-launch path with per-wave phase timestamps
+    (measurement only): stamps u64 [2048 * MOE_DECODE_STAMPS]."""
+    check(load().mh_moe_decode_stamped(_ptr(router), _dtype_of(router), _ptr(bias), mode, eps,
+                                       _qref(gate), _qref(up), _qref(down), n_experts, topk, _ptr(x),
+                                       _ptr(out), _ptr(logits), _ptr(ids), _ptr(weights), _ptr(act),
+                                       _ptr(scratch), _ptr(stamps), _stream(stream)), "moe_decode_stamped")
 
 
 def router_prefill(x, w, out, m: int, k: int, e: int, stream=None) -> None:
