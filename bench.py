@@ -46,6 +46,8 @@ BYTES = {
     "next_dense_down_q4_k11776": 13_593_600,  # 2048 rows x (5888 code + 736 s/b) B + x + y
     "next_gather_rows_q6_4096": 23_609_344,   # 4096 x (1536 code + 128 s/b + 4096 out) B + ids
     "next_sample_gumbel_128000": 272_008,  # 128000 bf16 logits + the seen bits + the key
+    # logits + seen read, w written once and read by 6 radix rounds and the draw
+    "next_sample_topk_topp_128000": 272_008 + 128_000 * 4 * 8,
     "next_token_tail_embed": 13_972,  # key read + clear, token, one Q6 row + s/b, gain, x and normed rows
 }
 FLOPS_CONFIG4 = 309_237_645_312
@@ -199,6 +201,12 @@ def bench_next_rows(torch, hip, dev, gen, steps, warmup):
     key = torch.zeros(1, dtype=torch.int64, device=dev)
     prm = [sample_params(0.8, 1234, i, 1.1) for i in range(8)]
     ms_s = timed(torch, lambda i: hip.sample_gumbel(rows[i % 4], 128000, seen, prm[i % 8], key), steps, warmup)
+    # the kept-set draw (top_k 40 then top_p 0.9) on the same rows
+    wsb = hip.sample_workspace_bytes(128000)
+    sws = torch.zeros(wsb, dtype=torch.uint8, device=dev)
+    prm_kp = [sample_params(0.8, 1234, i, 1.1, top_k=40, top_p=0.9) for i in range(8)]
+    ms_kp = timed(torch, lambda i: hip.sample_draw(rows[i % 4], 128000, seen, prm_kp[i % 8], key, sws, wsb),
+                  steps, warmup)
     # the prefill dense projections (dequant + GEMM fused), 4096 tokens: an
     # attention projection 2048 -> 2048 and the dense FFN gate 2048 -> 11776
     ms_x = []
@@ -219,7 +227,7 @@ def bench_next_rows(torch, hip, dev, gen, steps, warmup):
     ms_x.append(timed(torch, lambda i: hip.gemm_quant_bf16_nt(pa, 4096, pw[i % 4][0], pc, scr, 2048 * 2048),
                       steps, warmup))
     del pb, pc, pw, scr
-    return ms_p, ms_c, ms_d, ms_g, ms_t, ms_x, ms_s
+    return ms_p, ms_c, ms_d, ms_g, ms_t, ms_x, (ms_s, ms_kp)
 
 
 def moe_set(torch, dev, gen, E=64, H=2048, I=1536):
@@ -571,7 +579,7 @@ def main() -> int:
             value=round(BYTES["config1"] / (ms1 * 1e-3) / 1e9, 1), unit="GB/s",
             ms_per_step=round(ms1, 5), frac_of_hbm_peak=round(BYTES["config1"] / (ms1 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
         log("next rows: proj3, conv3, dense down K=11776, Q6 gather, token tail, Gumbel draw, dense prefill")
-        ms_p, ms_c, ms_d, ms_g, ms_t, ms_x, ms_s = bench_next_rows(torch, hip, dev, gen, steps, warmup)
+        ms_p, ms_c, ms_d, ms_g, ms_t, ms_x, (ms_s, ms_kp) = bench_next_rows(torch, hip, dev, gen, steps, warmup)
         for key, n, ms in zip(("next_dense_prefill_q4_4096x2048x2048", "next_dense_prefill_q4_4096x11776x2048",
                                "next_gemm_bf16_nt_4096x2048x2048", "next_gemm_quant_bf16_nt_q4_4096x2048x2048"),
                               (2048, 11776, 2048, 2048), ms_x):
@@ -581,7 +589,8 @@ def main() -> int:
                 frac_of_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4))
         for key, ms in (("next_proj3_gemv_scatter", ms_p), ("next_conv3_gemv", ms_c),
                         ("next_dense_down_q4_k11776", ms_d), ("next_gather_rows_q6_4096", ms_g),
-                        ("next_token_tail_embed", ms_t), ("next_sample_gumbel_128000", ms_s)):
+                        ("next_token_tail_embed", ms_t), ("next_sample_gumbel_128000", ms_s),
+                        ("next_sample_topk_topp_128000", ms_kp)):
             v = BYTES[key] / (ms * 1e-3) / 1e9
             others[key] = dict(value=round(v, 1), unit="GB/s", ms_per_step=round(ms, 5),
                                frac_of_hbm_peak=round(v / HBM_PEAK_GBS, 4))

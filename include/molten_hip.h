@@ -266,6 +266,26 @@ typedef struct {
 int mh_sample_gumbel(const uint16_t* logits, uint32_t n, const uint32_t* seen,
                      const mh_sample_params* params, uint64_t* best, mh_stream_t stream);
 
+/* src/lfm/sample.rs:264-330 encode_draw, every case (lfm_sample.metal
+ * lfm_sample_prep / _levels / _gather / _finish): the draw over the kept set
+ * {w >= tau}: top_k (0 = off; k >= n keeps every token) keeps the tokens
+ * whose w is at least the k-th largest (ties kept); top_p (< 1) then keeps,
+ * among those, the smallest set {w >= t} whose mass is at least top_p times
+ * the kept mass (tie groups whole); mass = exp(w - max w) in 2^-40 fixed
+ * point, so the decision is exact and independent of any summation order.
+ * The Gumbel-max over the kept tokens is folded into `best` as by
+ * mh_sample_gumbel (which this calls when neither is on).  workspace:
+ * mh_sample_workspace_bytes(n) bytes, 256-byte aligned, zeroed before the
+ * first call and left zero by every call; calls sharing one workspace must
+ * not overlap.  top_p must be in (0, 1]. */
+size_t mh_sample_workspace_bytes(uint32_t n);
+int mh_sample_draw(const uint16_t* logits, uint32_t n, const uint32_t* seen, const mh_sample_params* params,
+                   uint64_t* best, void* workspace, size_t workspace_bytes, mh_stream_t stream);
+
+/* src/lfm/sample.rs:332-353 encode_mark (lfm_sample.metal lfm_sample_mark):
+ * adds the drawn token *tok (ignored when >= n) to the seen-token bitmap. */
+int mh_sample_mark(const uint32_t* tok, uint32_t* seen, uint32_t n, mh_stream_t stream);
+
 /* src/kernels/lfm.rs:794 argmax_bf16: two-stage argmax of a bf16 row,
  * ties to the lowest index.  partials: scratch of >= 64*8 bytes. */
 int mh_argmax_bf16(const uint16_t* x, uint32_t n, void* partials, uint32_t* out,

@@ -89,6 +89,9 @@ _SIGNATURES = {
     "mh_conv3_gemv": [_qw, _vp, _vp, _vp, _vp, _vp, _vp],
     "mh_token_tail": [_vp, _vp, _u32, _vp],
     "mh_sample_gumbel": [_vp, _u32, _vp, _vp, _vp, _vp],
+    "mh_sample_workspace_bytes": [_u32],
+    "mh_sample_draw": [_vp, _u32, _vp, _vp, _vp, _vp, _sz, _vp],
+    "mh_sample_mark": [_vp, _vp, _u32, _vp],
     "mh_checkpoint_open": [ctypes.c_char_p, ctypes.POINTER(_vp)],
     "mh_checkpoint_close": [_vp],
     "mh_checkpoint_count": [_vp],
@@ -136,7 +139,7 @@ _SIGNATURES = {
                        _vp, _sz, _vp],
 }
 _RESTYPES = {"mh_last_error": ctypes.c_char_p, "mh_version": ctypes.c_char_p,
-             "mh_moe_prefill_workspace": ctypes.c_size_t, "mh_checkpoint_close": None,
+             "mh_moe_prefill_workspace": ctypes.c_size_t, "mh_sample_workspace_bytes": ctypes.c_size_t, "mh_checkpoint_close": None,
              "mh_checkpoint_count": ctypes.c_uint32, "mh_checkpoint_name": ctypes.c_char_p}
 
 _lib: Optional[ctypes.CDLL] = None
@@ -421,6 +424,24 @@ def sample_gumbel(logits, n: int, seen, params: SampleParams, best, stream=None)
     """src/lfm/sample.rs:264 encode_draw, temperature only (the key folds into best)."""
     check(load().mh_sample_gumbel(_ptr(logits), n, _ptr(seen), ctypes.byref(params), _ptr(best),
                                   _stream(stream)), "sample_gumbel")
+
+
+def sample_workspace_bytes(n: int) -> int:
+    """mh_sample_workspace_bytes: the kept-set draw's workspace for a vocabulary of n."""
+    return int(load().mh_sample_workspace_bytes(n))
+
+
+def sample_draw(logits, n: int, seen, params: SampleParams, best, workspace, workspace_bytes: int,
+                stream=None) -> None:
+    """src/lfm/sample.rs:264-330 encode_draw, every case: top-k / top-p kept set
+    (exact thresholds) and the Gumbel-max over it, folded into best."""
+    check(load().mh_sample_draw(_ptr(logits), n, _ptr(seen), ctypes.byref(params), _ptr(best), _ptr(workspace),
+                                workspace_bytes, _stream(stream)), "sample_draw")
+
+
+def sample_mark(tok, seen, n: int, stream=None) -> None:
+    """src/lfm/sample.rs:332 encode_mark: the drawn token into the seen bitmap."""
+    check(load().mh_sample_mark(_ptr(tok), _ptr(seen), n, _stream(stream)), "sample_mark")
 
 
 class TensorMeta(ctypes.Structure):

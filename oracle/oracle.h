@@ -132,6 +132,25 @@ uint64_t orc_sample_gumbel(const uint16_t* logits, uint32_t n, const uint32_t* s
                            float inv_penalty, int use_penalty, uint32_t seed_lo, uint32_t seed_hi, uint32_t pos,
                            uint64_t best);
 
+/* ---- next row: the kept-set draw (top-k / top-p; lfm_sample.metal:16-27,
+ * 196-931; src/lfm/sample.rs:286-353) -------------------------------------
+ * orc_mass_fixed: exp(w - m) in 2^-40 fixed point, truncated.  orc_mass_target:
+ * the least integer >= top_p * z, exact (128-bit).  Pinned: closed forms and
+ * float64 over random and edge values.  orc_sample_draw: w as the temperature
+ * draw; tau = the k-th largest w (top-k, ties kept), then the largest value t
+ * among the kept with mass(w >= t) >= target(mass of the kept, top_p) (top-p,
+ * tie groups whole); the Gumbel-max over {w >= tau}; *tau_key_out = tau's
+ * orderable key (0: every token).  Pinned: the kept set equals numpy's
+ * (partition for top-k, float64 cumulative softmax for top-p on logits with
+ * clear gaps), k = 1 and a tiny top_p reduce to greedy, top_k >= n and
+ * top_p = 1 to the temperature draw, and the draws' frequencies over many
+ * positions match softmax renormalized over the kept set (chi-square). */
+uint64_t orc_mass_fixed(float w, float m);
+uint64_t orc_mass_target(uint64_t z, float top_p);
+uint64_t orc_sample_draw(const uint16_t* logits, uint32_t n, const uint32_t* seen, float inv_temp, float penalty,
+                         float inv_penalty, int use_penalty, uint32_t top_k, float top_p, uint32_t seed_lo,
+                         uint32_t seed_hi, uint32_t pos, uint64_t best, uint32_t* tau_key_out);
+
 /* ---- a6: argmax over bf16 logits (lfm.metal:1113-1282) ------------------
  * value desc, index asc; -0 == +0; NaN never taken; none -> 0.  Pinned by
  * known-answer ties and numpy argmax on tie-free rows. */

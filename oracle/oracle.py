@@ -56,6 +56,9 @@ def lib() -> ctypes.CDLL:
         _lib.orc_gumbel.restype = ctypes.c_float
         _lib.orc_gumbel.argtypes = [ctypes.c_uint32]
         _lib.orc_sample_gumbel.restype = ctypes.c_uint64
+        _lib.orc_sample_draw.restype = ctypes.c_uint64
+        _lib.orc_mass_fixed.restype = ctypes.c_uint64
+        _lib.orc_mass_target.restype = ctypes.c_uint64
         _lib.orc_get_threads.restype = ctypes.c_int
     return _lib
 
@@ -194,6 +197,29 @@ def sample_gumbel(logits: np.ndarray, seen, inv_temp: float, penalty: float, use
                                        ctypes.c_float(inv_pen), ctypes.c_int(int(use_penalty)),
                                        ctypes.c_uint32(seed & 0xffffffff), ctypes.c_uint32(seed >> 32),
                                        ctypes.c_uint32(pos), ctypes.c_uint64(best)))
+
+
+def mass_fixed(w: float, m: float) -> int:
+    return int(lib().orc_mass_fixed(ctypes.c_float(w), ctypes.c_float(m)))
+
+
+def mass_target(z: int, top_p: float) -> int:
+    return int(lib().orc_mass_target(ctypes.c_uint64(z), ctypes.c_float(top_p)))
+
+
+def sample_draw(logits: np.ndarray, seen, inv_temp: float, penalty: float, use_penalty: bool, top_k: int,
+                top_p: float, seed: int, pos: int, best: int = 0):
+    """The kept-set draw (top-k / top-p): returns (key folded with best, tau's orderable key)."""
+    logits = np.ascontiguousarray(logits, np.uint16)
+    seen = None if seen is None else np.ascontiguousarray(seen, np.uint32)
+    inv_pen = np.float32(1.0) / np.float32(penalty)
+    tau = ctypes.c_uint32(0)
+    k = lib().orc_sample_draw(_p(logits), ctypes.c_uint32(logits.size), _p(seen), ctypes.c_float(inv_temp),
+                              ctypes.c_float(penalty), ctypes.c_float(inv_pen), ctypes.c_int(int(use_penalty)),
+                              ctypes.c_uint32(top_k), ctypes.c_float(top_p), ctypes.c_uint32(seed & 0xffffffff),
+                              ctypes.c_uint32(seed >> 32), ctypes.c_uint32(pos), ctypes.c_uint64(best),
+                              ctypes.byref(tau))
+    return int(k), int(tau.value)
 
 
 def gemv_quant_rows(h, x: np.ndarray, rows: np.ndarray, batch: int = 1) -> np.ndarray:

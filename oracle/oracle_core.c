@@ -426,6 +426,138 @@ uint64_t orc_sample_gumbel(const uint16_t* logits, uint32_t n, const uint32_t* s
     return best;
 }
 
+/* The kept-set draw (lfm_sample.metal:16-27 semantics; src/lfm/sample.rs:286-330).
+ * Kept set {w >= tau}: top-k keeps every token whose w is at least the k-th
+ * largest (ties kept); top-p keeps, among those, the smallest set {w >= t}
+ * whose mass is at least top_p times the set's mass (tie groups whole).  A
+ * token's mass is exp(w - M) (M the vocabulary's max w, exp the library's own)
+ * in 2^-40 fixed point, truncated, so every mass sum is an exact integer and
+ * the decision does not depend on any summation order.  The draw is the
+ * Gumbel-max over the kept tokens, keyed as the temperature-only draw. */
+static inline uint32_t smp_fkey(float v) {
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    if ((u << 1) == 0u) {
+        u = 0u;
+    }
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+static inline float smp_kfloat(uint32_t k) {
+    const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+    float v;
+    memcpy(&v, &u, 4);
+    return v;
+}
+
+uint64_t orc_mass_fixed(float w, float m) {
+    return (uint64_t)(orc_expf(w - m) * 1099511627776.0f);  /* 2^40, truncated */
+}
+
+/* The least integer T >= top_p * z (top_p in (0, 1), exact). */
+uint64_t orc_mass_target(uint64_t z, float top_p) {
+    uint32_t u;
+    memcpy(&u, &top_p, 4);
+    const uint32_t ex = (u >> 23) & 0xffu;
+    const uint64_t mant = ex ? (uint64_t)((u & 0x7fffffu) | 0x800000u) : (uint64_t)(u & 0x7fffffu);
+    const int s = 150 - (int)(ex ? ex : 1u);  /* top_p = mant * 2^-s */
+    const unsigned __int128 prod = (unsigned __int128)mant * z;
+    if (s >= 128) {
+        return prod != 0 ? 1u : 0u;
+    }
+    uint64_t t = (uint64_t)(prod >> s);
+    if ((prod & ((((unsigned __int128)1) << s) - 1)) != 0) {
+        t += 1u;
+    }
+    return t;
+}
+
+static int cmp_desc_u32(const void* a, const void* b) {
+    const uint32_t x = *(const uint32_t*)a, y = *(const uint32_t*)b;
+    return x < y ? 1 : x > y ? -1 : 0;
+}
+
+uint64_t orc_sample_draw(const uint16_t* logits, uint32_t n, const uint32_t* seen, float inv_temp, float penalty,
+                         float inv_penalty, int use_penalty, uint32_t top_k, float top_p, uint32_t seed_lo,
+                         uint32_t seed_hi, uint32_t pos, uint64_t best, uint32_t* tau_key_out) {
+    float* w = (float*)malloc((size_t)n * sizeof(float));
+    uint32_t* keys = (uint32_t*)malloc((size_t)n * sizeof(uint32_t));
+    uint32_t mkey = 0u;
+    for (uint32_t i = 0; i < n; ++i) {
+        float v = orc_bf16_to_f32(logits[i]);
+        if (use_penalty && ((seen[i >> 5] >> (i & 31u)) & 1u)) {
+            v = v > 0.0f ? v * inv_penalty : v * penalty;
+        }
+        float x = v * inv_temp;
+        uint32_t u;
+        memcpy(&u, &x, 4);
+        if ((u << 1) == 0u) {
+            x = 0.0f;
+        }
+        w[i] = x;
+        keys[i] = smp_fkey(x);
+        mkey = keys[i] > mkey ? keys[i] : mkey;
+    }
+    uint32_t tau = 0u;
+    const int use_k = top_k != 0u && top_k < n;
+    const int use_p = top_p < 1.0f;
+    if (use_k || use_p) {
+        uint32_t* sorted = (uint32_t*)malloc((size_t)n * sizeof(uint32_t));
+        memcpy(sorted, keys, (size_t)n * sizeof(uint32_t));
+        qsort(sorted, n, sizeof(uint32_t), cmp_desc_u32);
+        if (use_k) {
+            tau = sorted[top_k - 1u];
+        }
+        if (use_p) {
+            const float m = smp_kfloat(mkey);
+            uint64_t z = 0u;
+            for (uint32_t i = 0; i < n; ++i) {
+                if (keys[i] >= tau) {
+                    z += orc_mass_fixed(w[i], m);
+                }
+            }
+            const uint64_t target = orc_mass_target(z, top_p);
+            /* walk the distinct values downward; the first whose cumulative
+             * mass reaches the target is tau_p */
+            uint64_t cum = 0u;
+            uint32_t i = 0;
+            uint32_t tau_p = tau;
+            while (i < n && sorted[i] >= tau) {
+                const uint32_t k = sorted[i];
+                while (i < n && sorted[i] == k) {
+                    cum += orc_mass_fixed(smp_kfloat(k), m);
+                    ++i;
+                }
+                if (cum >= target) {
+                    tau_p = k;
+                    break;
+                }
+            }
+            tau = tau_p > tau ? tau_p : tau;
+        }
+        free(sorted);
+    }
+    const uint32_t key[2] = {seed_lo, seed_hi};
+    for (uint32_t q = 0; q < n / 4; ++q) {
+        const uint32_t ctr[4] = {q, pos, 0x53414D50u, 0u};
+        uint32_t r[4];
+        orc_philox(ctr, key, r);
+        for (uint32_t j = 0; j < 4; ++j) {
+            const uint32_t i = 4 * q + j;
+            if (keys[i] >= tau) {
+                const uint64_t k = orc_argmax_key(w[i] + orc_gumbel(r[j]), i);
+                best = k > best ? k : best;
+            }
+        }
+    }
+    if (tau_key_out) {
+        *tau_key_out = tau;
+    }
+    free(keys);
+    free(w);
+    return best;
+}
+
 /* ------------------------------------------------------------- argmax --- */
 
 uint32_t orc_argmax_bf16(const uint16_t* x, size_t n) {

@@ -193,6 +193,20 @@ def test_bf16_and_quant_gemm_arguments():
     assert ei.value.code == hip.MH_ERR_ALIGN
 
 
+def test_sample_draw_arguments():
+    p = hip.sample_params(1.0, 1, 0, top_k=40)
+    with pytest.raises(hip.MoltenError, match="workspace holds 16 bytes"):
+        hip.sample_draw(0x4000, 128000, None, p, 0x6000, 0x7000, 16, stream=0)
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.sample_draw(0x4000, 128000, None, hip.sample_params(1.0, 1, 0, top_p=0.0), 0x6000, 0x7000,
+                        1 << 20, stream=0)
+    assert ei.value.code == hip.MH_ERR_INVALID
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.sample_draw(0x4000, 128000, None, p, 0x6000, 0x7010, 1 << 20, stream=0)
+    assert ei.value.code == hip.MH_ERR_ALIGN
+    assert hip.sample_workspace_bytes(128000) >= 128000 * 4
+
+
 def test_sample_arguments():
     p = hip.sample_params(1.0, 1, 0)
     with pytest.raises(hip.MoltenError) as ei:

@@ -91,3 +91,133 @@ def test_draw_closed_forms(orc):
     # folding: a key already above every draw is kept
     top = (0xffffffff << 32) | 0xfffffff0
     assert orc.sample_gumbel(logits, None, 1.0, 1.0, False, 3, 0, best=top) == top
+
+
+# ---------------------------------------------------------------- kept set --
+
+def _fkey(v):
+    """Orderable u32 key of float32 values (-0 folded to +0)."""
+    u = np.asarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    u = np.where((u << np.uint64(1)) & np.uint64(0xffffffff) == 0, np.uint64(0), u)
+    neg = (u & np.uint64(0x80000000)) != 0
+    return np.where(neg, (~u) & np.uint64(0xffffffff), u | np.uint64(0x80000000)).astype(np.uint64)
+
+
+def test_mass_target_is_exact_ceiling(orc):
+    """The least integer >= top_p * z with top_p's exact f32 value."""
+    from fractions import Fraction
+
+    rng = np.random.default_rng(11)
+    zs = [0, 1, 2, 3, 1 << 40, (1 << 57) - 1, 128000 << 40] + [int(z) for z in rng.integers(0, 1 << 57, 300)]
+    ps = [0.5, 0.9, 0.95, 1e-3, 1e-30, 2.0 ** -126, 0.99999994] + list(rng.uniform(0, 1, 50))
+    for p in ps:
+        pf = Fraction(float(np.float32(p)))
+        for z in zs:
+            want = -((-pf * z).__floor__())  # ceiling
+            assert orc.mass_target(z, float(np.float32(p))) == want, (p, z)
+
+
+def test_mass_fixed_matches_float64(orc):
+    rng = np.random.default_rng(12)
+    m = 3.0
+    for w in list(rng.uniform(-40, 3, 2000)) + [3.0, -100.0, -87.0]:
+        w = float(np.float32(w))
+        got = orc.mass_fixed(w, m)
+        want = math.exp(float(np.float32(w - m))) * 2.0 ** 40
+        assert got <= want * (1 + 3e-7) + 1 and got >= want * (1 - 3e-7) - 1, (w, got, want)
+    assert orc.mass_fixed(m, m) == 1 << 40  # exp(0) = 1 exactly
+
+
+def _w(logits, temp):
+    return layout.bf16_to_f32(logits).astype(np.float32) * np.float32(1.0 / temp)
+
+
+@pytest.mark.parametrize("k", [1, 2, 17, 500, 4095])
+def test_topk_threshold_is_kth_largest(orc, k):
+    """tau = the k-th largest w (numpy partition); ties at the boundary are
+    kept (planted: the k-th value repeated around it)."""
+    rng = np.random.default_rng(k)
+    v = rng.normal(0, 2, 4096).astype(np.float32)
+    order = np.argsort(-v)
+    if k > 3:
+        v[order[k - 3:k + 3]] = v[order[k - 1]]  # a tie group straddling k
+    logits = layout.f32_to_bf16(v)
+    w = _w(logits, 0.7)
+    _, tau = orc.sample_draw(logits, None, float(np.float32(1 / 0.7)), 1.0, False, k, 1.0, 5, 0)
+    kth = np.partition(w, len(w) - k)[len(w) - k]
+    assert tau == int(_fkey(kth))
+    kept = int((_fkey(w) >= tau).sum())
+    assert kept >= k and kept == int((w >= kth).sum())
+
+
+def test_topp_threshold_matches_float64(orc):
+    """tau_p = the largest value t with softmax mass(w >= t) >= top_p, on
+    logits whose cumulative masses are far from the boundary (float64)."""
+    rng = np.random.default_rng(21)
+    for trial in range(20):
+        v = rng.normal(0, 3, 1000).astype(np.float32)
+        logits = layout.f32_to_bf16(v)
+        w = _w(logits, 1.0).astype(np.float64)
+        vals = np.unique(w)[::-1]
+        p = np.exp(w - w.max())
+        p /= p.sum()
+        cum = np.array([p[w >= t].sum() for t in vals])
+        top_p = float(rng.uniform(0.3, 0.95))
+        j = int(np.argmax(cum >= top_p))
+        if abs(cum[j] - top_p) < 1e-4 or (j > 0 and abs(cum[j - 1] - top_p) < 1e-4):
+            continue  # too close to call in float64 vs fixed point
+        _, tau = orc.sample_draw(logits, None, 1.0, 1.0, False, 0, float(np.float32(top_p)), 1, trial)
+        assert tau == int(_fkey(np.float32(vals[j]))), (trial, top_p)
+
+
+def test_topk_then_topp(orc):
+    """Both: top-p over the top-k set's own mass; tau >= tau_k."""
+    rng = np.random.default_rng(31)
+    v = rng.normal(0, 2, 2048).astype(np.float32)
+    logits = layout.f32_to_bf16(v)
+    w = _w(logits, 1.0).astype(np.float64)
+    k, top_p = 50, 0.6
+    kth = np.sort(w)[::-1][k - 1]
+    sub = w[w >= kth]
+    vals = np.unique(sub)[::-1]
+    p = np.exp(sub - w.max())
+    p /= p.sum()
+    cum = np.array([p[sub >= t].sum() for t in vals])
+    j = int(np.argmax(cum >= top_p))
+    _, tau = orc.sample_draw(logits, None, 1.0, 1.0, False, k, top_p, 1, 0)
+    assert tau == int(_fkey(np.float32(vals[j])))
+
+
+def test_kept_set_reductions(orc):
+    rng = np.random.default_rng(41)
+    logits = layout.f32_to_bf16(rng.normal(0, 2, 4096).astype(np.float32))
+    v = layout.bf16_to_f32(logits)
+    greedy = int(np.argmax(v))
+    for pos in range(8):
+        # k = 1 and a tiny top_p keep only the max: the draw is greedy
+        assert _token(orc.sample_draw(logits, None, 1.0, 1.0, False, 1, 1.0, 9, pos)[0]) == greedy
+        assert _token(orc.sample_draw(logits, None, 1.0, 1.0, False, 0, 1e-6, 9, pos)[0]) == greedy
+        # no top-k (k >= n is mapped to 0 by the host) and top_p = 1: the temperature draw
+        assert (orc.sample_draw(logits, None, 1.25, 1.0, False, 0, 1.0, 9, pos)[0]
+                == orc.sample_gumbel(logits, None, 1.25, 1.0, False, 9, pos))
+        # top-k over every token keeps every token: the same draw
+        assert (orc.sample_draw(logits, None, 1.25, 1.0, False, 4096, 1.0, 9, pos)[0]
+                == orc.sample_gumbel(logits, None, 1.25, 1.0, False, 9, pos))
+
+
+def test_kept_draw_follows_renormalized_softmax(orc):
+    """Over many positions the draws are distributed as softmax(w)
+    renormalized over the kept set, and never leave it."""
+    logits = layout.f32_to_bf16(np.float32([0.0, 1.0, 2.0, -1.0, 0.5, 1.5, -2.0, 0.25]))
+    w = layout.bf16_to_f32(logits).astype(np.float64)
+    kept = np.argsort(-w)[:4]  # top_k = 4
+    p = np.zeros(8)
+    p[kept] = np.exp(w[kept] - w.max())
+    p /= p.sum()
+    n = 20000
+    counts = np.zeros(8)
+    for pos in range(n):
+        counts[_token(orc.sample_draw(logits, None, 1.0, 1.0, False, 4, 1.0, 13, pos)[0])] += 1
+    assert counts[p == 0].sum() == 0
+    chi2 = float(((counts[kept] - n * p[kept]) ** 2 / (n * p[kept])).sum())
+    assert chi2 < 25.0, (chi2, counts / n, p)  # df 3
