@@ -71,53 +71,66 @@ __global__ __launch_bounds__(kThreads) void k_sample_gumbel(const uint16_t* logi
 // fixed point (truncated) so that every mass sum is an exact integer and the
 // decision does not depend on the order of any sum.  tau is found exactly by
 // a radix select over the orderable 32-bit keys of w: three rounds of 11, 11
-// and 10 bits, each round one launch in which every workgroup histograms its
-// tokens' digits (counts and masses) in LDS and adds them to a global
-// histogram, and the last workgroup to arrive picks the digit that holds the
-// threshold and writes the next round's prefix (a count phase for top-k, then
-// a mass phase for top-p restricted to the top-k set).  The draw then folds
-// the Gumbel-max over {w >= tau} into the key word, as the temperature draw.
+// and 10 bits per phase (a count phase for top-k, then a mass phase for top-p
+// restricted to the top-k set).  Each round is one launch in which every
+// workgroup histograms its tokens' digits in LDS and adds the nonzero bins to
+// that round's global histogram.  The digit a round picks is decided at the
+// start of the next launch, by every workgroup alike, from the round's
+// histogram and the state the round ran with (a suffix scan over the bins):
+// no arrival counter, no fence and no serial tail between rounds.  The first
+// count round runs inside the launch that computes w.  The draw launch
+// decides the last round and folds the Gumbel-max over {w >= tau} into the
+// key word, as the temperature draw.
 //
-// Workspace (caller-owned, zeroed once, left zero by every call): w f32[n],
-// the histogram, and the plan words.
-constexpr uint32_t kBlock = 4u * kThreads;  // tokens per workgroup
-constexpr int kDigits = 2048;               // 11-bit digits
+// Workspace (caller-owned; the first round's histogram zeroed before the
+// first call, and left zero by every call; the rest is rewritten by every
+// call): w f32[n], the per-workgroup max keys, one histogram per round, and
+// the state each round ran with.
+constexpr int kGroups = 4;                          // groups of 4 tokens per thread
+constexpr uint32_t kBlock = 4u * kGroups * kThreads;  // tokens per workgroup
+constexpr int kDigits = 2048;                       // 11-bit digits
+constexpr int kRounds = 6;                          // 3 count + 3 mass rounds at most
+constexpr int kPer = kDigits / kThreads;            // bins per thread in the scan
 
-struct SmpPlan {
-    uint32_t max_key;     // orderable key of M (atomic max by the prep kernel)
-    uint32_t arrive;      // workgroups done with the current launch
-    uint32_t prefix;      // digits chosen so far in this phase
-    uint32_t restrict_key;  // the mass phase's floor (tau_k, or 0)
-    uint32_t tau_key;     // the final threshold's key (0: every token)
+// The band a round histograms (keys whose bits above the round's digit equal
+// prefix, and >= restrict_key) and the target the next decision meets.
+struct SmpState {
+    uint32_t prefix;        // digits chosen so far in this phase
+    uint32_t restrict_key;  // the mass phase's floor (the top-k threshold, or 0)
+    uint32_t tau_key;       // the latest phase threshold (0: every token)
     uint32_t pad0;
-    unsigned long long base;    // count / mass above the current band
-    unsigned long long target;  // the phase's target (k, or the mass target)
+    unsigned long long base;    // count / mass of the keys above the band
+    unsigned long long target;  // k, or the mass target (0: set by the first mass round)
 };
 
 struct SmpWs {
     float* w;
-    uint32_t* hcnt;
-    unsigned long long* hmass;
-    SmpPlan* plan;
+    uint32_t* wmax;             // per-workgroup max key
+    unsigned long long* hist;   // kRounds x kDigits
+    SmpState* plan;             // the state each round ran with
 };
 
 size_t smp_align(size_t b) { return (b + 255u) & ~static_cast<size_t>(255u); }
 
+uint32_t smp_grid(uint32_t n) { return (n + kBlock - 1u) / kBlock; }
+
 SmpWs smp_layout(void* ws, uint32_t n) {
     char* p = static_cast<char*>(ws);
     SmpWs l;
+    l.hist = reinterpret_cast<unsigned long long*>(p);
+    p += smp_align(static_cast<size_t>(kRounds) * kDigits * 8u);
+    l.plan = reinterpret_cast<SmpState*>(p);
+    p += smp_align(kRounds * sizeof(SmpState));
+    l.wmax = reinterpret_cast<uint32_t*>(p);
+    p += smp_align(static_cast<size_t>(smp_grid(n)) * 4u);
     l.w = reinterpret_cast<float*>(p);
-    p += smp_align(static_cast<size_t>(n) * 4u);
-    l.hcnt = reinterpret_cast<uint32_t*>(p);
-    p += smp_align(kDigits * 4u);
-    l.hmass = reinterpret_cast<unsigned long long*>(p);
-    p += smp_align(kDigits * 8u);
-    l.plan = reinterpret_cast<SmpPlan*>(p);
     return l;
 }
 
-size_t smp_bytes(uint32_t n) { return smp_align(static_cast<size_t>(n) * 4u) + smp_align(kDigits * 4u) +
-                                      smp_align(kDigits * 8u) + smp_align(sizeof(SmpPlan)); }
+size_t smp_bytes(uint32_t n) {
+    return smp_align(static_cast<size_t>(kRounds) * kDigits * 8u) + smp_align(kRounds * sizeof(SmpState)) +
+           smp_align(static_cast<size_t>(smp_grid(n)) * 4u) + smp_align(static_cast<size_t>(n) * 4u);
+}
 
 __device__ __forceinline__ uint32_t smp_fkey(float v) {
     uint32_t u = __float_as_uint(v);
@@ -153,30 +166,160 @@ __device__ unsigned long long smp_mass_target(unsigned long long z, float top_p)
     return t;
 }
 
-__device__ __forceinline__ uint32_t coherent_load(const uint32_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned long long coherent_load(const unsigned long long* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ int smp_shift(int round) { return round == 0 ? 21 : round == 1 ? 10 : 0; }
+__device__ __forceinline__ int smp_width(int round) { return round == 2 ? 10 : 11; }
+
+// tokens i0 .. i0 + 3 of group g of this thread (coalesced within a group)
+__device__ __forceinline__ uint32_t smp_token0(int g) {
+    return blockIdx.x * kBlock + static_cast<uint32_t>(g) * (4u * kThreads) + 4u * threadIdx.x;
 }
 
-// w of every token and the vocabulary's max key.
+struct SmpDecideLds {
+    unsigned long long wsum[kThreads / 64];
+    uint32_t pick;  // 1 + the chosen digit (0: none yet)
+    SmpState out;
+};
+
+// A round's histogram bins of this thread and the state the round ran with.
+struct SmpPrev {
+    SmpState in;
+    unsigned long long val[kPer];
+};
+
+// (issued before the launch's other loads are waited for)
+__device__ __forceinline__ SmpPrev smp_prev_load(const SmpWs& ws, int prev) {
+    SmpPrev r;
+    r.in = ws.plan[prev];
+    const unsigned long long* h = ws.hist + static_cast<size_t>(prev) * kDigits + threadIdx.x * kPer;
+#pragma unroll
+    for (int j = 0; j < kPer; j += 2) {
+        const ulonglong2 v2 = *reinterpret_cast<const ulonglong2*>(h + j);
+        r.val[j] = v2.x;
+        r.val[j + 1] = v2.y;
+    }
+    return r;
+}
+
+// The state of the round after `prev` (phase pp, round pr): the highest digit
+// d of prev's histogram whose cumulative count / mass from the top reaches
+// the target.  Every workgroup computes the same state from the same words.
+__device__ SmpState smp_decide(const SmpPrev& pv, int pp, int pr, const mh_sample_params& p, SmpDecideLds& l) {
+    const SmpState& in = pv.in;
+    const unsigned long long* val = pv.val;
+    unsigned long long tsum = 0ull;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        tsum += val[j];
+    }
+    // inclusive suffix sum over the lanes (lane l: lanes l .. 63), then the
+    // waves' totals
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    unsigned long long suf = tsum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const unsigned long long o = __shfl_down(suf, off);
+        if (lane + off < 64) {
+            suf += o;
+        }
+    }
+    if (lane == 0) {
+        l.wsum[wave] = suf;
+    }
+    if (threadIdx.x == 0) {
+        l.pick = 0u;
+    }
+    __syncthreads();
+    unsigned long long later = 0ull, total = 0ull;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) {
+        total += l.wsum[w];
+        later += w > wave ? l.wsum[w] : 0ull;
+    }
+    const unsigned long long target = (pp == 1 && pr == 0) ? smp_mass_target(total, p.top_p) : in.target;
+    // the count / mass above this thread's bins, then the highest bin d with
+    // above(d) + val(d) >= target
+    unsigned long long above = in.base + later + (suf - tsum);
+    uint32_t mine = 0xffffffffu;
+    unsigned long long mine_above = 0ull;
+#pragma unroll
+    for (int j = kPer - 1; j >= 0; --j) {
+        if (mine == 0xffffffffu && above + val[j] >= target) {
+            mine = static_cast<uint32_t>(threadIdx.x * kPer + j);
+            mine_above = above;
+        }
+        above += val[j];
+    }
+    if (mine != 0xffffffffu) {
+        atomicMax(&l.pick, mine + 1u);  // LDS: the highest qualifying digit
+    }
+    __syncthreads();
+    const uint32_t pick = l.pick;
+    if (pick == 0u ? threadIdx.x == 0 : mine == pick - 1u) {
+        // (exactly one thread; no digit reaches the target only if the
+        // histogram is empty, and the band is then kept whole)
+        const uint32_t d = pick == 0u ? 0u : pick - 1u;
+        const uint32_t key = in.prefix | (d << smp_shift(pr));
+        SmpState o = in;
+        if (pr < 2) {
+            o.prefix = key;
+            o.base = pick == 0u ? in.base : mine_above;
+            o.target = target;
+        } else {
+            o.prefix = 0u;
+            o.base = 0ull;
+            o.target = 0ull;
+            o.restrict_key = pp == 0 ? key : in.restrict_key;
+            o.tau_key = key;
+        }
+        l.out = o;
+    }
+    __syncthreads();
+    return l.out;
+}
+
+// w of every token, the workgroups' max keys, and (COUNT0) the first count
+// round's histogram; zeroes the other rounds' histograms.
+template <bool COUNT0>
 __global__ __launch_bounds__(kThreads) void k_smp_prep(const uint16_t* logits, uint32_t n, const uint32_t* seen,
                                                        mh_sample_params p, SmpWs ws) {
+    __shared__ uint32_t lcnt[COUNT0 ? kDigits : 1];
     __shared__ uint32_t part[kThreads / 64];
-    const uint32_t i0 = 4u * (blockIdx.x * kThreads + threadIdx.x);
-    uint32_t kmax = 0u;
-    if (i0 < n) {
-        const uint2 raw = *reinterpret_cast<const uint2*>(logits + i0);
-        const float v[4] = {mh::bf16lo(raw.x), mh::bf16hi(raw.x), mh::bf16lo(raw.y), mh::bf16hi(raw.y)};
-        const uint32_t bits = p.use_penalty != 0u ? (seen[i0 >> 5] >> (i0 & 31u)) : 0u;
-        float w[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            w[j] = processed(v[j], ((bits >> j) & 1u) != 0u, p);
-            kmax = max(kmax, smp_fkey(w[j]));
+    if (COUNT0) {
+        for (int d = threadIdx.x; d < kDigits; d += kThreads) {
+            lcnt[d] = 0u;
         }
-        *reinterpret_cast<float4*>(ws.w + i0) = make_float4(w[0], w[1], w[2], w[3]);
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            SmpState s0 = {};
+            s0.target = p.top_k;
+            ws.plan[0] = s0;
+        }
+    }
+    for (uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < (kRounds - 1) * kDigits; i += gridDim.x * kThreads) {
+        ws.hist[kDigits + i] = 0ull;
+    }
+    if (COUNT0) {
+        __syncthreads();
+    }
+    uint32_t kmax = 0u;
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+        const uint32_t i0 = smp_token0(g);
+        if (i0 < n) {
+            const uint2 raw = *reinterpret_cast<const uint2*>(logits + i0);
+            const float v[4] = {mh::bf16lo(raw.x), mh::bf16hi(raw.x), mh::bf16lo(raw.y), mh::bf16hi(raw.y)};
+            const uint32_t bits = p.use_penalty != 0u ? (seen[i0 >> 5] >> (i0 & 31u)) : 0u;
+            float w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                w[j] = processed(v[j], ((bits >> j) & 1u) != 0u, p);
+                const uint32_t key = smp_fkey(w[j]);
+                kmax = max(kmax, key);
+                if (COUNT0) {
+                    atomicAdd(&lcnt[key >> 21], 1u);
+                }
+            }
+            *reinterpret_cast<float4*>(ws.w + i0) = make_float4(w[0], w[1], w[2], w[3]);
+        }
     }
     kmax = mh::wave_max_u32(kmax);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -189,175 +332,149 @@ __global__ __launch_bounds__(kThreads) void k_smp_prep(const uint16_t* logits, u
         for (int w = 1; w < kThreads / 64; ++w) {
             kmax = max(kmax, part[w]);
         }
-        __hip_atomic_fetch_max(&ws.plan->max_key, kmax, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ws.wmax[blockIdx.x] = kmax;
+    }
+    if (COUNT0) {
+        for (int d = threadIdx.x; d < kDigits; d += kThreads) {
+            if (lcnt[d] != 0u) {
+                __hip_atomic_fetch_add(ws.hist + d, static_cast<unsigned long long>(lcnt[d]), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
     }
 }
 
-// One radix round.  phase 0 counts (top-k), phase 1 masses (top-p); round r
-// takes digit bits [shift, shift + width) of the keys in the current band
-// (keys whose bits above shift + width equal the prefix, and >= the phase's
-// floor).  final_round: the last round of the last phase.
-__global__ __launch_bounds__(kThreads) void k_smp_round(uint32_t n, mh_sample_params p, SmpWs ws, int phase,
-                                                        int round, int final_round) {
-    __shared__ uint32_t lcnt[kDigits];
-    __shared__ unsigned long long lmass[kDigits];
-    __shared__ uint32_t last_l;
-    __shared__ unsigned long long sum_l[kThreads];
-    __shared__ uint32_t pick_l;
-    const int shift = round == 0 ? 21 : round == 1 ? 10 : 0;
-    const int width = round == 2 ? 10 : 11;
-    const uint32_t hi_mask = round == 0 ? 0u : ~((1u << (shift + width)) - 1u);
-    const uint32_t prefix = coherent_load(&ws.plan->prefix);
-    const uint32_t floor_key = phase == 1 ? coherent_load(&ws.plan->restrict_key) : 0u;
-    const float m = smp_kfloat(coherent_load(&ws.plan->max_key));
-    for (int d = threadIdx.x; d < kDigits; d += kThreads) {
-        lcnt[d] = 0u;
-        lmass[d] = 0ull;
+// The vocabulary's max key, from the workgroups' max keys.
+__device__ uint32_t smp_max_key(const SmpWs& ws, uint32_t* part) {
+    uint32_t k = 0u;
+    for (uint32_t i = threadIdx.x; i < gridDim.x; i += kThreads) {
+        k = max(k, ws.wmax[i]);
+    }
+    k = mh::wave_max_u32(k);
+    if ((threadIdx.x & 63) == 0) {
+        part[threadIdx.x >> 6] = k;
     }
     __syncthreads();
-    const uint32_t i0 = 4u * (blockIdx.x * kThreads + threadIdx.x);
-    if (i0 < n) {
-        const float4 w4 = *reinterpret_cast<const float4*>(ws.w + i0);
-        const float w[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t key = smp_fkey(w[j]);
-            if ((key & hi_mask) == prefix && key >= floor_key) {
-                const uint32_t d = (key >> shift) & ((1u << width) - 1u);
-                if (phase == 0) {
-                    atomicAdd(&lcnt[d], 1u);
-                } else {
-                    atomicAdd(&lmass[d], smp_mass(w[j], m));
+    for (int w = 0; w < kThreads / 64; ++w) {
+        k = max(k, part[w]);
+    }
+    return k;
+}
+
+// Round `step` of this call (phase PHASE, digit round `round`): decides the
+// previous round (phase pp, round pr) unless step is 0, records the state,
+// and histograms the band's digits (counts, or masses exp(w - M)).
+template <int PHASE>
+__global__ __launch_bounds__(kThreads) void k_smp_round(uint32_t n, mh_sample_params p, SmpWs ws, int step,
+                                                        int round, int pp, int pr) {
+    __shared__ uint32_t lcnt[PHASE == 0 ? kDigits : 1];
+    __shared__ unsigned long long lmass[PHASE == 1 ? kDigits : 1];
+    __shared__ SmpDecideLds dl;
+    __shared__ uint32_t part[kThreads / 64];
+    // every load of the launch is issued before any is waited for: the
+    // tokens, the previous round's bins and state, the max keys
+    float4 w4[kGroups];
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+        const uint32_t i0 = smp_token0(g);
+        w4[g] = i0 < n ? *reinterpret_cast<const float4*>(ws.w + i0) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    const SmpPrev pv = smp_prev_load(ws, step > 0 ? step - 1 : 0);
+    for (int d = threadIdx.x; d < kDigits; d += kThreads) {
+        if (PHASE == 0) {
+            lcnt[d] = 0u;
+        } else {
+            lmass[d] = 0ull;
+        }
+    }
+    float m = 0.0f;
+    if (PHASE == 1) {
+        m = smp_kfloat(smp_max_key(ws, part));
+    }
+    SmpState st = {};
+    if (step == 0) {
+        st.target = PHASE == 0 ? p.top_k : 0ull;
+    } else {
+        st = smp_decide(pv, pp, pr, p, dl);
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        ws.plan[step] = st;
+    }
+    __syncthreads();
+    const int shift = smp_shift(round), width = smp_width(round);
+    const uint32_t hi_mask = round == 0 ? 0u : ~((1u << (shift + width)) - 1u);
+    const uint32_t floor_key = PHASE == 1 ? st.restrict_key : 0u;
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+        const uint32_t i0 = smp_token0(g);
+        if (i0 < n) {
+            const float w[4] = {w4[g].x, w4[g].y, w4[g].z, w4[g].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t key = smp_fkey(w[j]);
+                if ((key & hi_mask) == st.prefix && key >= floor_key) {
+                    const uint32_t d = (key >> shift) & ((1u << width) - 1u);
+                    if (PHASE == 0) {
+                        atomicAdd(&lcnt[d], 1u);
+                    } else {
+                        atomicAdd(&lmass[d], smp_mass(w[j], m));
+                    }
                 }
             }
         }
     }
     __syncthreads();
+    unsigned long long* h = ws.hist + static_cast<size_t>(step) * kDigits;
     for (int d = threadIdx.x; d < kDigits; d += kThreads) {
-        if (phase == 0 && lcnt[d] != 0u) {
-            __hip_atomic_fetch_add(ws.hcnt + d, lcnt[d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long v = PHASE == 0 ? static_cast<unsigned long long>(lcnt[d]) : lmass[d];
+        if (v != 0ull) {
+            __hip_atomic_fetch_add(h + d, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        if (phase == 1 && lmass[d] != 0ull) {
-            __hip_atomic_fetch_add(ws.hmass + d, lmass[d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-    // the last workgroup to arrive sees every workgroup's additions
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t done = __hip_atomic_fetch_add(&ws.plan->arrive, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last_l = done == gridDim.x - 1u ? 1u : 0u;
-    }
-    __syncthreads();
-    if (last_l == 0u) {
-        return;
-    }
-    __threadfence();
-    // digits 8t .. 8t + 7 per thread: values, their sum, and a suffix scan
-    // over the threads (high digits first) of the sums
-    constexpr int kPer = kDigits / kThreads;
-    unsigned long long val[kPer];
-    unsigned long long tsum = 0ull;
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        const int d = threadIdx.x * kPer + j;
-        val[j] = phase == 0 ? static_cast<unsigned long long>(coherent_load(ws.hcnt + d)) : coherent_load(ws.hmass + d);
-        tsum += val[j];
-        if (phase == 0) {
-            __hip_atomic_store(ws.hcnt + d, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-            __hip_atomic_store(ws.hmass + d, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-    sum_l[threadIdx.x] = tsum;
-    if (threadIdx.x == 0) {
-        pick_l = 0u;  // 1 + the chosen digit (0: none yet)
-    }
-    __syncthreads();
-    unsigned long long base = round == 0 ? 0ull : coherent_load(&ws.plan->base);
-    unsigned long long target;
-    if (round == 0) {
-        if (phase == 0) {
-            target = p.top_k;
-        } else {
-            unsigned long long z = 0ull;
-            for (int t = 0; t < kThreads; ++t) {
-                z += sum_l[t];
-            }
-            target = smp_mass_target(z, p.top_p);
-        }
-    } else {
-        target = coherent_load(&ws.plan->target);
-    }
-    // the mass / count above this thread's digits (threads above it, in order)
-    unsigned long long above = base;
-    for (int t = kThreads - 1; t > static_cast<int>(threadIdx.x); --t) {
-        above += sum_l[t];
-    }
-    // the highest digit d with above(d) + val(d) >= target
-    uint32_t mine = 0xffffffffu;
-    unsigned long long mine_above = 0ull;
-#pragma unroll
-    for (int j = kPer - 1; j >= 0; --j) {
-        if (mine == 0xffffffffu && above + val[j] >= target) {
-            mine = static_cast<uint32_t>(threadIdx.x * kPer + j);
-            mine_above = above;
-        }
-        above += val[j];
-    }
-    if (mine != 0xffffffffu) {
-        atomicMax(&pick_l, mine + 1u);  // LDS: the highest qualifying digit
-    }
-    __syncthreads();
-    const uint32_t d = pick_l - 1u;
-    if (pick_l != 0u && mine == d) {
-        // (exactly one thread: the digit's owner)
-        const uint32_t key = prefix | (d << shift);
-        SmpPlan* pl = ws.plan;
-        if (round < 2) {
-            __hip_atomic_store(&pl->prefix, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&pl->base, mine_above, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&pl->target, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-            // the phase's threshold: the next phase starts from a clean band
-            __hip_atomic_store(&pl->prefix, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&pl->base, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&pl->target, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (phase == 0) {
-                __hip_atomic_store(&pl->restrict_key, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            __hip_atomic_store(&pl->tau_key, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (final_round) {
-                __hip_atomic_store(&pl->max_key, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(&pl->restrict_key, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-    }
-    if (threadIdx.x == 0) {
-        __hip_atomic_store(&ws.plan->arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
-// The Gumbel-max over {w >= tau}, folded into the key word; the last
-// workgroup clears the threshold word (the workspace is left zero).
-__global__ __launch_bounds__(kThreads) void k_smp_draw(uint32_t n, mh_sample_params p, SmpWs ws,
+// Decides the last round (step `last`: phase pp, round 2), then folds the
+// Gumbel-max over {w >= tau} into the key word; zeroes the first round's
+// histogram for the next call.
+__global__ __launch_bounds__(kThreads) void k_smp_draw(uint32_t n, mh_sample_params p, SmpWs ws, int last, int pp,
                                                        unsigned long long* best) {
     __shared__ unsigned long long part[kThreads / 64];
-    __shared__ uint32_t last_l;
-    const uint32_t tau = coherent_load(&ws.plan->tau_key);
-    const uint32_t q = blockIdx.x * kThreads + threadIdx.x;
-    const uint32_t i0 = 4u * q;
-    unsigned long long k = 0ull;
-    if (i0 < n) {
-        const float4 w4 = *reinterpret_cast<const float4*>(ws.w + i0);
-        const float w[4] = {w4.x, w4.y, w4.z, w4.w};
-        const mh::u32x4 r = mh::philox4x32_10(mh::u32x4{q, p.pos, kDomain, 0u}, p.seed_lo, p.seed_hi);
-        const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
+    __shared__ SmpDecideLds dl;
+    float4 w4[kGroups];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (smp_fkey(w[j]) >= tau) {
-                const unsigned long long kj = mh::argmax_key(w[j] + mh::gumbel_of(rw[j]), i0 + j);
-                k = kj > k ? kj : k;
+    for (int g = 0; g < kGroups; ++g) {
+        const uint32_t i0 = smp_token0(g);
+        w4[g] = i0 < n ? *reinterpret_cast<const float4*>(ws.w + i0) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    const SmpPrev pv = smp_prev_load(ws, last);
+    // the perturbed values (w + G) while the loads are in flight
+    float y[kGroups][4];
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+        const uint32_t i0 = smp_token0(g);
+        const mh::u32x4 r = mh::philox4x32_10(mh::u32x4{i0 / 4u, p.pos, kDomain, 0u}, p.seed_lo, p.seed_hi);
+        y[g][0] = mh::gumbel_of(r.x);
+        y[g][1] = mh::gumbel_of(r.y);
+        y[g][2] = mh::gumbel_of(r.z);
+        y[g][3] = mh::gumbel_of(r.w);
+    }
+    const uint32_t tau = smp_decide(pv, pp, 2, p, dl).tau_key;
+    for (uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < kDigits; i += gridDim.x * kThreads) {
+        ws.hist[i] = 0ull;
+    }
+    unsigned long long k = 0ull;
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+        const uint32_t i0 = smp_token0(g);
+        if (i0 < n) {
+            const float w[4] = {w4[g].x, w4[g].y, w4[g].z, w4[g].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (smp_fkey(w[j]) >= tau) {
+                    const unsigned long long kj = mh::argmax_key(w[j] + y[g][j], i0 + j);
+                    k = kj > k ? kj : k;
+                }
             }
         }
     }
@@ -375,13 +492,6 @@ __global__ __launch_bounds__(kThreads) void k_smp_draw(uint32_t n, mh_sample_par
         if (k != 0ull && k > __hip_atomic_load(best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
             __hip_atomic_fetch_max(best, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        const uint32_t done = __hip_atomic_fetch_add(&ws.plan->arrive, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last_l = done == gridDim.x - 1u ? 1u : 0u;
-    }
-    __syncthreads();
-    if (last_l != 0u && threadIdx.x == 0) {
-        __hip_atomic_store(&ws.plan->tau_key, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&ws.plan->arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -420,21 +530,36 @@ extern "C" int mh_sample_draw(const uint16_t* logits, uint32_t n, const uint32_t
     MH_ENSURE(mh::aligned(workspace, 256), MH_ERR_ALIGN, "%s: workspace not 256-byte aligned", op);
     const SmpWs ws = smp_layout(workspace, n);
     const hipStream_t s = mh::as_stream(stream);
-    const uint32_t grid = (n + kBlock - 1u) / kBlock;
-    hipLaunchKernelGGL(k_smp_prep, dim3(grid), dim3(kThreads), 0, s, logits, n, seen, *params, ws);
+    const uint32_t grid = smp_grid(n);
+    if (use_k) {
+        hipLaunchKernelGGL(k_smp_prep<true>, dim3(grid), dim3(kThreads), 0, s, logits, n, seen, *params, ws);
+    } else {
+        hipLaunchKernelGGL(k_smp_prep<false>, dim3(grid), dim3(kThreads), 0, s, logits, n, seen, *params, ws);
+    }
     MH_TRY(mh::launch_status("k_smp_prep"));
+    // the rounds of this call: (phase, round); a count round 0 ran in prep
+    int step = 0, pp = 0, pr = 0;
     for (int phase = 0; phase < 2; ++phase) {
         if ((phase == 0 && !use_k) || (phase == 1 && !use_p)) {
             continue;
         }
         for (int round = 0; round < 3; ++round) {
-            const int final_round = round == 2 && (phase == 1 || !use_p) ? 1 : 0;
-            hipLaunchKernelGGL(k_smp_round, dim3(grid), dim3(kThreads), 0, s, n, *params, ws, phase, round,
-                               final_round);
-            MH_TRY(mh::launch_status("k_smp_round"));
+            if (!(phase == 0 && round == 0)) {
+                if (phase == 0) {
+                    hipLaunchKernelGGL(k_smp_round<0>, dim3(grid), dim3(kThreads), 0, s, n, *params, ws, step, round,
+                                       pp, pr);
+                } else {
+                    hipLaunchKernelGGL(k_smp_round<1>, dim3(grid), dim3(kThreads), 0, s, n, *params, ws, step, round,
+                                       pp, pr);
+                }
+                MH_TRY(mh::launch_status("k_smp_round"));
+            }
+            pp = phase;
+            pr = round;
+            ++step;
         }
     }
-    hipLaunchKernelGGL(k_smp_draw, dim3(grid), dim3(kThreads), 0, s, n, *params, ws,
+    hipLaunchKernelGGL(k_smp_draw, dim3(grid), dim3(kThreads), 0, s, n, *params, ws, step - 1, pp,
                        reinterpret_cast<unsigned long long*>(best));
     return mh::launch_status("k_smp_draw");
 }

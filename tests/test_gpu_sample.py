@@ -53,7 +53,8 @@ def _keys_f32(v):
 def test_sample_draw_bit_exact(dev, orc, n, temp, penalty, top_k, top_p, seed, pos):
     """The kept-set draw's key equals the oracle's bit for bit (integer
     thresholds: counts and fixed-point masses; the draw as the temperature
-    draw), over repeated calls on one workspace, which is left zero."""
+    draw), over repeated calls on one workspace whose scratch part starts as
+    garbage and whose first 16 KiB are left zero."""
     rng = np.random.default_rng(n + top_k + pos)
     v = rng.normal(0, 3, n).astype(np.float32)
     # ties around the k-th largest and exact zeros
@@ -65,7 +66,10 @@ def test_sample_draw_bit_exact(dev, orc, n, temp, penalty, top_k, top_p, seed, p
     seen = rng.integers(0, 2 ** 32, (n + 31) // 32, dtype=np.uint64).astype(np.uint32)
     use_pen = penalty != 1.0
     ws_bytes = hip.sample_workspace_bytes(n)
-    ws = to_dev(np.zeros(ws_bytes, np.uint8))
+    # only the first 16 KiB must start at zero: the rest holds garbage
+    ws_host = np.full(ws_bytes, 0xA5, np.uint8)
+    ws_host[:16384] = 0
+    ws = to_dev(ws_host)
     dl, ds = to_dev(logits), to_dev(seen)
     for call in range(3):
         p = hip.sample_params(temp, seed, pos + call, penalty, top_k, top_p)
@@ -75,7 +79,7 @@ def test_sample_draw_bit_exact(dev, orc, n, temp, penalty, top_k, top_p, seed, p
         hip.sample_draw(dl, n, ds, p, best, ws, ws_bytes)
         got = int(from_dev(best, np.uint64)[0])
         assert got == want, (call, hex(got), hex(want))
-        assert not from_dev(ws, np.uint8)[-4096:].any()  # histogram and plan words left zero
+        assert not from_dev(ws, np.uint8)[:16384].any()  # the first round's histogram left zero
     # the drawn token is in the kept set
     w = layout.bf16_to_f32(logits).astype(np.float32) * np.float32(p.inv_temp)
     tok = (~got) & 0xffffffff
