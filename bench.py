@@ -534,6 +534,8 @@ def main() -> int:
     ap.add_argument("--timeline", type=int, default=0,
                     help="only print the per-phase timeline of config 3's decode step over this many "
                          "launches (device timestamps), then exit")
+    ap.add_argument("--only", choices=("config3", "config4"), default=None,
+                    help="only time this workload, print its line and exit (for profiler runs)")
     ap.add_argument("--eager", action="store_true",
                     help="launch the timed steps directly instead of replaying a graph "
                          "(for counter collection; host launch overhead is then timed)")
@@ -558,6 +560,17 @@ def main() -> int:
     if args.timeline > 0:
         print(json.dumps({"timeline": "config3_moe_decode_step",
                           **timeline_config3(torch, hip, dev, gen, args.timeline)}), flush=True)
+        return 0
+
+    if args.only == "config4":
+        ms4, ms4g = bench_config4(torch, hip, dev, gen, steps, warmup)
+        print(json.dumps({"only": "config4_prefill_moe", "ms_per_step": round(ms4, 4),
+                          "grouped_gemm_only_ms": round(ms4g, 4),
+                          "grouped_gemm_only_tflops": round(FLOPS_CONFIG4 / (ms4g * 1e-3) / 1e12, 2)}), flush=True)
+        return 0
+    if args.only == "config3":
+        ms3 = bench_config3(torch, hip, dev, gen, steps, warmup)
+        print(json.dumps({"only": "config3_moe_decode_step", "ms_per_step": round(ms3, 5)}), flush=True)
         return 0
 
     log("config 2: Q4 LM head + argmax")

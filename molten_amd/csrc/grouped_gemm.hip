@@ -412,10 +412,13 @@ struct SegLayout {
 //   * scales and biases: every 8 stages, 16 bytes (8 groups) of the column's
 //     scale row (lanes 0-31) and bias row (lanes 32-63), two slots.
 // Stage g's loads ("group g": its A, plus the B half-block that starts at g,
-// plus the scale/bias block that starts at g) are issued after the barrier
-// that ends stage g - 3, two stages ahead of use; the wave waits for its own
-// loads of a group (vmcnt) and one barrier per stage publishes the A rows
-// of all four waves.
+// plus the scale/bias block that starts at g) are spread over the MFMA steps
+// 0..2 of stage g - 2, one load after each row block's MFMAs, so the wave's
+// vector-memory issue never holds up a run of MFMAs.  One barrier per stage,
+// before its step 3 (the wave's own loads of group g + 1 waited for, its
+// reads of the stage's A slot done), publishes every wave's group g + 1 and
+// frees the slot that group g + 3 refills; the next stage's first A
+// fragments and B words are then read under step 3's MFMAs.
 template <int RB, int RBMAX, int NS, int NBW, int NMAT, bool GATHER, int EPI>
 __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint32_t n0,
                                          uint32_t mp0, uint32_t m_end, uint32_t lds0, int lane,
@@ -468,6 +471,44 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
             sboff[t] = min(col0 + static_cast<uint32_t>(i32), a.w_rows - 1u) * groups * 2u;
         }
     }
+    // the loads of group g: A load q, then the B codes (one load per
+    // fragment half, even groups) and the scale/bias words (every 8th group);
+    // load i of the group is issued when sel(i) is true
+    auto issue_sel = [&](uint32_t g, auto&& sel) {
+        const uint32_t abuf = __builtin_amdgcn_readfirstlane(lds0 + (g % 3u) * L::A_STAGE + wave * QA * 1024u);
+        const mh::gbytes ag = mh::uniform_ptr(abase + g * 128u);
+#pragma unroll
+        for (int q = 0; q < QA; ++q) {
+            if (sel(q)) {
+                dma16s(ag, aoffs[q], abuf + q * 1024u);
+            }
+        }
+        if ((g & 1u) == 0) {
+            const uint32_t hb = g >> 1;
+            const uint32_t bbuf = __builtin_amdgcn_readfirstlane(lds0 + L::B_OFF + (hb & 1u) * L::B_HALF + wave * NB * 2048u);
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+                const mh::gbytes cg = mh::uniform_ptr(cbase[t / NBW] + hb * 64u);
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    if (sel(QA + 2 * t + p)) {
+                        dma16s(cg, bcoffs[t][p], bbuf + t * 2048u + p * 1024u);
+                    }
+                }
+            }
+        }
+        if ((g & 7u) == 0) {
+            const uint32_t sbk = g >> 3;
+            const uint32_t sbuf = lds0 + L::SB_OFF + (sbk & 1u) * L::SB_BLK + wave * NB * 1024u;
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+                if (sel(QA + 2 * NB + t)) {
+                    const mh::gbytes src = h ? bbase[t / NBW] : sbase[t / NBW];
+                    dma16(src + sboff[t] + sbk * 16u, sbuf + t * 1024u);
+                }
+            }
+        }
+    };
     auto issue_group = [&](uint32_t g) {
         const uint32_t abuf = __builtin_amdgcn_readfirstlane(lds0 + (g % 3u) * L::A_STAGE + wave * QA * 1024u);
         const mh::gbytes ag = mh::uniform_ptr(abase + g * 128u);
@@ -578,11 +619,11 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
         bfr[0][t] = deq_word(bc[t].x, sf[t], s16[t], bf[t]);
     }
     __builtin_amdgcn_s_barrier();
-    if (nkb > 2) {
-        issue_group(2);
-    }
     read_a(0, 0, av[0]);
-    for (uint32_t kb = 0; kb < nkb; ++kb) {
+    // stage kb; LOADS: group kb + 2 exists (its loads are spread over steps
+    // 0..2), NEXT: stage kb + 1 exists
+    auto stage = [&](uint32_t kb, auto loads_c, auto next_c) {
+        constexpr bool LOADS = decltype(loads_c)::value, NEXT = decltype(next_c)::value;
         // steps 0..2: the next step's A reads in flight and its B words
         // dequantized while this step's MFMAs run
 #pragma unroll
@@ -606,15 +647,24 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
                         bfr[nxt][t] = deq_word(wv, sf[t], s16[t], bf[t]);
                     }
                 }
+                // group kb + 2's loads, one after each row block's MFMAs:
+                // load i in step i % 3 after row block (i / 3) % RB
+                if constexpr (LOADS) {
+                    issue_sel(kb + 2, [&](int i) { return i % 3 == j && (i / 3) % RB == rb; });
+                }
             }
         }
-        // step 3; under its MFMAs the wave reads stage kb + 1's B codes and
-        // scale/bias words (its own loads) and dequantizes that stage's step 0
-        const bool next = kb + 1 < nkb;
+        // step 3.  Before it: this wave's loads of group kb + 1 have landed
+        // and its reads of stage kb's A slot are done; one barrier then
+        // publishes every wave's group kb + 1 and frees the slot.  The next
+        // stage's B codes, scale/bias words and first A fragments are read
+        // under step 3's MFMAs, and that stage's step-0 B words dequantized.
         lgkm_wait<0>(av[1]);
-        if (next) {
+        if constexpr (NEXT) {
             wait_own(kb + 1);
+            __builtin_amdgcn_s_barrier();
             read_bsb(kb + 1, bc, sbw);
+            read_a(kb + 1, 0, av[0]);
         }
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
@@ -625,26 +675,28 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
                 for (int cb = 0; cb < NBW; ++cb)
                     acc[mat][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                         bfr[1][mat * NBW + cb], af, acc[mat][rb][cb], 0, 0, 0);
-            if (rb == (RB - 1) / 2 && next) {
-                lgkm_wait<0>(bc);
-                lgkm_wait<0>(sbw);
-                scale_bias(kb + 1, sbw);
+            if constexpr (NEXT) {
+                if (rb == (RB - 1) / 2) {
+                    // (the RB A reads issued after them may still be in flight)
+                    lgkm_wait<RB>(bc);
+                    lgkm_wait<RB>(sbw);
+                    scale_bias(kb + 1, sbw);
 #pragma unroll
-                for (int t = 0; t < NB; ++t) {
-                    bfr[0][t] = deq_word(bc[t].x, sf[t], s16[t], bf[t]);
+                    for (int t = 0; t < NB; ++t) {
+                        bfr[0][t] = deq_word(bc[t].x, sf[t], s16[t], bf[t]);
+                    }
                 }
             }
         }
-        if (next) {
-            // every wave's group kb + 1 has landed and every wave is done with
-            // stage kb's A slot
-            __builtin_amdgcn_s_barrier();
-            if (kb + 3 < nkb) {
-                issue_group(kb + 3);
-            }
-            read_a(kb + 1, 0, av[0]);
-        }
+    };
+    using yes = std::true_type;
+    using no = std::false_type;
+    uint32_t kb = 0;
+    for (; kb + 2 < nkb; ++kb) {
+        stage(kb, yes{}, yes{});
     }
+    stage(kb, no{}, yes{});
+    stage(kb + 1, no{}, no{});
     // every wave is done with the ring before another pass refills it
     __builtin_amdgcn_s_barrier();
 
