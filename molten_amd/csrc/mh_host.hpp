@@ -46,6 +46,17 @@ int check_quant_dequant(const mh_quant_weights* w, const char* op);
 
 // Launch status after hipLaunchKernelGGL.
 // Internal launches of the prefill MoE step (moe_prefill.hip, moe_decode.hip).
+// Prefill routing after the router logits: top-k per token with per-block
+// expert histograms hb (ceil(m / kPrefillRouteBlock) + 1 rows of e words: the blocks, then
+// the totals), their per-expert prefix, then the stable scatter, counts,
+// offsets and both block maps (three launches).
+constexpr uint32_t kPrefillRouteBlock = 16;  // tokens per routing block (histogram row)
+int moe_route_sort_maps(const float* logits, const float* bias, int mode, float eps, uint32_t m,
+                        uint32_t e, uint32_t topk, uint32_t* ids, uint16_t* gw, uint32_t* hb,
+                        uint32_t* counts, uint32_t* offsets, uint32_t* gu_off, uint32_t* dn_off,
+                        uint32_t* ids_sorted, uint32_t* slotpos, uint32_t* gu, uint32_t max_gu, uint32_t* dn,
+                        uint32_t max_dn, uint32_t bm, uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n,
+                        uint32_t dn_n, mh_stream_t stream);
 int moe_sort_maps(const uint32_t* ids, uint32_t s, uint32_t e, uint32_t topk, uint32_t* counts,
                   uint32_t* offsets, uint32_t* gu_off, uint32_t* dn_off, uint32_t* ids_sorted,
                   uint32_t* slotpos, uint32_t* gu, uint32_t max_gu, uint32_t* dn, uint32_t max_dn,
@@ -61,9 +72,8 @@ int moe_decode_fused(const void* router, int router_dtype, const float* bias, in
 uint32_t moe_decode_fused_waves();
 int gemv_mfma(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint64_t* slots, uint32_t* ids,
               uint32_t batch, hipStream_t stream);
-int router_prefill_route(const uint16_t* x, const void* w, int w_dtype, float* logits,
-                         const float* bias, uint32_t* ids, uint16_t* gw, uint32_t m, uint32_t k,
-                         uint32_t e, uint32_t topk, int mode, float eps, mh_stream_t stream);
+int router_prefill_logits(const uint16_t* x, const void* w, int w_dtype, float* logits, uint32_t m,
+                          uint32_t k, uint32_t e, mh_stream_t stream);
 
 inline int launch_status(const char* what) {
     const hipError_t e = hipGetLastError();

@@ -64,7 +64,6 @@ struct DenseArgs {
     uint32_t topk;
     int mode;
     float eps;
-    uint32_t route_rows;  // k_dense_rows: also route each token (ids/weights [m, topk])
 };
 
 // Stage x rows [t0, t0 + nt) into LDS as padded f32 chunks, one 32-element
@@ -176,111 +175,153 @@ __global__ __launch_bounds__(kThreads) void k_dense_gemv(DenseArgs a) {
     }
 }
 
-// Many tokens, K <= 2048 (the prefill router): a workgroup owns 4 tokens,
-// each wave a quarter of the experts.  A wave keeps the tokens' x chunks in
-// registers (lane c holds chunk c), streams its experts' rows (the next row's
-// loads in flight during the current row's fmas), reduces the four tokens'
-// chunk sums in one 4-row butterfly and gathers expert e's logits into lane
-// e % 64 of a per-token register; the logits are stored with one coalesced
-// store per token.  Same chunk order as k_dense_gemv.
-constexpr int kRowTokens = 4;
-constexpr int kMaxExpertGroups = mh::kMaxExperts / 64;
+// Router logits of many tokens, tiled: a workgroup takes kRtTokens tokens
+// and kRtExperts experts; the experts' rows are staged once in the LDS as
+// f32 (chunk c of row e as 8 pieces of 16 bytes, piece q at q ^ ((c >> 1) &
+// 7), so the 16 lanes of a 16-byte read cover all 64 banks once), then each
+// wave runs its tokens in groups of four with x in registers (lane c holds
+// chunk c) against one expert row at a time from the LDS (the next row's
+// read in flight; two workgroups per CU cover each other's waits).  Per
+// (token, expert) the arithmetic is the chunk order of k_dense_gemv: lane
+// c's fma chain over its 32 elements from 0, then the xor butterfly over the
+// 64 chunks (four tokens in one 4-row butterfly); W comes from the L2 once
+// per workgroup.
+constexpr int kRtTokens = 64;
+constexpr int kRtExperts = 8;
+constexpr int kRtGroup = 4;                                // tokens per group
+constexpr int kRtGroups = kRtTokens / (kRtGroup * kWaves);  // groups per wave
 
 template <typename WT>
-__global__ __launch_bounds__(kThreads) void k_dense_rows(DenseArgs a) {
+__global__ __launch_bounds__(kThreads, 2) void k_router_tiles(DenseArgs a) {
+    extern __shared__ float wl[];  // [kRtExperts][C][8 pieces][4]
+    __shared__ float zl[kRtTokens][kRtExperts];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t C = a.k / 32u;
     const bool live = lane < static_cast<int>(C);
     const uint32_t c = live ? lane : 0u;
-    const uint32_t t0 = blockIdx.x * kRowTokens;
-    const uint32_t per_wave = (a.n + kWaves - 1) / kWaves;
-    const uint32_t e_begin = wave * per_wave;
-    const uint32_t e_end = min(a.n, e_begin + per_wave);
-    float out[kMaxExpertGroups][kRowTokens];
+    const uint32_t t_base = blockIdx.x * kRtTokens;
+    const uint32_t e0 = blockIdx.y * kRtExperts;
+    const uint32_t ne = min(static_cast<uint32_t>(kRtExperts), a.n - e0);
+    const uint32_t t_wave = static_cast<uint32_t>(wave * kRtGroup * kRtGroups);
+    auto load_group = [&](int g, uint32_t (&xw)[kRtGroup][16]) {
 #pragma unroll
-    for (int g = 0; g < kMaxExpertGroups; ++g)
+        for (int t = 0; t < kRtGroup; ++t) {
+            const uint32_t tok = min(t_base + t_wave + static_cast<uint32_t>(kRtGroup * g + t), a.m - 1u);
+            const uint4* xv = reinterpret_cast<const uint4*>(a.x + static_cast<size_t>(tok) * a.k + 32u * c);
 #pragma unroll
-        for (int t = 0; t < kRowTokens; ++t) out[g][t] = 0.0f;
-    if (e_begin < e_end) {
-        float xr[kRowTokens][32];
-#pragma unroll
-        for (int t = 0; t < kRowTokens; ++t) {
-            const uint32_t tok = min(t0 + t, a.m - 1u);
-            float xs;
-            mh::load_x_chunk(a.x + static_cast<size_t>(tok) * a.k + 32u * c, xr[t], xs);
-        }
-        const WT* w = static_cast<const WT*>(a.w) + 32u * c;
-        mh::RowWords<WT> cur, nxt;
-        cur.load(w + static_cast<size_t>(e_begin) * a.k);
-        for (uint32_t e = e_begin; e < e_end; ++e) {
-            if (e + 1 < e_end) {
-                nxt.load(w + static_cast<size_t>(e + 1) * a.k);
-            }
-            float wr[32];
-            cur.to_f32(wr);
-            float h[kRowTokens];
-#pragma unroll
-            for (int t = 0; t < kRowTokens; ++t) {
-                float p = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 32; ++i) {
-                    p = __builtin_fmaf(wr[i], xr[t][i], p);
-                }
-                h[t] = live ? 0.0f + p : 0.0f;
-            }
-            const float v = mh::reduce_rows4(h, lane);
-            const uint32_t g = e >> 6, le = e & 63u;
-#pragma unroll
-            for (int t = 0; t < kRowTokens; ++t) {
-                const float vt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 60 + t));
-#pragma unroll
-                for (int gg = 0; gg < kMaxExpertGroups; ++gg) {
-                    if (gg == static_cast<int>(g) && static_cast<uint32_t>(lane) == le) {
-                        out[gg][t] = vt;
-                    }
-                }
-            }
-            cur = nxt;
-        }
-#pragma unroll
-        for (int t = 0; t < kRowTokens; ++t) {
-            if (t0 + t < a.m) {
-#pragma unroll
-                for (int g = 0; g < kMaxExpertGroups; ++g) {
-                    const uint32_t e = g * 64u + lane;
-                    if (e >= e_begin && e < e_end) {
-                        a.y[static_cast<size_t>(t0 + t) * a.n + e] = out[g][t];
-                    }
-                }
+            for (int q = 0; q < 4; ++q) {
+                const uint4 v = xv[q];
+                xw[t][4 * q] = v.x; xw[t][4 * q + 1] = v.y; xw[t][4 * q + 2] = v.z; xw[t][4 * q + 3] = v.w;
             }
         }
+    };
+    // stage rows e0 .. e0 + ne: 8 elements (two pieces) per thread and step
+    const WT* w = static_cast<const WT*>(a.w);
+    for (uint32_t i = threadIdx.x; i < ne * C * 4u; i += kThreads) {
+        const uint32_t e = i / (C * 4u), r = i % (C * 4u), cc = r / 4u, q2 = r % 4u;
+        const size_t src = static_cast<size_t>(e0 + e) * a.k + 32u * cc + 8u * q2;
+        float v[8];
+        if constexpr (sizeof(WT) == 4) {
+            const float4 lo = *reinterpret_cast<const float4*>(w + src);
+            const float4 hi = *reinterpret_cast<const float4*>(w + src + 4);
+            v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+            v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+        } else {
+            const uint4 u = *reinterpret_cast<const uint4*>(w + src);
+            const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[2 * j] = mh::bf16lo(uw[j]);
+                v[2 * j + 1] = mh::bf16hi(uw[j]);
+            }
+        }
+        const uint32_t swz = (cc >> 1) & 7u;
+        float* base = wl + static_cast<size_t>(e * C + cc) * 32u;
+        *reinterpret_cast<float4*>(base + 4u * ((2u * q2) ^ swz)) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4*>(base + 4u * ((2u * q2 + 1u) ^ swz)) = make_float4(v[4], v[5], v[6], v[7]);
     }
-    if (!a.route_rows) {
-        return;
-    }
-    // routing of the workgroup's tokens: logits through LDS, one wave per token
-    __shared__ float zl[kRowTokens][mh::kMaxExperts];
-    __shared__ float ss[kRowTokens][mh::kMaxExperts], cc[kRowTokens][mh::kMaxExperts];
-#pragma unroll
-    for (int t = 0; t < kRowTokens; ++t)
-#pragma unroll
-        for (int g = 0; g < kMaxExpertGroups; ++g) {
-            const uint32_t e = g * 64u + lane;
-            if (e >= e_begin && e < e_end) {
-                zl[t][e] = out[g][t];
-            }
-        }
     __syncthreads();
-    const uint32_t t = static_cast<uint32_t>(wave);
-    if (t < static_cast<uint32_t>(kRowTokens) && t0 + t < a.m) {
-        for (uint32_t i = lane; i < a.n; i += 64) {
-            mh::route_score(zl[t][i], a.bias ? a.bias[i] : 0.0f, a.mode, ss[t][i], cc[t][i]);
+    const uint32_t swz = (c >> 1) & 7u;
+    auto read_row = [&](uint32_t e, float (&wr)[32]) {
+        const float* base = wl + static_cast<size_t>(e * C + c) * 32u;
+#pragma unroll
+        for (uint32_t q = 0; q < 8; ++q) {
+            const float4 v = *reinterpret_cast<const float4*>(base + 4u * (q ^ swz));
+            wr[4 * q] = v.x; wr[4 * q + 1] = v.y; wr[4 * q + 2] = v.z; wr[4 * q + 3] = v.w;
         }
-        mh::route_select(ss[t], cc[t], a.n, a.topk, a.mode, a.eps,
-                         a.ids + static_cast<size_t>(t0 + t) * a.topk,
-                         a.weights + static_cast<size_t>(t0 + t) * a.topk);
+    };
+#pragma unroll 1
+    for (int g = 0; g < kRtGroups; ++g) {
+        float xr[kRtGroup][32];
+        {
+            uint32_t xw[kRtGroup][16];
+            load_group(g, xw);
+#pragma unroll
+            for (int t = 0; t < kRtGroup; ++t) {
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    xr[t][2 * q] = mh::bf16lo(xw[t][q]);
+                    xr[t][2 * q + 1] = mh::bf16hi(xw[t][q]);
+                }
+            }
+        }
+        auto expert = [&](uint32_t e, const float (&wr)[32]) {
+#pragma unroll
+            for (int half = 0; half < kRtGroup / 4; ++half) {
+                float h[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    float p = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 32; ++i) {
+                        p = __builtin_fmaf(wr[i], xr[4 * half + t][i], p);
+                    }
+                    h[t] = live ? 0.0f + p : 0.0f;
+                }
+                const float v = mh::reduce_rows4(h, lane);
+                if (lane >= 60) {
+                    zl[t_wave + kRtGroup * g + 4 * half + (lane - 60)][e] = v;
+                }
+            }
+        };
+        // two row buffers, the next row's read in flight
+        float wa[32], wb[32];
+        read_row(0, wa);
+        for (uint32_t e = 0; e < ne; e += 2) {
+            if (e + 1 < ne) {
+                read_row(e + 1, wb);
+            }
+            expert(e, wa);
+            if (e + 1 < ne) {
+                if (e + 2 < ne) {
+                    read_row(e + 2, wa);
+                }
+                expert(e + 1, wb);
+            }
+        }
     }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < kRtTokens * ne; i += kThreads) {
+        const uint32_t t = i / ne, e = i % ne;
+        if (t_base + t < a.m) {
+            a.y[static_cast<size_t>(t_base + t) * a.n + e0 + e] = zl[t][e];
+        }
+    }
+}
+
+template <typename WT>
+int launch_router_tiles(const DenseArgs& a, hipStream_t stream) {
+    const uint32_t C = a.k / 32u;
+    const size_t lds = static_cast<size_t>(kRtExperts) * C * 32u * sizeof(float);
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_router_tiles<WT>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess) {
+        return mh::hip_error(e, "k_router_tiles: LDS attribute");
+    }
+    const dim3 grid((a.m + kRtTokens - 1) / kRtTokens, (a.n + kRtExperts - 1) / kRtExperts);
+    hipLaunchKernelGGL(k_router_tiles<WT>, grid, dim3(kThreads), lds, stream, a);
+    return mh::launch_status("k_router_tiles");
 }
 
 // Decode router logits only (the routing runs in the expert kernel): one
@@ -344,10 +385,8 @@ int dispatch_dense(const DenseArgs& a, hipStream_t stream) {
     if (a.m == 1) {
         return launch_dense<WT, 1, 1>(a, stream);
     }
-    if (a.k <= 2048u && a.n <= static_cast<uint32_t>(mh::kMaxExperts) && a.done == nullptr) {
-        hipLaunchKernelGGL(k_dense_rows<WT>, dim3((a.m + kRowTokens - 1) / kRowTokens), dim3(kThreads), 0,
-                           stream, a);
-        return mh::launch_status("k_dense_rows");
+    if (a.k <= 2048u && a.done == nullptr) {
+        return launch_router_tiles<WT>(a, stream);
     }
     return launch_dense<WT, 8, 4>(a, stream);
 }
@@ -906,35 +945,16 @@ int mh_route_token(const float* logits, const float* bias, uint32_t* ids, uint16
 
 namespace mh {
 
-// Prefill router and routing in one launch (mh_moe_prefill's first step).
-int router_prefill_route(const uint16_t* x, const void* w, int w_dtype, float* logits,
-                         const float* bias, uint32_t* ids, uint16_t* gw, uint32_t m, uint32_t k,
-                         uint32_t e, uint32_t topk, int mode, float eps, mh_stream_t stream) {
+// Prefill router logits (mh_moe_prefill's first step; the routing follows).
+int router_prefill_logits(const uint16_t* x, const void* w, int w_dtype, float* logits, uint32_t m,
+                          uint32_t k, uint32_t e, mh_stream_t stream) {
     const char* op = "mh_moe_prefill (router)";
     MH_ENSURE(w_dtype == MH_DTYPE_F32 || w_dtype == MH_DTYPE_BF16, MH_ERR_INVALID,
               "%s: router dtype %d", op, w_dtype);
-    MH_TRY(route_checks(op, logits, ids, gw, m, e, topk, mode));
     DenseArgs a;
     MH_TRY(dense_common(op, w, w_dtype == MH_DTYPE_F32, x, logits, m, e, k, a));
-    if (k > 2048u) {  // the register-resident rows kernel needs one chunk per lane
-        MH_TRY(w_dtype == MH_DTYPE_F32 ? dispatch_dense<float>(a, mh::as_stream(stream))
-                                       : dispatch_dense<uint16_t>(a, mh::as_stream(stream)));
-        return mh_moe_route_batch(logits, bias, ids, gw, m, e, topk, mode, eps, stream);
-    }
-    a.bias = bias;
-    a.ids = ids;
-    a.weights = gw;
-    a.topk = topk;
-    a.mode = mode;
-    a.eps = eps;
-    a.route_rows = 1u;
-    const dim3 grid((m + kRowTokens - 1) / kRowTokens);
-    if (w_dtype == MH_DTYPE_F32) {
-        hipLaunchKernelGGL(k_dense_rows<float>, grid, dim3(kThreads), 0, mh::as_stream(stream), a);
-    } else {
-        hipLaunchKernelGGL(k_dense_rows<uint16_t>, grid, dim3(kThreads), 0, mh::as_stream(stream), a);
-    }
-    return mh::launch_status("k_dense_rows (routed)");
+    return w_dtype == MH_DTYPE_F32 ? dispatch_dense<float>(a, mh::as_stream(stream))
+                                   : dispatch_dense<uint16_t>(a, mh::as_stream(stream));
 }
 
 }  // namespace mh

@@ -8,6 +8,7 @@
 // stable in slot order (token-major, rank-major), like the reference's.
 #include "mh_device.hpp"
 #include "mh_host.hpp"
+#include "mh_route.hpp"
 
 namespace {
 
@@ -269,6 +270,193 @@ __global__ __launch_bounds__(1024) void k_sorted_blocks(const uint32_t* ids, con
     scatter_expert(ids, ex, offsets[ex], ids_sorted, slotpos, s, topk);
 }
 
+// Prefill routing in three launches after the router logits (kRouteBlock
+// tokens per block; one block's slots fit one 256-thread workgroup).
+//
+// k_route_hist: workgroup j routes tokens [16 j, 16 j + 16), one per wave,
+// with the scores in registers (lane l holds experts l + 64 i) and the
+// selection and weights of route_select_ids / route_weights_regs; it writes
+// the ids and weights and the block's expert histogram hb[j][0 .. e).
+constexpr uint32_t kRouteBlock = mh::kPrefillRouteBlock;
+
+template <int TK, int EB>
+__global__ __launch_bounds__(1024) void k_route_hist(const float* logits, const float* bias, uint32_t m,
+                                                     uint32_t e, int mode, float eps, uint32_t* ids, uint16_t* gw,
+                                                     uint32_t* hb) {
+    __shared__ uint32_t hist[mh::kMaxExperts];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t t0 = blockIdx.x * kRouteBlock;
+    const uint32_t nt = min(kRouteBlock, m - t0);
+    for (uint32_t i = threadIdx.x; i < e; i += blockDim.x) {
+        hist[i] = 0u;
+    }
+    const uint32_t t = t0 + min(wave, nt - 1u);
+    float sc[EB], cd[EB];
+#pragma unroll
+    for (int q = 0; q < EB; ++q) {
+        const uint32_t i = lane + 64u * q;
+        sc[q] = 0.0f;
+        cd[q] = -__builtin_inff();
+        if (i < e) {
+            mh::route_score(logits[static_cast<size_t>(t) * e + i], bias ? bias[i] : 0.0f, mode, sc[q], cd[q]);
+        }
+    }
+    uint32_t idv[TK];
+    float sv[TK];
+    mh::route_select_ids<TK, EB>(sc, cd, idv, sv);
+    uint32_t wb[TK];
+    mh::route_weights_regs<TK>(sv, mode, eps, wb);
+    __syncthreads();
+    if (wave < nt && lane < static_cast<uint32_t>(TK)) {
+        uint32_t x = idv[0], w = wb[0];
+#pragma unroll
+        for (int r = 1; r < TK; ++r) {
+            x = lane == static_cast<uint32_t>(r) ? idv[r] : x;
+            w = lane == static_cast<uint32_t>(r) ? wb[r] : w;
+        }
+        ids[static_cast<size_t>(t) * TK + lane] = x;
+        gw[static_cast<size_t>(t) * TK + lane] = static_cast<uint16_t>(w);
+        atomicAdd(&hist[x], 1u);
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < e; i += blockDim.x) {
+        hb[static_cast<size_t>(blockIdx.x) * e + i] = hist[i];
+    }
+}
+
+// Exclusive prefix over a 256-thread workgroup (one value per thread);
+// *total the sum.  Ends with a barrier.
+__device__ __forceinline__ uint32_t block_excl_scan_256(uint32_t v, uint32_t* total) {
+    __shared__ uint32_t wtot[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t inc = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t o = __shfl_up(inc, d);
+        if (lane >= d) inc += o;
+    }
+    if (lane == 63) wtot[wave] = inc;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t t = wtot[w];
+        before += w < wave ? t : 0u;
+        all += t;
+    }
+    __syncthreads();
+    *total = all;
+    return before + inc - v;
+}
+
+// k_hist_prefix: workgroup x scans expert x's column of the block
+// histograms in block order: hb[b][x] becomes the count of expert x's slots
+// in blocks before b (in place), tot[x] the expert's total.
+__global__ __launch_bounds__(256) void k_hist_prefix(uint32_t* hb, uint32_t* tot, uint32_t nblk, uint32_t e) {
+    const uint32_t x = blockIdx.x;
+    uint32_t carry = 0u;
+    for (uint32_t b0 = 0; b0 < nblk; b0 += 256u) {
+        const uint32_t b = b0 + threadIdx.x;
+        const uint32_t v = b < nblk ? hb[static_cast<size_t>(b) * e + x] : 0u;
+        uint32_t all;
+        const uint32_t before = block_excl_scan_256(v, &all);
+        if (b < nblk) {
+            hb[static_cast<size_t>(b) * e + x] = carry + before;
+        }
+        carry += all;
+    }
+    if (threadIdx.x == 0) {
+        tot[x] = carry;
+    }
+}
+
+// k_scatter_maps: workgroup j takes the expert totals (counts, offsets and
+// both block-map offsets by two workgroup scans) and its block's prefix row,
+// scatters block j's slots stably (slot order; ranks within each 64-slot
+// chunk from ballots), writes the block-map entries of experts j, j + G, ...
+// and zeroes its share of both maps' unused tails.  Workgroup 0 writes
+// counts, offsets and the block-map offsets.
+__global__ __launch_bounds__(256) void k_scatter_maps(const uint32_t* ids, const uint32_t* pre, const uint32_t* tot,
+                                                      uint32_t m, uint32_t e, uint32_t topk, uint32_t* counts,
+                                                      uint32_t* offsets, uint32_t* gu_off, uint32_t* dn_off,
+                                                      uint32_t* ids_sorted, uint32_t* slotpos, uint4* gu,
+                                                      uint32_t max_gu, uint4* dn, uint32_t max_dn, uint32_t bm,
+                                                      uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n, uint32_t dn_n) {
+    __shared__ uint32_t tot_l[mh::kMaxExperts], off_l[mh::kMaxExperts], base_l[mh::kMaxExperts],
+        rb_l[mh::kMaxExperts];
+    __shared__ uint32_t chist[4][mh::kMaxExperts];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t j = blockIdx.x;
+    const uint32_t total = tid < e ? tot[tid] : 0u;
+    const uint32_t before = tid < e ? pre[static_cast<size_t>(j) * e + tid] : 0u;
+    // this block's slots (at most 256, one per thread)
+    const uint32_t s0 = j * kRouteBlock * topk;
+    const uint32_t ns = min(kRouteBlock, m - j * kRouteBlock) * topk;
+    const bool act = tid < ns;
+    const uint32_t v = act ? ids[s0 + tid] : 0xffffffffu;
+    uint32_t all;
+    const uint32_t off = block_excl_scan_256(total, &all);
+    const uint32_t rows = tid < e ? (total + bm - 1u) / bm : 0u;
+    uint32_t rows_all;
+    const uint32_t rbefore = block_excl_scan_256(rows, &rows_all);
+    const uint32_t gu_tiles = gu_n / gu_bn, dn_tiles = dn_n / dn_bn;
+    if (tid < e) {
+        tot_l[tid] = total;
+        off_l[tid] = off;
+        base_l[tid] = off + before;
+        rb_l[tid] = rbefore;
+        if (j == 0) {
+            counts[tid] = total;
+            offsets[tid] = off;
+            gu_off[tid] = rbefore * gu_tiles;
+            dn_off[tid] = rbefore * dn_tiles;
+        }
+    }
+    for (uint32_t i = tid; i < 4u * mh::kMaxExperts; i += 256u) {
+        (&chist[0][0])[i] = 0u;
+    }
+    __syncthreads();
+    // block-map entries of experts j, j + G, ...
+    for (uint32_t ex = j; ex < e; ex += gridDim.x) {
+        if (tot_l[ex] != 0u) {
+            write_map(gu, max_gu, rb_l[ex] * gu_tiles, tot_l[ex], off_l[ex], ex, bm, gu_bn, gu_n);
+            write_map(dn, max_dn, rb_l[ex] * dn_tiles, tot_l[ex], off_l[ex], ex, bm, dn_bn, dn_n);
+        }
+    }
+    // the maps' unused tails
+    for (uint32_t i = rows_all * gu_tiles + j * 256u + tid; i < max_gu; i += gridDim.x * 256u) {
+        gu[i] = make_uint4(0, 0, 0, 0);
+    }
+    for (uint32_t i = rows_all * dn_tiles + j * 256u + tid; i < max_dn; i += gridDim.x * 256u) {
+        dn[i] = make_uint4(0, 0, 0, 0);
+    }
+    // rank within the wave's 64-slot chunk by ballots over the distinct experts
+    const unsigned long long below = (1ull << lane) - 1ull;
+    unsigned long long todo = __ballot(act);
+    uint32_t rank = 0u;
+    while (todo != 0ull) {
+        const int leader = __ffsll(static_cast<long long>(todo)) - 1;
+        const uint32_t lv = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), leader));
+        const unsigned long long same = __ballot(v == lv);
+        if (v == lv) {
+            rank = static_cast<uint32_t>(__popcll(same & below));
+        }
+        if (lane == static_cast<uint32_t>(leader)) {
+            chist[wave][lv] = static_cast<uint32_t>(__popcll(same));
+        }
+        todo &= ~same;
+    }
+    __syncthreads();
+    if (act) {
+        uint32_t pos = base_l[v] + rank;
+        for (uint32_t c = 0; c < wave; ++c) {
+            pos += chist[c][v];
+        }
+        ids_sorted[pos] = (s0 + tid) / topk;
+        slotpos[s0 + tid] = pos;
+    }
+}
+
 unsigned grid_for(size_t n, unsigned per = 256) {
     const size_t want = (n + per - 1) / per;
     const size_t cap = static_cast<size_t>(mh::cu_count()) * 16;
@@ -360,6 +548,45 @@ namespace mh {
 
 // Internal to mh_moe_prefill (declared in mh_host.hpp, not in the public
 // header): the two fused routing launches above.
+int moe_route_sort_maps(const float* logits, const float* bias, int mode, float eps, uint32_t m,
+                        uint32_t e, uint32_t topk, uint32_t* ids, uint16_t* gw, uint32_t* hb,
+                        uint32_t* counts, uint32_t* offsets, uint32_t* gu_off, uint32_t* dn_off,
+                        uint32_t* ids_sorted, uint32_t* slotpos, uint32_t* gu, uint32_t max_gu, uint32_t* dn,
+                        uint32_t max_dn, uint32_t bm, uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n,
+                        uint32_t dn_n, mh_stream_t stream) {
+    static_assert(kRouteBlock * mh::kMaxTopk <= 256, "a block's slots, one per thread");
+    MH_ENSURE(e >= 1 && e <= static_cast<uint32_t>(mh::kMaxExperts) && topk >= 1 &&
+                  topk <= static_cast<uint32_t>(mh::kMaxTopk) && topk <= e,
+              MH_ERR_INVALID, "prefill routing: %u experts, top-%u", e, topk);
+    const hipStream_t st = mh::as_stream(stream);
+    const uint32_t nblk = (m + kRouteBlock - 1u) / kRouteBlock;
+    const bool eb1 = e <= 64u;
+#define MH_ROUTE_HIST(TK)                                                                                   \
+    case TK:                                                                                                \
+        if (eb1) {                                                                                          \
+            hipLaunchKernelGGL((k_route_hist<TK, 1>), dim3(nblk), dim3(1024), 0, st, logits, bias, m, e, mode, \
+                               eps, ids, gw, hb);                                                           \
+        } else {                                                                                            \
+            hipLaunchKernelGGL((k_route_hist<TK, 4>), dim3(nblk), dim3(1024), 0, st, logits, bias, m, e, mode, \
+                               eps, ids, gw, hb);                                                           \
+        }                                                                                                   \
+        break;
+    switch (topk) {
+        MH_ROUTE_HIST(1) MH_ROUTE_HIST(2) MH_ROUTE_HIST(3) MH_ROUTE_HIST(4)
+        MH_ROUTE_HIST(5) MH_ROUTE_HIST(6) MH_ROUTE_HIST(7) MH_ROUTE_HIST(8)
+        default: break;
+    }
+#undef MH_ROUTE_HIST
+    MH_TRY(mh::launch_status("k_route_hist"));
+    uint32_t* tot = hb + static_cast<size_t>(nblk) * e;
+    hipLaunchKernelGGL(k_hist_prefix, dim3(e), dim3(256), 0, st, hb, tot, nblk, e);
+    MH_TRY(mh::launch_status("k_hist_prefix"));
+    hipLaunchKernelGGL(k_scatter_maps, dim3(nblk), dim3(256), 0, st, ids, hb, tot, m, e, topk, counts, offsets,
+                       gu_off, dn_off, ids_sorted, slotpos, reinterpret_cast<uint4*>(gu), max_gu,
+                       reinterpret_cast<uint4*>(dn), max_dn, bm, gu_bn, dn_bn, gu_n, dn_n);
+    return mh::launch_status("k_scatter_maps");
+}
+
 int moe_sort_maps(const uint32_t* ids, uint32_t s, uint32_t e, uint32_t topk,
                               uint32_t* counts, uint32_t* offsets, uint32_t* gu_off,
                               uint32_t* dn_off, uint32_t* ids_sorted, uint32_t* slotpos,

@@ -1,13 +1,16 @@
 // moe_prefill_step.hip -- the whole prefill MoE block in one call
 // (src/lfm.rs:847-965 moe_prefill), on a caller-provided workspace.
 //
-// Sequence (five launches and the combine): router logits with the per-token
-// top-k fused -> counts, offsets and block-map offsets in one workgroup ->
-// per-expert stable scatter with that expert's block-map entries -> grouped
-// gate/up GEMM with the ids_sorted row gather and the SwiGLU epilogue fused ->
+// Sequence (five launches and the combine): router logits (expert rows held
+// in the LDS, tokens streamed) -> per-token top-k with per-block expert
+// histograms -> counts, offsets, block-map offsets, the stable scatter and
+// the block maps (every workgroup sums the histograms) -> grouped gate/up
+// GEMM with the ids_sorted row gather and the SwiGLU epilogue fused ->
 // grouped down GEMM -> weighted combine.  Compared with the reference's sequence this drops the
 // materialised gathered rows and the separate gate/up outputs (two 4-byte
 // round trips per routed element); the values are the same.
+#include <algorithm>
+
 #include "mh_device.hpp"
 #include "mh_host.hpp"
 
@@ -44,7 +47,9 @@ Layout layout_for(uint32_t m, uint32_t e, uint32_t topk, uint32_t d_model, uint3
         static_cast<size_t>(l.max_gu) * 16,  // gate/up block map
         static_cast<size_t>(l.max_dn) * 16,  // down block map
         s * n_inter * 2,                 // act bf16 [s, n_inter]
-        s * d_model * 2,                 // ed bf16 [s, d_model]
+        std::max(s * d_model * 2,        // ed bf16 [s, d_model]; before the down GEMM, the
+                                         // routing's block histograms and expert totals
+                 (static_cast<size_t>((m + mh::kPrefillRouteBlock - 1) / mh::kPrefillRouteBlock) + 1) * e * 4),
     };
     size_t at = 0;
     for (int i = 0; i < MH_PREFILL_WS_REGIONS; ++i) {
@@ -116,11 +121,13 @@ int mh_moe_prefill(const void* router, int router_dtype, const float* bias, int 
     uint16_t* ed = reinterpret_cast<uint16_t*>(at(MH_PREFILL_WS_ED));
     const uint32_t s = m * topk;
 
-    MH_TRY(mh::router_prefill_route(x, router, router_dtype, logits, bias, ids, gw, m, d_model,
-                                    n_experts, topk, mode, eps, stream));
-    MH_TRY(mh::moe_sort_maps(ids, s, n_experts, topk, counts, offsets, gu_off, dn_off, ids_sorted,
-                             slotpos, gu_map, l.max_gu, dn_map, l.max_dn, kBM, kGuBN, kDnBN,
-                             n_inter, d_model, stream));
+    // the block histograms of the routing live in the down GEMM's output
+    // region until that GEMM runs
+    MH_TRY(mh::router_prefill_logits(x, router, router_dtype, logits, m, d_model, n_experts, stream));
+    MH_TRY(mh::moe_route_sort_maps(logits, bias, mode, eps, m, n_experts, topk, ids, gw,
+                                   reinterpret_cast<uint32_t*>(ed), counts, offsets, gu_off, dn_off,
+                                   ids_sorted, slotpos, gu_map, l.max_gu, dn_map, l.max_dn, kBM, kGuBN,
+                                   kDnBN, n_inter, d_model, stream));
     MH_TRY(mh_gemm_q4_grouped_gu_act(x, ids_sorted, m, gate, up, act, gu_map, l.max_gu, s, n_inter,
                                      kBM, kGuBN, stream));
     MH_TRY(mh_gemm_q4_grouped(act, down, ed, dn_map, l.max_dn, s, d_model, kBM, kDnBN, stream));
