@@ -149,8 +149,8 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void k_grouped(GemmArgs a
     const uint32_t live_rb = min(static_cast<uint32_t>(RB), (m_end - m0 + 31u) / 32u);
     const uint32_t lds0 = static_cast<uint32_t>((uintptr_t)((lds_ptr)lds));
 
-    // 32-bit byte offsets from wave-uniform bases (the host checks that the
-    // operands fit in 4 GiB), so each load is scalar base + vector offset.
+    // 32-bit byte offsets from wave-uniform bases (launch_t rejects operands
+    // past 4 GiB), so each load is scalar base + vector offset.
     const mh::gbytes abase = mh::uniform_ptr(a.a);
     mh::gbytes cbase[NMAT], sbase[NMAT], bbase[NMAT];
     cbase[0] = mh::uniform_ptr(a.c0);
@@ -882,6 +882,11 @@ int launch_seg(const GemmArgs& a, uint32_t n_blocks, hipStream_t s) {
 
 template <int BM, int NBW, int NW, bool GATHER, int EPI>
 int launch_t(const GemmArgs& a, uint32_t n_blocks, hipStream_t s) {
+    // k_grouped forms A and weight offsets in 32 bits from uniform bases
+    MH_ENSURE(static_cast<uint64_t>(a.a_rows) * a.k * 2u < (1ull << 32) &&
+                  static_cast<uint64_t>(a.w_rows) * a.k / 2u < (1ull << 32),
+              MH_ERR_UNSUPPORTED, "grouped GEMM: A (%u rows x %u) or the weights (%u rows) exceed 4 GiB",
+              a.a_rows, a.k, a.w_rows);
     constexpr int NMAT = (EPI == EPI_STORE) ? 1 : 2;
     constexpr size_t lds = static_cast<size_t>(kStages) * (BM * 128 + NW * NMAT * NBW * (1024 + 256));
     auto kern = k_grouped<BM, NBW, NW, GATHER, EPI>;

@@ -193,6 +193,21 @@ def test_bf16_and_quant_gemm_arguments():
     assert ei.value.code == hip.MH_ERR_ALIGN
 
 
+def test_grouped_gemm_rejects_operands_past_4_gib():
+    """The tile kernel forms A and weight offsets in 32 bits: operands of 4 GiB
+    or more are refused on the host (no device call is made)."""
+    with pytest.raises(hip.MoltenError, match="exceed 4 GiB") as ei:
+        hip.gemm_q4_dense(0x4000, 1 << 20, _qw(out_features=256), 0x6000, stream=0)  # A = 4 GiB
+    assert ei.value.code == hip.MH_ERR_UNSUPPORTED
+    with pytest.raises(hip.MoltenError, match="exceed 4 GiB") as ei:  # weights = 4 GiB
+        hip.gemm_q4_dense(0x4000, 64, _qw(out_features=1 << 22), 0x6000, stream=0)
+    assert ei.value.code == hip.MH_ERR_UNSUPPORTED
+    with pytest.raises(hip.MoltenError, match="exceed 4 GiB") as ei:  # gathered rows, grouped map
+        hip.gemm_q4_grouped_mlx(0x4000, _qw(out_features=256), 0x6000, 0x7000, 8, 1 << 20, 256,
+                                hip.MoeTile.T128, stream=0)
+    assert ei.value.code == hip.MH_ERR_UNSUPPORTED
+
+
 def test_sample_draw_arguments():
     p = hip.sample_params(1.0, 1, 0, top_k=40)
     with pytest.raises(hip.MoltenError, match="workspace holds 16 bytes"):
