@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from molten_amd import hip, layout
-from tests.devutil import dev_quant, empty_dev, from_dev, to_dev, zeros_dev
+from tests.devutil import dev_quant, empty_dev, float_report, from_dev, to_dev, zeros_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -43,6 +43,7 @@ def assert_logits(got, want, n, k, batch, gs=64):
     if not _mfma_path(n, k, batch, gs):
         np.testing.assert_array_equal(got, want)
         return
+    float_report(got, want, f"logits n={n} k={k} batch={batch}")
     g = layout.bf16_to_f32(got).astype(np.float64)
     w = layout.bf16_to_f32(want).astype(np.float64)
     assert np.isfinite(g).all()

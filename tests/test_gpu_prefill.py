@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 from molten_amd import hip, layout
-from tests.devutil import dev_quant, empty_dev, from_dev, to_dev, zeros_dev
+from tests.devutil import dev_quant, empty_dev, float_report, from_dev, to_dev, zeros_dev
 from tests.synth import moe_weights, router_weights
 
 pytestmark = pytest.mark.gpu
@@ -21,10 +21,14 @@ def _log(msg):
 
 
 def assert_close(got_bf16, ref_bf16, what, rel_l2=5e-3, max_rel=2e-2):
+    """Tolerance of the float outputs: rel-L2 <= 5e-3 and max abs err <= 2e-2
+    x max |ref|; the literal max abs err and the bf16-ulp histogram are
+    printed (float_report)."""
     g = bf(got_bf16).astype(np.float64)
     r = bf(ref_bf16).astype(np.float64)
     l2 = np.linalg.norm(g - r) / max(np.linalg.norm(r), 1e-30)
     mx = np.abs(g - r).max() / max(np.abs(r).max(), 1e-30)
+    float_report(got_bf16, ref_bf16, what)
     _log(f"{what}: rel-L2 {l2:.2e}, max|err|/max|ref| {mx:.2e}, "
          f"bit-equal {np.mean(got_bf16 == ref_bf16):.4f}")
     assert l2 <= rel_l2 and mx <= max_rel, (what, l2, mx)
@@ -236,16 +240,17 @@ def test_moe_prefill_small(dev, orc, mode):
     assert_close(got["out"], want["out"], f"prefill out m=256 mode={mode}")
 
 
-def test_moe_prefill_config4_full_size(dev, orc):
-    """Config 4 (4096 tokens, top-4 of 64): routing, counts, offsets and the
-    sort bit-exact over all 16384 slots; the output checked on 96 sampled
-    tokens against the oracle's expert GEMMs for those tokens."""
-    _log("moe prefill config 4 full size")
-    got, want, mask = _run_prefill(orc, 4096, 1, 2026, sample=96)
+@pytest.mark.parametrize("mode", [1, 0])
+def test_moe_prefill_config4_full_size(dev, orc, mode):
+    """Config 4 (4096 tokens, top-4 of 64), softmax routing with a bf16 router
+    and sigmoid + bias routing with an f32 router: routing, counts, offsets
+    and the sort bit-exact over all 16384 slots; the output of every token
+    against the oracle's expert GEMMs."""
+    _log(f"moe prefill config 4 full size mode={mode}")
+    got, want, _ = _run_prefill(orc, 4096, mode, 2026 + mode)
     for key in ("ids", "gw", "counts", "offsets", "ids_sorted", "slotpos"):
         np.testing.assert_array_equal(got[key], want[key], err_msg=key)
-    sel = mask == 1
-    assert_close(got["out"][sel], want["out"][sel], "prefill out config 4 (sampled tokens)")
+    assert_close(got["out"], want["out"], f"prefill out config 4 mode={mode} (all 4096 tokens)")
 
 
 def _dense_map(m, n, bm=128, bn=64):
