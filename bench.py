@@ -534,7 +534,7 @@ def main() -> int:
     ap.add_argument("--timeline", type=int, default=0,
                     help="only print the per-phase timeline of config 3's decode step over this many "
                          "launches (device timestamps), then exit")
-    ap.add_argument("--only", choices=("config3", "config4"), default=None,
+    ap.add_argument("--only", choices=("config2", "config3", "config4"), default=None,
                     help="only time this workload, print its line and exit (for profiler runs)")
     ap.add_argument("--eager", action="store_true",
                     help="launch the timed steps directly instead of replaying a graph "
@@ -567,6 +567,11 @@ def main() -> int:
         print(json.dumps({"only": "config4_prefill_moe", "ms_per_step": round(ms4, 4),
                           "grouped_gemm_only_ms": round(ms4g, 4),
                           "grouped_gemm_only_tflops": round(FLOPS_CONFIG4 / (ms4g * 1e-3) / 1e12, 2)}), flush=True)
+        return 0
+    if args.only == "config2":
+        ms2 = bench_lm_head(torch, hip, dev, gen, 4, 1, steps, warmup, copies=5)
+        print(json.dumps({"only": "config2_lm_head_q4_argmax", "ms_per_step": round(ms2, 5),
+                          "GB/s": round(BYTES["config2"] / (ms2 * 1e-3) / 1e9, 1)}), flush=True)
         return 0
     if args.only == "config3":
         ms3 = bench_config3(torch, hip, dev, gen, steps, warmup)

@@ -226,18 +226,27 @@ __device__ __forceinline__ unsigned long long wave_argmax_key(float bv, uint32_t
 }
 
 // Rows of the batch-1 kernel: each wave owns blocks of kBlockRows consecutive
-// rows; x is held in registers (lane c owns chunk c, K <= 2048).
+// rows; lane c owns chunk c of every row (K <= 2048).
 constexpr int kBlockRows = 8;
 constexpr int kGroupRows = 4;
 constexpr int kMaxGroups = 64;  // K / group size <= 2048 / 32
 
 // Batch 1, K <= 2048, even K / group size.  Each wave owns blocks of
 // kBlockRows consecutive rows (one block per wave up to kArgSlots
-// workgroups).  A block's scales and biases are read with a few wide loads
-// and staged in LDS as (scale | bias << 16) words; the codes of the block's
-// two row groups are loaded non-temporally (each byte is read once), group
-// 1 while group 0 is computed; each group's four row values are reduced
-// together, and the block's outputs are stored by lanes 0..7 at once.
+// workgroups).  Per block: the scales and biases are read with a few wide
+// loads and staged in LDS as f32 (scale, bias) pairs; the codes of the
+// block's two row groups are loaded non-temporally (each byte is read once)
+// and computed one group after the other.  x is converted once per
+// workgroup: wave 0 turns its chunk words into the f32 values the chunk dots
+// take (odd positions times 1/16 for Q4) and the ascending chunk sums, and
+// the other waves read them from LDS after one barrier.  Each lane's eight
+// row values go to LDS as [row][chunk]; lane 8r + j then reads chunks
+// 8j .. 8j + 7 of row r and adds them as the chunk order's butterfly does
+// (pairs, quads, octets: levels 1-3), and levels 4-6 (chunks xor 8, 16,
+// 32) are the lane pairs j ^ 1, j ^ 2 (quad_perm) and j ^ 4 (row_shr:4),
+// leaving row r's sum in lane 8r + 7.  Adding +0 to that sum instead of to
+// every lane's value gives the same bits: an IEEE sum is -0 only when both
+// operands are -0, so zero signs change nothing else in the tree.
 // FAST: K == 2048, group size 64 and N a multiple of kBlockRows (every lane
 // owns a chunk, 32 groups per row, no partial block).  ARGMAX: per-lane
 // bests, a DPP wave argmax, then the finisher (or the reference's atomic
@@ -245,7 +254,12 @@ constexpr int kMaxGroups = 64;  // K / group size <= 2048 / 32
 template <int BITS, bool FAST, bool ARGMAX>
 __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
     constexpr int BR = kBlockRows, R = kGroupRows;
-    __shared__ uint32_t sbl[kWaves][BR * kMaxGroups];
+    constexpr int GM = FAST ? 32 : kMaxGroups;     // staged groups per row
+    constexpr int NSB = BR * GM / 128;              // scale / bias word loads per lane
+    __shared__ uint4 sbl[kWaves][BR * GM / 2];      // (s, b) f32 pairs of groups 2i, 2i + 1
+    __shared__ float tl[kWaves][BR * 64];           // the block's lane values, [row][chunk]
+    __shared__ float xl[64 * kXPitch];              // x as the chunk dots take it
+    __shared__ float xsl[64];                       // ascending sums of the x chunks
     const int lane = threadIdx.x & (mh::kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / mh::kWave);
     const uint32_t C = a.k / 32u;
@@ -254,87 +268,128 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
     const bool live = FAST || lane < static_cast<int>(C);
     const uint32_t c = live ? lane : 0u;
     const unsigned long long launches = ARGMAX ? read_launches(a) : 0ull;
-
-    // x is converted after the first block's loads are issued
-    uint32_t xw[16];
-    mh::load_x_words(a.x + 32u * c, xw);
-    float xr[32];
-    float xs = 0.0f;
-    bool x_ready = false;
     const uint32_t code_off = c * BITS * 4u;
     const uint32_t gc = FAST ? static_cast<uint32_t>(lane) / 2u : (32u * c) / a.gs;
     const uint32_t row_bytes = FAST ? 2048u * BITS / 8u : a.row_words * 4u;
-    uint32_t* sb = sbl[wave];
-
-    float lbv = -__builtin_inff();  // per-lane best of the rows this lane stored
-    uint32_t lbi = 0u;
     const uint32_t n_blocks = (N + BR - 1) / BR;
-    for (uint32_t blk = blockIdx.x * kWaves + wave; blk < n_blocks; blk += gridDim.x * kWaves) {
+    const uint32_t stride = gridDim.x * kWaves;
+
+    uint32_t xw[16];
+    if (wave == 0) {
+        mh::load_x_words(a.x + 32u * c, xw);
+    }
+    uint32_t sw[NSB], bw[NSB];
+    mh::Chunk<BITS> A[R], Bc[R];
+    // a block's scale / bias words (clamped indices: every lane loads) and
+    // both groups of codes
+    auto issue = [&](uint32_t blk) {
         const uint32_t row0 = blk * BR;
         const uint32_t nrows = FAST ? static_cast<uint32_t>(BR) : min(static_cast<uint32_t>(BR), N - row0);
-        // scale/bias words of the block's rows (contiguous, dword aligned)
         const uint32_t nd = nrows * G / 2u;
         const uint32_t* s2 = reinterpret_cast<const uint32_t*>(a.scales + static_cast<size_t>(row0) * G);
         const uint32_t* b2 = reinterpret_cast<const uint32_t*>(a.biases + static_cast<size_t>(row0) * G);
-        constexpr int NSB = BR * (FAST ? 32 : kMaxGroups) / 128;
 #pragma unroll
         for (int j = 0; j < NSB; ++j) {
             const uint32_t i = lane + mh::kWave * j;
-            if (FAST || i < nd) {
-                const uint32_t sw = s2[i], bw = b2[i];
-                *reinterpret_cast<uint2*>(sb + 2u * i) =
-                    make_uint2(__builtin_amdgcn_perm(bw, sw, 0x05040100u),   // s.lo | b.lo << 16
-                               __builtin_amdgcn_perm(bw, sw, 0x07060302u));  // s.hi | b.hi << 16
-            }
+            const uint32_t ic = FAST || i < nd ? i : nd - 1u;
+            sw[j] = s2[ic];
+            bw[j] = b2[ic];
         }
         const char* codes = reinterpret_cast<const char*>(a.codes) + static_cast<size_t>(row0) * row_bytes;
-        auto load = [&](int grp, mh::Chunk<BITS>(&ch)[R]) {
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const uint32_t rr = FAST ? grp * R + r : min(static_cast<uint32_t>(grp * R + r), nrows - 1u);
-                ch[r].load_nt(mh::uniform_ptr(codes + rr * row_bytes), code_off);
-            }
-        };
-        float yv = 0.0f;
-        auto compute = [&](int grp, const mh::Chunk<BITS>(&ch)[R]) {
-            float h[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const uint32_t rr = FAST ? grp * R + r : min(static_cast<uint32_t>(grp * R + r), nrows - 1u);
-                const uint32_t w = sb[rr * G + gc];
-                const float p = ch[r].dot(xr);
-                const float hv = __builtin_fmaf(__uint_as_float(w << 16), p,
-                                                __uint_as_float(w & 0xffff0000u) * xs);
-                h[r] = live ? 0.0f + hv : 0.0f;
-            }
-            const float v = mh::reduce_rows4(h, lane);
-            const float mv = __int_as_float(__builtin_amdgcn_ds_bpermute((60 + (lane & 3)) * 4, __float_as_int(v)));
-            if ((lane >> 2) == grp) {
-                yv = mv;
-            }
-        };
-        mh::Chunk<BITS> A[R], Bc[R];
-        load(0, A);
-        if (!x_ready) {
-            mh::x_words_fence(xw);
-            mh::x_words_to_f32(xw, xr, xs);
-            if (BITS == 4) {
-                mh::q4_scale_x(xr);
-            }
-            x_ready = true;
+        for (int r = 0; r < 2 * R; ++r) {
+            const uint32_t rr = FAST ? r : min(static_cast<uint32_t>(r), nrows - 1u);
+            (r < R ? A[r] : Bc[r - R]).load_nt(mh::uniform_ptr(codes + rr * row_bytes), code_off);
         }
-        load(1, Bc);
+    };
+    // the first block's loads go out unconditionally (a wave past the last
+    // block re-reads it; only the last workgroup can have one), so that no
+    // path without them meets the x conversion's wait
+    const uint32_t blk0 = blockIdx.x * kWaves + wave;
+    issue(min(blk0, n_blocks - 1u));
+
+    // x: wave 0 converts, every wave reads after the barrier
+    float xr[32];
+    float xs = 0.0f;
+    if (wave == 0) {
+        mh::x_words_fence(xw);
+        mh::x_words_to_f32(xw, xr, xs);
+        if (BITS == 4) {
+            mh::q4_scale_x(xr);
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            *reinterpret_cast<float4*>(xl + lane * kXPitch + 4 * q) =
+                make_float4(xr[4 * q], xr[4 * q + 1], xr[4 * q + 2], xr[4 * q + 3]);
+        }
+        xsl[lane] = xs;
+    }
+    // LDS writes done, then the barrier; the asm's memory clobber keeps the
+    // reads below it (the code loads above stay in flight)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (wave != 0) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float4 v = *reinterpret_cast<const float4*>(xl + lane * kXPitch + 4 * q);
+            xr[4 * q] = v.x; xr[4 * q + 1] = v.y; xr[4 * q + 2] = v.z; xr[4 * q + 3] = v.w;
+        }
+        xs = xsl[lane];
+    }
+
+    uint4* sb = sbl[wave];
+    float* tw = tl[wave];
+    float lbv = -__builtin_inff();  // per-lane best of the rows this lane stored
+    uint32_t lbi = 0u;
+    // one block from the loaded words: stage (s, b), both groups, the row sums
+    auto process = [&](uint32_t blk) {
+        const uint32_t row0 = blk * BR;
+        const uint32_t nrows = FAST ? static_cast<uint32_t>(BR) : min(static_cast<uint32_t>(BR), N - row0);
+        // (s, b) as f32 bits: word i holds groups 2i (low halves) and 2i + 1
+#pragma unroll
+        for (int j = 0; j < NSB; ++j) {
+            const uint32_t i = lane + mh::kWave * j;
+            sb[i] = make_uint4(sw[j] << 16, bw[j] << 16, sw[j] & 0xffff0000u, bw[j] & 0xffff0000u);
+        }
+        const uint2* sbp = reinterpret_cast<const uint2*>(sb);
+        auto compute = [&](int grp, const mh::Chunk<BITS>(&ch)[R]) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t rr = FAST ? grp * R + r : min(static_cast<uint32_t>(grp * R + r), nrows - 1u);
+                const uint2 w = sbp[rr * G + gc];
+                const float p = ch[r].dot(xr);
+                const float hv = __builtin_fmaf(__uint_as_float(w.x), p, __uint_as_float(w.y) * xs);
+                tw[(grp * R + r) * 64 + lane] = live ? hv : 0.0f;
+            }
+        };
         compute(0, A);
         compute(1, Bc);
-        const uint16_t yb = mh::f32_to_bf16(yv);
-        if (lane < static_cast<int>(nrows)) {
+        __builtin_amdgcn_wave_barrier();
+        // lane 8r + j: chunks 8j .. 8j + 7 of row r
+        const float4 t0 = *reinterpret_cast<const float4*>(tw + 8 * lane);
+        const float4 t1 = *reinterpret_cast<const float4*>(tw + 8 * lane + 4);
+        float v = ((t0.x + t0.y) + (t0.z + t0.w)) + ((t1.x + t1.y) + (t1.z + t1.w));
+        v = v + mh::qmove<0xB1>(v);             // chunks xor 8  (quad_perm 1,0,3,2)
+        v = v + mh::qmove<0x4E>(v);             // chunks xor 16 (quad_perm 2,3,0,1)
+        v = v + mh::dpp_move<0x114, 0xf>(v);    // chunks xor 32 (row_shr:4; lanes 8r+4..7)
+        __builtin_amdgcn_wave_barrier();
+        const uint32_t r = static_cast<uint32_t>(lane) >> 3;
+        if ((lane & 7) == 7 && r < nrows) {
+            const uint16_t yb = mh::f32_to_bf16(v + 0.0f);
             if (a.y != nullptr) {
-                a.y[row0 + lane] = yb;
+                a.y[row0 + r] = yb;
             }
             if (ARGMAX) {
-                mh::argmax_merge(lbv, lbi, mh::bf16_to_f32(yb), row0 + lane);
+                mh::argmax_merge(lbv, lbi, mh::bf16_to_f32(yb), row0 + r);
             }
         }
+    };
+    if (blk0 < n_blocks) {
+        process(blk0);
+    }
+    // later rounds (more blocks than the grid has waves)
+    for (uint32_t blk = blk0 + stride; blk < n_blocks; blk += stride) {
+        issue(blk);
+        process(blk);
     }
     if (!ARGMAX) {
         return;
