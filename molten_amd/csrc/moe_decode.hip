@@ -180,12 +180,17 @@ __global__ __launch_bounds__(kThreads) void k_dense_gemv(DenseArgs a) {
 // f32 (chunk c of row e as 8 pieces of 16 bytes, piece q at q ^ ((c >> 1) &
 // 7), so the 16 lanes of a 16-byte read cover all 64 banks once), then each
 // wave runs its tokens in groups of four with x in registers (lane c holds
-// chunk c) against one expert row at a time from the LDS (the next row's
-// read in flight; two workgroups per CU cover each other's waits).  Per
-// (token, expert) the arithmetic is the chunk order of k_dense_gemv: lane
-// c's fma chain over its 32 elements from 0, then the xor butterfly over the
-// 64 chunks (four tokens in one 4-row butterfly); W comes from the L2 once
-// per workgroup.
+// chunk c; the first group's x is loaded before the rows are staged) against
+// one expert row at a time from the LDS (the next row's read in flight; two
+// workgroups per CU cover each other's waits).  Per (token, expert) the
+// arithmetic is the chunk order of k_dense_gemv: lane c's fma chain over its
+// 32 elements from 0, then the xor butterfly over the 64 chunks -- here for
+// eight values at once (four tokens x two experts): each lane's eight chain
+// values go to the LDS as [value][chunk], lane 8v + j adds chunks 8j .. 8j +
+// 7 of value v (levels 1-3) and levels 4-6 are DPP quad_perm and row_shr:4,
+// leaving value v in lane 8v + 7; the chunk order's +0 is applied once to
+// that sum (an IEEE sum is -0 only when both operands are, so the bits are
+// the same).  W comes from the L2 once per workgroup.
 constexpr int kRtTokens = 64;
 constexpr int kRtExperts = 8;
 constexpr int kRtGroup = 4;                                // tokens per group
@@ -195,6 +200,7 @@ template <typename WT>
 __global__ __launch_bounds__(kThreads, 2) void k_router_tiles(DenseArgs a) {
     extern __shared__ float wl[];  // [kRtExperts][C][8 pieces][4]
     __shared__ float zl[kRtTokens][kRtExperts];
+    __shared__ __attribute__((aligned(16))) float tl[kWaves][8 * 64];  // a wave's chain values, [value][chunk]
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t C = a.k / 32u;
@@ -204,6 +210,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_router_tiles(DenseArgs a) {
     const uint32_t e0 = blockIdx.y * kRtExperts;
     const uint32_t ne = min(static_cast<uint32_t>(kRtExperts), a.n - e0);
     const uint32_t t_wave = static_cast<uint32_t>(wave * kRtGroup * kRtGroups);
+    float* tw = tl[wave];
     auto load_group = [&](int g, uint32_t (&xw)[kRtGroup][16]) {
 #pragma unroll
         for (int t = 0; t < kRtGroup; ++t) {
@@ -216,6 +223,8 @@ __global__ __launch_bounds__(kThreads, 2) void k_router_tiles(DenseArgs a) {
             }
         }
     };
+    uint32_t xw[kRtGroup][16];
+    load_group(0, xw);
     // stage rows e0 .. e0 + ne: 8 elements (two pieces) per thread and step
     const WT* w = static_cast<const WT*>(a.w);
     for (uint32_t i = threadIdx.x; i < ne * C * 4u; i += kThreads) {
@@ -244,62 +253,70 @@ __global__ __launch_bounds__(kThreads, 2) void k_router_tiles(DenseArgs a) {
     __syncthreads();
     const uint32_t swz = (c >> 1) & 7u;
     auto read_row = [&](uint32_t e, float (&wr)[32]) {
-        const float* base = wl + static_cast<size_t>(e * C + c) * 32u;
+        const uint32_t ec = min(e, ne - 1u);  // a missing odd expert reads a staged row; never stored
+        const float* base = wl + static_cast<size_t>(ec * C + c) * 32u;
 #pragma unroll
         for (uint32_t q = 0; q < 8; ++q) {
             const float4 v = *reinterpret_cast<const float4*>(base + 4u * (q ^ swz));
             wr[4 * q] = v.x; wr[4 * q + 1] = v.y; wr[4 * q + 2] = v.z; wr[4 * q + 3] = v.w;
         }
     };
-#pragma unroll 1
-    for (int g = 0; g < kRtGroups; ++g) {
+    // one group of four tokens against the staged experts
+    auto group = [&](int g, const uint32_t (&xg)[kRtGroup][16]) {
         float xr[kRtGroup][32];
-        {
-            uint32_t xw[kRtGroup][16];
-            load_group(g, xw);
+#pragma unroll
+        for (int t = 0; t < kRtGroup; ++t) {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                xr[t][2 * q] = mh::bf16lo(xg[t][q]);
+                xr[t][2 * q + 1] = mh::bf16hi(xg[t][q]);
+            }
+        }
+        // lane c's chain values of the group's four tokens for one expert
+        // row into values v0 .. v0 + 3 of the wave's LDS block
+        auto chains = [&](const float (&wr)[32], int v0) {
 #pragma unroll
             for (int t = 0; t < kRtGroup; ++t) {
+                float p = 0.0f;
 #pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    xr[t][2 * q] = mh::bf16lo(xw[t][q]);
-                    xr[t][2 * q + 1] = mh::bf16hi(xw[t][q]);
+                for (int i = 0; i < 32; ++i) {
+                    p = __builtin_fmaf(wr[i], xr[t][i], p);
                 }
-            }
-        }
-        auto expert = [&](uint32_t e, const float (&wr)[32]) {
-#pragma unroll
-            for (int half = 0; half < kRtGroup / 4; ++half) {
-                float h[4];
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    float p = 0.0f;
-#pragma unroll
-                    for (int i = 0; i < 32; ++i) {
-                        p = __builtin_fmaf(wr[i], xr[4 * half + t][i], p);
-                    }
-                    h[t] = live ? 0.0f + p : 0.0f;
-                }
-                const float v = mh::reduce_rows4(h, lane);
-                if (lane >= 60) {
-                    zl[t_wave + kRtGroup * g + 4 * half + (lane - 60)][e] = v;
-                }
+                tw[(v0 + t) * 64 + lane] = live ? p : 0.0f;
             }
         };
-        // two row buffers, the next row's read in flight
+        // experts e, e + 1: eight values, then the 64-chunk sums
         float wa[32], wb[32];
         read_row(0, wa);
+#pragma unroll 1
         for (uint32_t e = 0; e < ne; e += 2) {
-            if (e + 1 < ne) {
-                read_row(e + 1, wb);
+            read_row(e + 1, wb);
+            chains(wa, 0);
+            if (e + 2 < ne) {
+                read_row(e + 2, wa);
             }
-            expert(e, wa);
-            if (e + 1 < ne) {
-                if (e + 2 < ne) {
-                    read_row(e + 2, wa);
-                }
-                expert(e + 1, wb);
+            chains(wb, 4);
+            __builtin_amdgcn_wave_barrier();
+            const float4 q0 = *reinterpret_cast<const float4*>(tw + 8 * lane);
+            const float4 q1 = *reinterpret_cast<const float4*>(tw + 8 * lane + 4);
+            float v = ((q0.x + q0.y) + (q0.z + q0.w)) + ((q1.x + q1.y) + (q1.z + q1.w));
+            v = v + mh::qmove<0xB1>(v);           // chunks xor 8  (quad_perm 1,0,3,2)
+            v = v + mh::qmove<0x4E>(v);           // chunks xor 16 (quad_perm 2,3,0,1)
+            v = v + mh::dpp_move<0x114, 0xf>(v);  // chunks xor 32 (row_shr:4)
+            __builtin_amdgcn_wave_barrier();
+            const uint32_t val = static_cast<uint32_t>(lane) >> 3;  // token (val & 3), expert e + (val >> 2)
+            const uint32_t ee = e + (val >> 2);
+            if ((lane & 7) == 7 && ee < ne) {
+                zl[t_wave + kRtGroup * g + (val & 3u)][ee] = v + 0.0f;
             }
         }
+    };
+    group(0, xw);  // the first group's x was loaded before the staging
+#pragma unroll 1
+    for (int g = 1; g < kRtGroups; ++g) {
+        uint32_t xn[kRtGroup][16];
+        load_group(g, xn);
+        group(g, xn);
     }
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < kRtTokens * ne; i += kThreads) {
