@@ -518,6 +518,17 @@ def read_traffic():
         return None
 
 
+def calibrate_copy(torch, dev, mib):
+    """A plain elementwise kernel (f32 negate) that reads and writes exactly
+    `mib` MiB each: the scale of the PMC byte counters in the same run."""
+    src = torch.ones((mib << 20) // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -562,6 +573,8 @@ def main() -> int:
                           **timeline_config3(torch, hip, dev, gen, args.timeline)}), flush=True)
         return 0
 
+    if args.only is not None and args.calibrate_copy_mib > 0:
+        calibrate_copy(torch, dev, args.calibrate_copy_mib)
     if args.only == "config4":
         ms4, ms4g = bench_config4(torch, hip, dev, gen, steps, warmup)
         print(json.dumps({"only": "config4_prefill_moe", "ms_per_step": round(ms4, 4),
@@ -582,13 +595,7 @@ def main() -> int:
     ms2 = bench_lm_head(torch, hip, dev, gen, 4, 1, steps, warmup, copies=5)
     gbs2 = BYTES["config2"] / (ms2 * 1e-3) / 1e9
     if args.calibrate_copy_mib > 0:
-        # reads and writes exactly calibrate_copy_mib MiB each, in one kernel
-        src = torch.ones((args.calibrate_copy_mib << 20) // 4, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            torch.neg(src, out=dst)
-        torch.cuda.synchronize()
-        del src, dst
+        calibrate_copy(torch, dev, args.calibrate_copy_mib)
     others = {}
     if not args.only_headline:
         log("config 1: Q4 GEMV 2048x2048")
