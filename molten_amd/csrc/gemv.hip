@@ -251,13 +251,14 @@ constexpr int kMaxGroups = 64;  // K / group size <= 2048 / 32
 // owns a chunk, 32 groups per row, no partial block).  ARGMAX: per-lane
 // bests, a DPP wave argmax, then the finisher (or the reference's atomic
 // max).
-template <int BITS, bool FAST, bool ARGMAX>
+template <int BITS, bool FAST, bool ARGMAX, int NG>
 __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
-    constexpr int BR = kBlockRows, R = kGroupRows;
+    static_assert(NG == 1 || NG == 2, "one or two 4-row groups per block");
+    constexpr int R = kGroupRows, BR = NG * R;
     constexpr int GM = FAST ? 32 : kMaxGroups;     // staged groups per row
     constexpr int NSB = BR * GM / 128;              // scale / bias word loads per lane
     __shared__ uint4 sbl[kWaves][BR * GM / 2];      // (s, b) f32 pairs of groups 2i, 2i + 1
-    __shared__ float tl[kWaves][BR * 64];           // the block's lane values, [row][chunk]
+    __shared__ float tl[kWaves][kBlockRows * 64];   // the block's lane values, [row][chunk]
     __shared__ float xl[64 * kXPitch];              // x as the chunk dots take it
     __shared__ float xsl[64];                       // ascending sums of the x chunks
     const int lane = threadIdx.x & (mh::kWave - 1);
@@ -279,9 +280,9 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
         mh::load_x_words(a.x + 32u * c, xw);
     }
     uint32_t sw[NSB], bw[NSB];
-    mh::Chunk<BITS> A[R], Bc[R];
+    mh::Chunk<BITS> A[R], Bc[R];  // Bc: NG == 2 only
     // a block's scale / bias words (clamped indices: every lane loads) and
-    // both groups of codes
+    // its groups of codes
     auto issue = [&](uint32_t blk) {
         const uint32_t row0 = blk * BR;
         const uint32_t nrows = FAST ? static_cast<uint32_t>(BR) : min(static_cast<uint32_t>(BR), N - row0);
@@ -297,7 +298,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
         }
         const char* codes = reinterpret_cast<const char*>(a.codes) + static_cast<size_t>(row0) * row_bytes;
 #pragma unroll
-        for (int r = 0; r < 2 * R; ++r) {
+        for (int r = 0; r < NG * R; ++r) {
             const uint32_t rr = FAST ? r : min(static_cast<uint32_t>(r), nrows - 1u);
             (r < R ? A[r] : Bc[r - R]).load_nt(mh::uniform_ptr(codes + rr * row_bytes), code_off);
         }
@@ -362,9 +363,12 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
             }
         };
         compute(0, A);
-        compute(1, Bc);
+        if constexpr (NG == 2) {
+            compute(1, Bc);
+        }
         __builtin_amdgcn_wave_barrier();
-        // lane 8r + j: chunks 8j .. 8j + 7 of row r
+        // lane 8r + j: chunks 8j .. 8j + 7 of row r (rows past the block's
+        // NG * 4 hold stale values and are never emitted)
         const float4 t0 = *reinterpret_cast<const float4*>(tw + 8 * lane);
         const float4 t1 = *reinterpret_cast<const float4*>(tw + 8 * lane + 4);
         float v = ((t0.x + t0.y) + (t0.z + t0.w)) + ((t1.x + t1.y) + (t1.z + t1.w));
@@ -648,12 +652,20 @@ template <int BITS, bool ARGMAX>
 int launch_rows(const GemvArgs& a, hipStream_t stream) {
     // one block per wave while the finisher has a slot for every workgroup
     // (the hardware keeps as many workgroups resident as registers allow);
-    // beyond that the waves loop over blocks
-    const uint32_t grid = grid_for((a.n + kBlockRows - 1) / kBlockRows, kRowsGridCap);
-    if (a.k == 2048u && a.gs == 64u && a.n % kBlockRows == 0u) {
-        return launch(k_gemv_rows<BITS, true, ARGMAX>, a, grid, 0, stream, "k_gemv_rows");
+    // beyond that the waves loop over blocks.  Matrices with fewer 8-row
+    // blocks than the chip has SIMDs x 4 take 4-row blocks: twice the waves,
+    // half the serial arithmetic per wave (latency-bound sizes).
+    const uint32_t blocks8 = (a.n + kBlockRows - 1) / kBlockRows;
+    const bool small = blocks8 < static_cast<uint32_t>(mh::cu_count()) * 4u * kWaves;
+    const bool fast = a.k == 2048u && a.gs == 64u && a.n % (small ? kGroupRows : kBlockRows) == 0u;
+    if (small) {
+        const uint32_t grid = grid_for((a.n + kGroupRows - 1) / kGroupRows, kRowsGridCap);
+        return fast ? launch(k_gemv_rows<BITS, true, ARGMAX, 1>, a, grid, 0, stream, "k_gemv_rows")
+                    : launch(k_gemv_rows<BITS, false, ARGMAX, 1>, a, grid, 0, stream, "k_gemv_rows");
     }
-    return launch(k_gemv_rows<BITS, false, ARGMAX>, a, grid, 0, stream, "k_gemv_rows");
+    const uint32_t grid = grid_for(blocks8, kRowsGridCap);
+    return fast ? launch(k_gemv_rows<BITS, true, ARGMAX, 2>, a, grid, 0, stream, "k_gemv_rows")
+                : launch(k_gemv_rows<BITS, false, ARGMAX, 2>, a, grid, 0, stream, "k_gemv_rows");
 }
 
 template <int BITS>
