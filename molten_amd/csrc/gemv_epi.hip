@@ -10,7 +10,10 @@
 
 namespace {
 
-constexpr int BR = mh::kBlockRows;
+// 4-row blocks: these projections are latency-bound (a few MB), so twice the
+// waves with half the serial arithmetic each finish sooner than 8-row blocks
+constexpr int kNG = 1;
+constexpr int BR = kNG * mh::kGroupRows;
 
 // ------------------------------------------------------------- proj3 ---
 
@@ -55,7 +58,7 @@ __global__ __launch_bounds__(64) void k_proj3(Proj3Args a) {
     const uint32_t rows = seg == 0 ? a.rows[0] : (seg == 1 ? a.rows[1] : a.rows[2]);
     const uint32_t row0 = blk * BR;
     const uint32_t nrows = FAST ? static_cast<uint32_t>(BR) : min(static_cast<uint32_t>(BR), rows - row0);
-    const float yv = walk.block(m, row0, nrows, xr, xs, [] {});
+    const float yv = walk.template block<kNG>(m, row0, nrows, xr, xs, [] {});
     if (lane < static_cast<int>(nrows)) {
         const uint32_t j = row0 + lane;
         const uint16_t yb = mh::f32_to_bf16(yv);
@@ -98,7 +101,7 @@ __global__ __launch_bounds__(192) void k_conv3(Conv3Args a) {
     float xr[32], xs;
     mh::x_chunk_regs<4>(a.x, walk.chunk(), xr, xs);
     const uint32_t nrows = FAST ? static_cast<uint32_t>(BR) : min(static_cast<uint32_t>(BR), H - c0);
-    const float y = walk.block(a.m, static_cast<uint32_t>(wave) * H + c0, nrows, xr, xs, [] {});
+    const float y = walk.template block<kNG>(a.m, static_cast<uint32_t>(wave) * H + c0, nrows, xr, xs, [] {});
     if (lane < BR) {
         vals[wave][lane] = y;
     }

@@ -47,18 +47,19 @@ struct RowWalk {
     }
     __device__ __forceinline__ uint32_t chunk() const { return live ? static_cast<uint32_t>(lane) : 0u; }
 
-    // Rows row0 .. row0 + nrows - 1 (nrows <= kBlockRows; FAST: == kBlockRows)
-    // of m: the block's scales and biases are read with a few word loads and
-    // staged in LDS as (scale | bias << 16) words; the codes of the block's
-    // two row groups are loaded non-temporally (each byte is read once),
-    // group 1 while group 0 is computed; each group's four row values are
-    // reduced together.  Lane j < nrows receives row row0 + j's f32 sum in
-    // the chunk order.  prep() runs once the first group's loads are out
-    // (the caller may finish preparing xr / xs there).
-    template <typename Prep>
+    // Rows row0 .. row0 + nrows - 1 (nrows <= 4 NG; FAST: == 4 NG) of m: the
+    // block's scales and biases are read with a few word loads and staged in
+    // LDS as (scale | bias << 16) words; the codes of the block's NG row
+    // groups are loaded non-temporally (each byte is read once), group 1
+    // while group 0 is computed; each group's four row values are reduced
+    // together.  Lane j < nrows receives row row0 + j's f32 sum in the chunk
+    // order.  prep() runs once the first group's loads are out (the caller
+    // may finish preparing xr / xs there).
+    template <int NG = 2, typename Prep>
     __device__ __forceinline__ float block(const RowMatrix& m, uint32_t row0, uint32_t nrows, float (&xr)[32],
                                            float& xs, Prep&& prep) const {
-        constexpr int BR = kBlockRows, R = kGroupRows;
+        static_assert(NG == 1 || NG == 2, "one or two 4-row groups");
+        constexpr int R = kGroupRows, BR = NG * R;
         const uint32_t nd = nrows * G / 2u;
         const uint32_t* s2 = reinterpret_cast<const uint32_t*>(m.scales + static_cast<size_t>(row0) * G);
         const uint32_t* b2 = reinterpret_cast<const uint32_t*>(m.biases + static_cast<size_t>(row0) * G);
@@ -112,9 +113,13 @@ struct RowWalk {
         // the loads issued so far
         __builtin_amdgcn_sched_barrier(0);
         prep();
-        load(1, Bc);
+        if constexpr (NG == 2) {
+            load(1, Bc);
+        }
         compute(0, A);
-        compute(1, Bc);
+        if constexpr (NG == 2) {
+            compute(1, Bc);
+        }
         return yv;
     }
 };
