@@ -277,8 +277,10 @@ int mh_sample_gumbel(const uint16_t* logits, uint32_t n, const uint32_t* seen,
  * mh_sample_gumbel (which this calls when neither is on).  workspace:
  * mh_sample_workspace_bytes(n) bytes, 256-byte aligned, zeroed before the
  * first call; every call leaves the part that must start at zero (its first
- * 16 KiB) zero again and rewrites the rest.  Calls sharing one workspace
- * must not overlap.  top_p must be in (0, 1]. */
+ * MH_SAMPLE_ZERO_BYTES bytes) zero again and rewrites the rest.  Calls
+ * sharing one workspace must not overlap.  top_p must be in (0, 1]; n at
+ * most 2^31. */
+#define MH_SAMPLE_ZERO_BYTES 16640u
 size_t mh_sample_workspace_bytes(uint32_t n);
 int mh_sample_draw(const uint16_t* logits, uint32_t n, const uint32_t* seen, const mh_sample_params* params,
                    uint64_t* best, void* workspace, size_t workspace_bytes, mh_stream_t stream);

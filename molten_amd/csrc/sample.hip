@@ -80,12 +80,16 @@ __global__ __launch_bounds__(kThreads) void k_sample_gumbel(const uint16_t* logi
 // no arrival counter, no fence and no serial tail between rounds.  The first
 // count round runs inside the launch that computes w.  The draw launch
 // decides the last round and folds the Gumbel-max over {w >= tau} into the
-// key word, as the temperature draw.
+// key word, as the temperature draw.  With both top-k and top-p on, the mass
+// phase has no launches of its own: the draw launch appends the top-k set to
+// a list and its last workgroup decides top-p over the list
+// (k_smp_draw_kept).
 //
-// Workspace (caller-owned; the first round's histogram zeroed before the
-// first call, and left zero by every call; the rest is rewritten by every
-// call): w f32[n], the per-workgroup max keys, one histogram per round, and
-// the state each round ran with.
+// Workspace (caller-owned; its head -- the kept list's counters and the
+// first round's histogram -- zeroed before the first call and left zero by
+// every call; the rest is rewritten by every call): w f32[n], the
+// per-workgroup max keys, one histogram per round, the state each round ran
+// with, and the kept list.
 constexpr int kGroups = 4;                          // groups of 4 tokens per thread
 constexpr uint32_t kBlock = 4u * kGroups * kThreads;  // tokens per workgroup
 constexpr int kDigits = 2048;                       // 11-bit digits
@@ -103,11 +107,24 @@ struct SmpState {
     unsigned long long target;  // k, or the mass target (0: set by the first mass round)
 };
 
+// The zeroed head of the workspace (with the first round's histogram after
+// it): the kept-set draw's append counter and finished-workgroup count.
+struct SmpCtl {
+    uint32_t kept;
+    uint32_t done;
+};
+constexpr uint32_t kKeptCap = 256;  // kept tokens the finishing workgroup takes from the list
+constexpr size_t kCtlBytes = 256;
+constexpr size_t kZeroBytes = kCtlBytes + static_cast<size_t>(kDigits) * 8u;  // ctl + round 0's bins
+static_assert(kZeroBytes == MH_SAMPLE_ZERO_BYTES, "the header's zero-region size");
+
 struct SmpWs {
     float* w;
     uint32_t* wmax;             // per-workgroup max key
     unsigned long long* hist;   // kRounds x kDigits
     SmpState* plan;             // the state each round ran with
+    SmpCtl* ctl;
+    unsigned long long* kept;   // kKeptCap x {key << 32 | 2^31 | index, mass, draw key}
 };
 
 size_t smp_align(size_t b) { return (b + 255u) & ~static_cast<size_t>(255u); }
@@ -117,19 +134,24 @@ uint32_t smp_grid(uint32_t n) { return (n + kBlock - 1u) / kBlock; }
 SmpWs smp_layout(void* ws, uint32_t n) {
     char* p = static_cast<char*>(ws);
     SmpWs l;
+    l.ctl = reinterpret_cast<SmpCtl*>(p);
+    p += kCtlBytes;
     l.hist = reinterpret_cast<unsigned long long*>(p);
     p += smp_align(static_cast<size_t>(kRounds) * kDigits * 8u);
     l.plan = reinterpret_cast<SmpState*>(p);
     p += smp_align(kRounds * sizeof(SmpState));
     l.wmax = reinterpret_cast<uint32_t*>(p);
     p += smp_align(static_cast<size_t>(smp_grid(n)) * 4u);
+    l.kept = reinterpret_cast<unsigned long long*>(p);
+    p += smp_align(static_cast<size_t>(kKeptCap) * 3u * 8u);
     l.w = reinterpret_cast<float*>(p);
     return l;
 }
 
 size_t smp_bytes(uint32_t n) {
-    return smp_align(static_cast<size_t>(kRounds) * kDigits * 8u) + smp_align(kRounds * sizeof(SmpState)) +
-           smp_align(static_cast<size_t>(smp_grid(n)) * 4u) + smp_align(static_cast<size_t>(n) * 4u);
+    return kCtlBytes + smp_align(static_cast<size_t>(kRounds) * kDigits * 8u) +
+           smp_align(kRounds * sizeof(SmpState)) + smp_align(static_cast<size_t>(smp_grid(n)) * 4u) +
+           smp_align(static_cast<size_t>(kKeptCap) * 3u * 8u) + smp_align(static_cast<size_t>(n) * 4u);
 }
 
 __device__ __forceinline__ uint32_t smp_fkey(float v) {
@@ -495,6 +517,219 @@ __global__ __launch_bounds__(kThreads) void k_smp_draw(uint32_t n, mh_sample_par
     }
 }
 
+// Exclusive prefix of v over the workgroup's threads (and the total).
+__device__ uint32_t smp_block_excl(uint32_t v, uint32_t* part, uint32_t& total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t inc = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t o = __shfl_up(inc, off);
+        if (lane >= off) {
+            inc += o;
+        }
+    }
+    if (lane == 63) {
+        part[wave] = inc;
+    }
+    __syncthreads();
+    uint32_t before = 0u;
+    total = 0u;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) {
+        before += w < wave ? part[w] : 0u;
+        total += part[w];
+    }
+    __syncthreads();
+    return before + inc - v;
+}
+
+// The kept-set draw when both top-k and top-p are on, in one launch after
+// the count rounds: every workgroup decides the last count round (tau_k),
+// appends its tokens with key >= tau_k to the kept list (key and index, mass,
+// draw key) and counts itself finished; the last workgroup to finish takes
+// top-p over the list -- tau_p is the greatest kept key whose cumulative
+// mass (every kept token with a key >= it) reaches the target, which is the
+// radix select's tie-group walk -- and folds the draw over {key >= tau_p}
+// into the key word.  A list longer than kKeptCap (ties at the threshold, or
+// a large k) is decided by that workgroup alone with the mass phase's three
+// radix rounds over all tokens.  The finishing workgroup leaves the counters
+// zero for the next call.
+__global__ __launch_bounds__(kThreads) void k_smp_draw_kept(uint32_t n, mh_sample_params p, SmpWs ws, int last,
+                                                            unsigned long long* best) {
+    __shared__ unsigned long long partk[kThreads / 64];
+    __shared__ uint32_t partu[kThreads / 64];
+    __shared__ SmpDecideLds dl;
+    __shared__ uint32_t wg_base, is_last;
+    __shared__ unsigned long long lk[kKeptCap], lm[kKeptCap], lg[kKeptCap];
+    __shared__ unsigned long long lmass[kDigits];
+    __shared__ uint32_t tau_l;
+    float4 w4[kGroups];
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+        const uint32_t i0 = smp_token0(g);
+        w4[g] = i0 < n ? *reinterpret_cast<const float4*>(ws.w + i0) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    const SmpPrev pv = smp_prev_load(ws, last);
+    float y[kGroups][4];
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+        const uint32_t i0 = smp_token0(g);
+        const mh::u32x4 r = mh::philox4x32_10(mh::u32x4{i0 / 4u, p.pos, kDomain, 0u}, p.seed_lo, p.seed_hi);
+        y[g][0] = mh::gumbel_of(r.x);
+        y[g][1] = mh::gumbel_of(r.y);
+        y[g][2] = mh::gumbel_of(r.z);
+        y[g][3] = mh::gumbel_of(r.w);
+    }
+    const float m = smp_kfloat(smp_max_key(ws, partu));
+    const uint32_t tau_k = smp_decide(pv, 0, 2, p, dl).tau_key;
+    for (uint32_t i = blockIdx.x * kThreads + threadIdx.x; i < kDigits; i += gridDim.x * kThreads) {
+        __hip_atomic_store(ws.hist + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // this workgroup's kept tokens into the list
+    uint32_t cnt = 0u;
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+        const uint32_t i0 = smp_token0(g);
+        const float w[4] = {w4[g].x, w4[g].y, w4[g].z, w4[g].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            cnt += i0 < n && smp_fkey(w[j]) >= tau_k ? 1u : 0u;
+        }
+    }
+    uint32_t total = 0u;
+    const uint32_t excl = smp_block_excl(cnt, partu, total);
+    if (threadIdx.x == 0) {
+        wg_base = total != 0u ? __hip_atomic_fetch_add(&ws.ctl->kept, total, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT)
+                              : 0u;
+    }
+    __syncthreads();
+    // entries as device-coherent stores (no dirty L2 lines for the release
+    // below to write back), then the finished count with release / acquire
+    uint32_t pos = wg_base + excl;
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+        const uint32_t i0 = smp_token0(g);
+        const float w[4] = {w4[g].x, w4[g].y, w4[g].z, w4[g].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t key = smp_fkey(w[j]);
+            if (i0 < n && key >= tau_k) {
+                if (pos < kKeptCap) {
+                    __hip_atomic_store(ws.kept + 3u * pos, (static_cast<unsigned long long>(key) << 32) | 0x80000000u | (i0 + j), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(ws.kept + 3u * pos + 1u, smp_mass(w[j], m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(ws.kept + 3u * pos + 2u, mh::argmax_key(w[j] + y[g][j], i0 + j), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                ++pos;
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // every wave's entries
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        is_last = __hip_atomic_fetch_add(&ws.ctl->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                          gridDim.x - 1u
+                      ? 1u
+                      : 0u;
+    }
+    __syncthreads();
+    if (is_last == 0u) {
+        return;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the other workgroups' entries
+    const uint32_t K = __hip_atomic_load(&ws.ctl->kept, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned long long kb = 0ull;  // this thread's best draw key
+    if (K <= kKeptCap) {
+        const uint32_t t = threadIdx.x;
+        if (t < K) {
+            lk[t] = __hip_atomic_load(ws.kept + 3u * t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            lm[t] = __hip_atomic_load(ws.kept + 3u * t + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            lg[t] = __hip_atomic_load(ws.kept + 3u * t + 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (t == 0) {
+            tau_l = tau_k;
+        }
+        __syncthreads();
+        // z: the kept mass; entry t's cumulative mass (keys >= its key)
+        unsigned long long z = 0ull, cum = 0ull;
+        const uint32_t kt = t < K ? static_cast<uint32_t>(lk[t] >> 32) : 0u;
+        if (t < K) {
+            for (uint32_t j = 0; j < K; ++j) {
+                const unsigned long long mj = lm[j];
+                z += mj;
+                cum += static_cast<uint32_t>(lk[j] >> 32) >= kt ? mj : 0ull;
+            }
+            const unsigned long long target = smp_mass_target(z, p.top_p);
+            if (cum >= target) {
+                atomicMax(&tau_l, kt);  // LDS: the greatest qualifying key
+            }
+        }
+        __syncthreads();
+        const uint32_t tau = tau_l;
+        if (t < K && kt >= tau) {
+            kb = lg[t];
+        }
+    } else {
+        // the mass phase's radix rounds over every token, by this workgroup
+        SmpState st = {};
+        st.restrict_key = tau_k;
+        for (int round = 0; round < 3; ++round) {
+            for (int d = threadIdx.x; d < kDigits; d += kThreads) {
+                lmass[d] = 0ull;
+            }
+            __syncthreads();
+            const int shift = smp_shift(round), width = smp_width(round);
+            const uint32_t hi_mask = round == 0 ? 0u : ~((1u << (shift + width)) - 1u);
+            for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+                const float w = ws.w[i];
+                const uint32_t key = smp_fkey(w);
+                if ((key & hi_mask) == st.prefix && key >= st.restrict_key) {
+                    atomicAdd(&lmass[(key >> shift) & ((1u << width) - 1u)], smp_mass(w, m));
+                }
+            }
+            __syncthreads();
+            SmpPrev hv;
+            hv.in = st;
+#pragma unroll
+            for (int j = 0; j < kPer; ++j) {
+                hv.val[j] = lmass[threadIdx.x * kPer + j];
+            }
+            st = smp_decide(hv, 1, round, p, dl);
+        }
+        const uint32_t tau = st.tau_key;
+        for (uint32_t i0 = 4u * threadIdx.x; i0 < n; i0 += 4u * kThreads) {
+            const float4 v = *reinterpret_cast<const float4*>(ws.w + i0);
+            const float w[4] = {v.x, v.y, v.z, v.w};
+            const mh::u32x4 r = mh::philox4x32_10(mh::u32x4{i0 / 4u, p.pos, kDomain, 0u}, p.seed_lo, p.seed_hi);
+            const float g[4] = {mh::gumbel_of(r.x), mh::gumbel_of(r.y), mh::gumbel_of(r.z), mh::gumbel_of(r.w)};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (smp_fkey(w[j]) >= tau) {
+                    const unsigned long long kj = mh::argmax_key(w[j] + g[j], i0 + j);
+                    kb = kj > kb ? kj : kb;
+                }
+            }
+        }
+    }
+    kb = mh::wave_max_u64(kb);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        partk[wave] = kb;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int w = 1; w < kThreads / 64; ++w) {
+            kb = partk[w] > kb ? partk[w] : kb;
+        }
+        __hip_atomic_store(&ws.ctl->kept, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&ws.ctl->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (kb != 0ull && kb > __hip_atomic_load(best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+            __hip_atomic_fetch_max(best, kb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
 __global__ void k_smp_mark(const uint32_t* tok, uint32_t* seen, uint32_t n) {
     if (threadIdx.x == 0) {
         const uint32_t t = tok[0];
@@ -513,7 +748,8 @@ extern "C" int mh_sample_draw(const uint16_t* logits, uint32_t n, const uint32_t
                               size_t workspace_bytes, mh_stream_t stream) {
     const char* op = "mh_sample_draw";
     MH_ENSURE(logits && params && best, MH_ERR_INVALID, "%s: NULL argument", op);
-    MH_ENSURE(n > 0 && n % 4u == 0u, MH_ERR_INVALID, "%s: vocabulary %u not a positive multiple of 4", op, n);
+    MH_ENSURE(n > 0 && n % 4u == 0u && n <= 0x80000000u, MH_ERR_INVALID,
+              "%s: vocabulary %u not a positive multiple of 4 (at most 2^31)", op, n);
     MH_ENSURE(params->use_penalty == 0u || seen != nullptr, MH_ERR_INVALID, "%s: the penalty needs the seen set", op);
     MH_ENSURE(params->top_p > 0.0f, MH_ERR_INVALID, "%s: top_p must be in (0, 1]", op);
     MH_ENSURE(mh::aligned(logits, 8) && mh::aligned(best, 8) && mh::aligned(seen, 4), MH_ERR_ALIGN,
@@ -537,10 +773,13 @@ extern "C" int mh_sample_draw(const uint16_t* logits, uint32_t n, const uint32_t
         hipLaunchKernelGGL(k_smp_prep<false>, dim3(grid), dim3(kThreads), 0, s, logits, n, seen, *params, ws);
     }
     MH_TRY(mh::launch_status("k_smp_prep"));
-    // the rounds of this call: (phase, round); a count round 0 ran in prep
+    // the rounds of this call: (phase, round); a count round 0 ran in prep.
+    // With both on, the mass phase is decided over the top-k list by the
+    // kept-set draw's last workgroup (k_smp_draw_kept).
+    const bool kept_draw = use_k && use_p;
     int step = 0, pp = 0, pr = 0;
     for (int phase = 0; phase < 2; ++phase) {
-        if ((phase == 0 && !use_k) || (phase == 1 && !use_p)) {
+        if ((phase == 0 && !use_k) || (phase == 1 && (!use_p || kept_draw))) {
             continue;
         }
         for (int round = 0; round < 3; ++round) {
@@ -558,6 +797,11 @@ extern "C" int mh_sample_draw(const uint16_t* logits, uint32_t n, const uint32_t
             pr = round;
             ++step;
         }
+    }
+    if (kept_draw) {
+        hipLaunchKernelGGL(k_smp_draw_kept, dim3(grid), dim3(kThreads), 0, s, n, *params, ws, step - 1,
+                           reinterpret_cast<unsigned long long*>(best));
+        return mh::launch_status("k_smp_draw_kept");
     }
     hipLaunchKernelGGL(k_smp_draw, dim3(grid), dim3(kThreads), 0, s, n, *params, ws, step - 1, pp,
                        reinterpret_cast<unsigned long long*>(best));

@@ -426,6 +426,9 @@ def sample_gumbel(logits, n: int, seen, params: SampleParams, best, stream=None)
                                   _stream(stream)), "sample_gumbel")
 
 
+SAMPLE_ZERO_BYTES = 16640  # MH_SAMPLE_ZERO_BYTES: the kept-set workspace's head that must start zero
+
+
 def sample_workspace_bytes(n: int) -> int:
     """mh_sample_workspace_bytes: the kept-set draw's workspace for a vocabulary of n."""
     return int(load().mh_sample_workspace_bytes(n))

@@ -1,6 +1,7 @@
 """The C ABI on the CPU: the library loads, exports every declared symbol,
 and rejects bad arguments before touching the GPU runtime."""
 import ctypes
+import os
 
 import pytest
 
@@ -233,3 +234,17 @@ def test_sample_arguments():
     with pytest.raises(hip.MoltenError) as ei:  # the penalty reads the seen set
         hip.sample_gumbel(0x4000, 128000, None, hip.sample_params(1.0, 1, 0, penalty=1.2), 0x6000, stream=0)
     assert ei.value.code == hip.MH_ERR_INVALID
+
+
+def test_python_mirrors_of_header_constants():
+    """The sizes hip.py hands to callers match the header's defines."""
+    import re
+    text = open(os.path.join(os.path.dirname(__file__), "..", "include", "molten_hip.h")).read()
+
+    def define(name):
+        m = re.search(r"#define %s (\d+)u" % name, text)
+        assert m, name
+        return int(m.group(1))
+
+    assert hip.SAMPLE_ZERO_BYTES == define("MH_SAMPLE_ZERO_BYTES")
+    assert hip.ARGMAX_SLOTS == define("MH_ARGMAX_SLOTS")

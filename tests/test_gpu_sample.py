@@ -54,7 +54,7 @@ def test_sample_draw_bit_exact(dev, orc, n, temp, penalty, top_k, top_p, seed, p
     """The kept-set draw's key equals the oracle's bit for bit (integer
     thresholds: counts and fixed-point masses; the draw as the temperature
     draw), over repeated calls on one workspace whose scratch part starts as
-    garbage and whose first 16 KiB are left zero."""
+    garbage and whose head (hip.SAMPLE_ZERO_BYTES) is left zero."""
     rng = np.random.default_rng(n + top_k + pos)
     v = rng.normal(0, 3, n).astype(np.float32)
     # ties around the k-th largest and exact zeros
@@ -66,9 +66,9 @@ def test_sample_draw_bit_exact(dev, orc, n, temp, penalty, top_k, top_p, seed, p
     seen = rng.integers(0, 2 ** 32, (n + 31) // 32, dtype=np.uint64).astype(np.uint32)
     use_pen = penalty != 1.0
     ws_bytes = hip.sample_workspace_bytes(n)
-    # only the first 16 KiB must start at zero: the rest holds garbage
+    # only the head must start at zero: the rest holds garbage
     ws_host = np.full(ws_bytes, 0xA5, np.uint8)
-    ws_host[:16384] = 0
+    ws_host[:hip.SAMPLE_ZERO_BYTES] = 0
     ws = to_dev(ws_host)
     dl, ds = to_dev(logits), to_dev(seen)
     for call in range(3):
@@ -79,11 +79,43 @@ def test_sample_draw_bit_exact(dev, orc, n, temp, penalty, top_k, top_p, seed, p
         hip.sample_draw(dl, n, ds, p, best, ws, ws_bytes)
         got = int(from_dev(best, np.uint64)[0])
         assert got == want, (call, hex(got), hex(want))
-        assert not from_dev(ws, np.uint8)[:16384].any()  # the first round's histogram left zero
+        assert not from_dev(ws, np.uint8)[:hip.SAMPLE_ZERO_BYTES].any()  # counters and round 0's bins left zero
     # the drawn token is in the kept set
     w = layout.bf16_to_f32(logits).astype(np.float32) * np.float32(p.inv_temp)
     tok = (~got) & 0xffffffff
     assert use_pen or _keys_f32(w[tok]) >= tau
+
+
+@pytest.mark.parametrize("n,top_k,top_p,levels,seed", [
+    (128000, 1000, 0.9, 0, 21),   # a kept list longer than the finishing workgroup takes
+    (128000, 40, 0.5, 24, 22),    # few distinct values: thousands tied at the k-th largest
+    (128000, 200, 0.99, 0, 23),   # a list below the cap
+    (4096, 4095, 0.7, 8, 24),     # nearly every token kept, ties
+])
+def test_sample_draw_kept_list_and_ties(dev, orc, n, top_k, top_p, levels, seed):
+    """top-k with top-p: the mass phase decided over the kept list by the
+    draw's last workgroup, and, when the list is longer than it takes (large
+    k, or ties at the threshold), by its own radix rounds over every token;
+    bit for bit against the oracle over two calls on one workspace."""
+    rng = np.random.default_rng(seed)
+    v = rng.normal(0, 3, n).astype(np.float32)
+    if levels:
+        v = np.round(v * levels / 8.0) * np.float32(8.0 / levels)
+    logits = layout.f32_to_bf16(v.astype(np.float32))
+    seen = np.zeros((n + 31) // 32, np.uint32)
+    ws_bytes = hip.sample_workspace_bytes(n)
+    ws_host = np.full(ws_bytes, 0x5A, np.uint8)
+    ws_host[:hip.SAMPLE_ZERO_BYTES] = 0
+    ws = to_dev(ws_host)
+    dl, ds = to_dev(logits), to_dev(seen)
+    for call in range(2):
+        p = hip.sample_params(1.0, seed, call, 1.0, top_k, top_p)
+        want, tau = orc.sample_draw(logits, None, p.inv_temp, 1.0, False, top_k, p.top_p, seed, call)
+        best = to_dev(np.zeros(1, np.uint64))
+        hip.sample_draw(dl, n, ds, p, best, ws, ws_bytes)
+        got = int(from_dev(best, np.uint64)[0])
+        assert got == want, (call, hex(got), hex(want))
+        assert not from_dev(ws, np.uint8)[:hip.SAMPLE_ZERO_BYTES].any()
 
 
 def test_sample_mark_sets_the_bit(dev):
