@@ -38,6 +38,7 @@ constexpr int kMaxB = 8;
 constexpr int kSlotWords = 6;  // per (batch row, workgroup): lower bound, dropped bound, 4 candidates
 constexpr int kPerKind = kGrid / 64;  // a finisher lane's words of one kind (word kind * kGrid + workgroup)
 constexpr int kCand = 4;
+constexpr int kRecompute = 4;  // rows whose chunk-order values the finisher forms per round of loads
 constexpr uint32_t kArgSlots = MH_ARGMAX_SLOTS;
 constexpr uint32_t kMaxCand = kTileRows * 68;  // finisher's candidate list (a wave's stage buffer)
 constexpr uint32_t kSpinLimit = 1u << 24;
@@ -139,7 +140,7 @@ __device__ __forceinline__ float key_value(unsigned long long key) {
 // taken on.  Every row's loads go out before the first dot.
 template <int BITS, int U>
 __device__ void chunk_values(const MfmaArgs& a, const uint32_t (&rows)[U], const float (&xr)[32], float xs,
-                             bool live, uint32_t c, float (&out)[U]) {
+                             bool live, uint32_t c, float (&out)[U], uint32_t cnt = U) {
     mh::Chunk<BITS> ch[U];
     float s[U], b[U];
     const uint32_t g = (32u * c) / 64u;
@@ -151,9 +152,12 @@ __device__ void chunk_values(const MfmaArgs& a, const uint32_t (&rows)[U], const
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const float p = ch[u].dot(xr);
-        const float acc = live ? 0.0f + __builtin_fmaf(s[u], p, b[u] * xs) : 0.0f;
-        out[u] = mh::lane63(mh::wave_sum_lane63(acc));
+        out[u] = 0.0f;
+        if (static_cast<uint32_t>(u) < cnt) {  // uniform: rows past cnt repeat the last one
+            const float p = ch[u].dot(xr);
+            const float acc = live ? 0.0f + __builtin_fmaf(s[u], p, b[u] * xs) : 0.0f;
+            out[u] = mh::lane63(mh::wave_sum_lane63(acc));
+        }
     }
 }
 
@@ -445,8 +449,8 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         return;
     }
 
-    // ---- workgroup summary per batch row: greatest lower bound, the four
-    // greatest upper bounds (candidates), the greatest of the rest
+    // ---- workgroup summary per batch row: greatest lower bound, up to four
+    // candidates (upper bound and row), the greatest upper bound of the rest
     if (col) {
         m_lb[n][wave * 4 + q] = lbv;
         m_u1[n][wave * 4 + q] = u1;
@@ -455,8 +459,11 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
     }
     __syncthreads();
     // wave b < B summarises batch row b: lane e < 32 holds entry e (wave e / 4,
-    // quarter e % 4); the candidates are the four greatest keys (upper bound
-    // desc, row asc), taken one per round by a wave max
+    // quarter e % 4).  The candidates are the entries whose bf16 upper bound
+    // reaches the workgroup's lower bound when there are at most four of them,
+    // else the four greatest keys (upper bound desc, row asc); either way every
+    // row that can still reach the global lower bound is a candidate or raises
+    // the dropped bound, so the finisher decides the same
     const uint32_t last = gridDim.x - 1;
     if (wave < B) {
         const uint32_t b = static_cast<uint32_t>(wave);
@@ -468,11 +475,34 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         lb = mh::wave_max_f32(lb);
         unsigned long long out[kSlotWords];
         out[0] = mh::argmax_key(lb, 0u);
+        // the entries whose bf16 upper bound reaches this workgroup's lower
+        // bound (the others can never reach the global one); at most kCand of
+        // them (the usual case) are the candidates as they are, in lane order
+        const bool take = key != 0ull && static_cast<uint32_t>(key >> 32) >= mh::bf16_ge_threshold(lb);
+        unsigned long long tm = __ballot(take);
+        if (__popcll(tm) <= kCand) {
 #pragma unroll
-        for (int c = 0; c < kCand; ++c) {
-            const unsigned long long m = mh::wave_max_u64(key);
-            out[2 + c] = m != 0ull ? m : mh::argmax_key(-__builtin_inff(), 0xffffffffu);
-            key = key == m ? 0ull : key;  // keys are distinct (distinct rows)
+            for (int c = 0; c < kCand; ++c) {
+                unsigned long long m = mh::argmax_key(-__builtin_inff(), 0xffffffffu);
+                if (tm != 0ull) {
+                    const int pos = __builtin_ctzll(tm);
+                    m = (static_cast<unsigned long long>(static_cast<uint32_t>(
+                             __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(key >> 32)), pos)))
+                         << 32) |
+                        static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(key)), pos));
+                    tm &= tm - 1ull;
+                }
+                out[2 + c] = m;
+            }
+            key = take ? 0ull : key;
+        } else {
+            // the four greatest keys, one per round by a wave max
+#pragma unroll
+            for (int c = 0; c < kCand; ++c) {
+                const unsigned long long m = mh::wave_max_u64(key);
+                out[2 + c] = m != 0ull ? m : mh::argmax_key(-__builtin_inff(), 0xffffffffu);
+                key = key == m ? 0ull : key;  // keys are distinct (distinct rows)
+            }
         }
         // the rest of the entries' upper bounds join the dropped bound
         dmax = fmaxf(dmax, key != 0ull ? key_value(key) : -__builtin_inff());
@@ -512,6 +542,15 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         return;
     }
     const uint32_t b = static_cast<uint32_t>(wave);
+    // this lane's chunk of x for a recompute, loaded while the words arrive
+    const uint32_t C = K / 32u;
+    const bool live = static_cast<uint32_t>(lane) < C;
+    const uint32_t c = live ? static_cast<uint32_t>(lane) : 0u;
+    float xr[32], xs;
+    mh::load_x_chunk(a.x + static_cast<size_t>(b) * K + 32u * c, xr, xs);
+    if (BITS == 4) {
+        mh::q4_scale_x(xr);
+    }
     // word j: kind j / kPerKind, workgroup lane + 64 (j % kPerKind)
     constexpr int kWords = kSlotWords * kPerKind;
     static_assert(kWords <= 32, "pending mask");
@@ -588,29 +627,21 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         // chunk-order values of the candidates (or of every row), four rows'
         // loads at a time; the staged kernel's merge: NaN never wins, with no
         // other value (-inf, 0)
-        const uint32_t C = K / 32u;
-        const bool live = static_cast<uint32_t>(lane) < C;
-        const uint32_t c = live ? static_cast<uint32_t>(lane) : 0u;
-        float xr[32], xs;
-        mh::load_x_chunk(a.x + static_cast<size_t>(b) * K + 32u * c, xr, xs);
-        if (BITS == 4) {
-            mh::q4_scale_x(xr);
-        }
         const uint32_t count = all_rows ? a.n : nc;
         unsigned long long best = mh::argmax_key(-__builtin_inff(), 0u);
-        for (uint32_t i0 = 0; i0 < count; i0 += 4u) {
-            uint32_t rows[4];
+        for (uint32_t i0 = 0; i0 < count; i0 += kRecompute) {
+            uint32_t rows[kRecompute];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < kRecompute; ++u) {
                 const uint32_t i = i0 + u < count ? i0 + u : count - 1u;
                 rows[u] = all_rows ? i : cand[i];
             }
-            float vals[4];
-            chunk_values<BITS, 4>(a, rows, xr, xs, live, c, vals);
+            float vals[kRecompute];
+            chunk_values<BITS, kRecompute>(a, rows, xr, xs, live, c, vals, count - i0);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < kRecompute; ++u) {
                 const float val = mh::round_bf16(vals[u]);
-                if (val == val) {
+                if (val == val && i0 + u < count) {
                     const unsigned long long key = mh::argmax_key(val, rows[u]);
                     best = key > best ? key : best;
                 }
