@@ -253,6 +253,49 @@ def test_moe_prefill_config4_full_size(dev, orc, mode):
     assert_close(got["out"], want["out"], f"prefill out config 4 mode={mode} (all 4096 tokens)")
 
 
+@pytest.mark.parametrize("m,e,h,mode", [(300, 64, 2048, 1), (300, 64, 2048, 0), (4096, 64, 2048, 1),
+                                         (200, 48, 1024, 1), (200, 32, 1024, 0)])
+def test_moe_prefill_bf16_router_routing(dev, orc, m, e, h, mode):
+    """mh_moe_prefill's routing with a bf16 router, including expert counts
+    below 64 and K = 1024: ids and weights bit-exact against the oracle's
+    chunk-order logits routed on the CPU, and the stored logit of every chosen
+    expert equal to the oracle's bit for bit.  The router holds an exact
+    duplicate row (equal logits: the lower expert wins) and a row one bf16 ulp
+    from another (a near tie); x holds a zero token (64 equal logits) and one
+    with an infinite element."""
+    _log(f"bf16 router routing m={m} e={e} h={h} mode={mode}")
+    rng = np.random.default_rng(7 + m + e + mode)
+    topk, n_inter = 4, 512
+    gate, up, down = moe_weights(rng, e, h, n_inter)
+    r = layout.f32_to_bf16(rng.normal(0, 0.02, (e, h)).astype(np.float32))
+    r[7] = r[3]
+    r[11] = r[5]
+    r[11, 17] += 1
+    bias = rng.normal(0, 0.05, e).astype(np.float32) if mode == 0 else None
+    x = layout.synth_bf16(rng, (m, h))
+    x[5] = 0
+    x[9, 100] = 0x7f80
+    dg, _ = dev_quant(gate)
+    du, _ = dev_quant(up)
+    dd, _ = dev_quant(down)
+    total, offs = hip.moe_prefill_workspace(m, e, topk, h, n_inter)
+    ws = zeros_dev((total // 4,), np.uint32)
+    out = zeros_dev((m, h), np.uint16)
+    hip.moe_prefill(to_dev(r), None if bias is None else to_dev(bias), dg, du, dd, e, topk,
+                    to_dev(x), m, out, ws, total, mode=mode)
+    wsb = from_dev(ws, np.uint32).view(np.uint8)
+    ids = wsb[offs["ids"]:offs["ids"] + m * topk * 4].view(np.uint32).reshape(m, topk)
+    gw = wsb[offs["gw"]:offs["gw"] + m * topk * 2].view(np.uint16).reshape(m, topk)
+    lg = wsb[offs["logits"]:offs["logits"] + m * e * 4].view(np.float32).reshape(m, e)
+    z = orc.gemv_dense(r, x)
+    want_ids, want_gw = orc.route(z, bias, topk, mode)
+    np.testing.assert_array_equal(ids, want_ids, err_msg="ids")
+    np.testing.assert_array_equal(gw, want_gw, err_msg="weights")
+    rows = np.arange(m)[:, None]
+    np.testing.assert_array_equal(lg[rows, ids].view(np.uint32), z[rows, ids].view(np.uint32),
+                                  err_msg="chosen logits")
+
+
 def _dense_map(m, n, bm=128, bn=64):
     """Block map of a dense product (one matrix): (m0, n0, n0, m_end) per tile."""
     ents = [(m0, n0, n0, min(m0 + bm, m)) for m0 in range(0, m, bm) for n0 in range(0, n, bn)]
