@@ -127,17 +127,9 @@ __device__ __forceinline__ void load3_coherent(const uint32_t* p0, const uint32_
         : "memory");
 }
 
-// SBL: the gate/up scales and biases of a triple (12 rows of G groups, G a
-// multiple of 8 and at most kSbMaxG, rows 16-byte aligned) are read with one
-// 16-byte load per lane into the wave's LDS rows and taken from there: one
-// load instruction instead of twelve 2-byte loads, whose address processing
-// (64 lanes each) held up the issue of the triple's code loads.
-constexpr uint32_t kSbMaxG = 40;
-
-template <typename WT, int TK, int EB, bool STAMPS, bool SBL>
+template <typename WT, int TK, int EB, bool STAMPS>
 __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
     static_assert(kReadsPerThread == 3, "load3_coherent covers a thread's share");
-    __shared__ __attribute__((aligned(16))) uint16_t sb_l[SBL ? kWaves : 1][12][SBL ? kSbMaxG : 8];
     __shared__ __attribute__((aligned(16))) uint16_t act_l[kMaxAct];
     __shared__ __attribute__((aligned(16))) float actf_l[kMaxAct];
     __shared__ float xs_l[kMaxAct / 32];
@@ -288,20 +280,11 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
     const uint32_t gc = (32u * c) / a.gs;
     mh::Chunk<4> ch[6];
     uint16_t sv[6], bv[6];
-    // (SBL) lane l < 12 P loads 16-byte piece l % P of row array l / P =
-    // kind * 6 + q (kind 0 scales, 1 biases; q the ch index); lanes past 12 P
-    // reload piece 0 of array 0 and store nothing
-    const uint32_t sbp = G / 8u;
-    const bool sb_st = static_cast<uint32_t>(lane) < 12u * sbp;
-    const uint32_t sb_ra = sb_st ? static_cast<uint32_t>(lane) / sbp : 0u;
-    const uint32_t sb_pc = sb_st ? static_cast<uint32_t>(lane) % sbp : 0u;
-    uint4 sbv = make_uint4(0u, 0u, 0u, 0u);
     auto load_triple = [&](uint32_t t) {
         // activations past the end (last triple) load a valid row and are
         // never stored
         const uint32_t slot0 = (3u * t) / a.NI;
         const uint32_t i0 = 3u * t - slot0 * a.NI;
-        size_t rows[3];
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
             const bool wrap = i0 + j >= a.NI;
@@ -309,28 +292,14 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
             const uint32_t slot = past ? slot0 : slot0 + (wrap ? 1u : 0u);
             const uint32_t i = past ? i0 : i0 + j - (wrap ? a.NI : 0u);
             const uint32_t e = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(exv), slot));
-            rows[j] = static_cast<size_t>(e) * a.NI + i;
-        }
-        if constexpr (SBL) {  // first: the dots wait for it before their own rows
-            const uint32_t q = sb_ra % 6u, j = q / 2u;
-            const size_t row = j == 0u ? rows[0] : (j == 1u ? rows[1] : rows[2]);
-            const uint16_t* base = sb_ra < 6u ? ((q & 1u) ? a.usc : a.gsc) : ((q & 1u) ? a.ubi : a.gbi);
-            sbv = *reinterpret_cast<const uint4*>(base + row * G + 8u * sb_pc);
-        }
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            const size_t row = rows[j];
+            const size_t row = static_cast<size_t>(e) * a.NI + i;
             const size_t sbi = row * G + gc;
             ch[2 * j].load_nt(mh::uniform_ptr(reinterpret_cast<const char*>(a.gc) + row * row_bytes), c * 16u);
-            if constexpr (!SBL) {
-                sv[2 * j] = a.gsc[sbi];
-                bv[2 * j] = a.gbi[sbi];
-            }
+            sv[2 * j] = a.gsc[sbi];
+            bv[2 * j] = a.gbi[sbi];
             ch[2 * j + 1].load_nt(mh::uniform_ptr(reinterpret_cast<const char*>(a.uc) + row * row_bytes), c * 16u);
-            if constexpr (!SBL) {
-                sv[2 * j + 1] = a.usc[sbi];
-                bv[2 * j + 1] = a.ubi[sbi];
-            }
+            sv[2 * j + 1] = a.usc[sbi];
+            bv[2 * j + 1] = a.ubi[sbi];
         }
     };
     uint32_t t = gw;
@@ -358,16 +327,6 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
         mh::x_words_to_f32(xw, xr, xs);
         mh::q4_scale_x(xr);
         while (t < triples) {
-            if constexpr (SBL) {
-                if (sb_st) {
-                    *reinterpret_cast<uint4*>(&sb_l[wave][sb_ra][8u * sb_pc]) = sbv;
-                }
-#pragma unroll
-                for (int q = 0; q < 6; ++q) {
-                    sv[q] = sb_l[wave][q][gc];
-                    bv[q] = sb_l[wave][6 + q][gc];
-                }
-            }
             float h[8];
 #pragma unroll
             for (int q = 0; q < 6; ++q) {
@@ -580,15 +539,9 @@ int moe_decode_fused(const void* router, int router_dtype, const float* bias, in
     a.E = n_experts; a.K = K; a.NI = NI; a.gs = gate->group_size;
     const bool f32 = router_dtype == MH_DTYPE_F32;
     const bool eb1 = n_experts <= 64u;  // one expert per lane in the routing
-    const uint32_t G = K / gate->group_size;
-    const bool sbl = G % 8u == 0u && G <= kSbMaxG && mh::aligned(gate->scales, 16) && mh::aligned(gate->biases, 16) &&
-                     mh::aligned(up->scales, 16) && mh::aligned(up->biases, 16);
-#define MH_FUSED_LAUNCH_SB(TK, EB, ST, SB)                                                                      \
-    if (f32) hipLaunchKernelGGL((k_moe_decode_fused<float, TK, EB, ST, SB>), dim3(kGrid), dim3(kThreads), 0, stream, a); \
-    else hipLaunchKernelGGL((k_moe_decode_fused<uint16_t, TK, EB, ST, SB>), dim3(kGrid), dim3(kThreads), 0, stream, a);
-#define MH_FUSED_LAUNCH_ST(TK, EB, ST)              \
-    if (sbl) { MH_FUSED_LAUNCH_SB(TK, EB, ST, true) } \
-    else { MH_FUSED_LAUNCH_SB(TK, EB, ST, false) }
+#define MH_FUSED_LAUNCH_ST(TK, EB, ST)                                                                            \
+    if (f32) hipLaunchKernelGGL((k_moe_decode_fused<float, TK, EB, ST>), dim3(kGrid), dim3(kThreads), 0, stream, a); \
+    else hipLaunchKernelGGL((k_moe_decode_fused<uint16_t, TK, EB, ST>), dim3(kGrid), dim3(kThreads), 0, stream, a);
 #define MH_FUSED_LAUNCH_EB(TK, EB)          \
     if (stamps) { MH_FUSED_LAUNCH_ST(TK, EB, true) } \
     else { MH_FUSED_LAUNCH_ST(TK, EB, false) }
@@ -601,7 +554,6 @@ int moe_decode_fused(const void* router, int router_dtype, const float* bias, in
         case 3: MH_FUSED_LAUNCH(3) break;
         default: MH_FUSED_LAUNCH(4) break;
     }
-#undef MH_FUSED_LAUNCH_SB
 #undef MH_FUSED_LAUNCH_ST
 #undef MH_FUSED_LAUNCH_EB
 #undef MH_FUSED_LAUNCH
