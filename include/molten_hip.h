@@ -175,10 +175,10 @@ int mh_gemv_head_argmax(const mh_quant_weights* w, const uint16_t* x, uint64_t* 
  * the slots, writes the token ids and re-zeroes the slots, so no two
  * workgroups contend on one atomic.  scratch: MH_ARGMAX_SCRATCH_WORDS(batch)
  * u64 words, zeroed before the first call; the slots are left zero and the
- * last word counts the launches of the chunk-order kernels' finisher (their
- * keys carry a tag of the count, so a key written late after an expired
- * wait is never taken for a later launch's; the matrix-core path keeps no
- * count); calls that overlap on one scratch buffer race.  When the
+ * last word counts the finisher's launches (every published key carries a
+ * tag of the count, so a key written late after an expired wait is never
+ * taken for a later launch's); calls that overlap on one scratch buffer
+ * race.  When the
  * collector's bounded wait expires the ids are 0xffffffff and
  * MH_STATUS_ARGMAX_WAIT is set.  No reference counterpart (BASELINE configs
  * 2 and 5 store the logits; molten's head stores none). */

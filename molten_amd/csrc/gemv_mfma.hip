@@ -135,6 +135,19 @@ __device__ __forceinline__ float key_value(unsigned long long key) {
     return __uint_as_float((o & 0x7fffffffu & neg) | (~o & ~neg));
 }
 
+// A word a workgroup publishes for the finisher: an argmax_key's high word
+// (the orderable value), then the launch's 8-bit tag and 24 low bits (~row
+// of a candidate, rows < 2^24; 0 for none; all ones for a bound).  The
+// finisher takes only words with its launch's tag, so neither a word an
+// earlier launch's workgroup wrote late (after that finisher's wait expired)
+// nor leftover scratch contents are read as this launch's (consecutive
+// launches differ in tag).
+constexpr uint32_t kRowMask = 0xffffffu;
+__device__ __forceinline__ unsigned long long pack_word(unsigned long long key, uint32_t tag, uint32_t low24) {
+    return (key & 0xffffffff00000000ull) | (tag << 24) | low24;
+}
+__device__ __forceinline__ uint32_t word_tag(unsigned long long w) { return static_cast<uint32_t>(w) >> 24; }
+
 // Chunk-order values of U rows for one batch row (the staged kernel's
 // formula: lane c owns chunk c, K <= 2048): the exact values the argmax is
 // taken on.  Every row's loads go out before the first dot.
@@ -358,6 +371,13 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
     const uint32_t first_c = first < n_tiles ? first : 0u;
     auto tile_c = [&](uint32_t st) { return n_stages > 0u ? tile_of(st < n_stages ? st : last_st) : first_c; };
     auto stage_c = [&](uint32_t st) { return (st < n_stages ? st : last_st) % n_st; };
+    // the launch count (the scratch word after the slots; the finisher bumps
+    // it once every workgroup has published), read before x so that the wait
+    // for x covers it
+    const unsigned long long launches_v =
+        a.slots != nullptr
+            ? __hip_atomic_load(a.slots + static_cast<size_t>(B) * kArgSlots, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+            : 0ull;
     // ---- x to LDS in operand order (columns >= B zero), clamped addresses,
     // no branches
     constexpr int kXPer = kMaxG * 8 * 16 / kThreads;
@@ -380,6 +400,11 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         const bool live_col = u % 16u < static_cast<uint32_t>(B);
         xl[u] = live_col ? xv[j] : mh::u32x4{0u, 0u, 0u, 0u};
     }
+    // (uniform, taken now that x is in: no later wait for the count)
+    const unsigned long long launches =
+        (static_cast<unsigned long long>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(launches_v >> 32))) << 32) |
+        __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(launches_v));
+    const uint32_t tag = static_cast<uint32_t>(launches % 255ull) + 1u;
 #pragma unroll
     for (int u = 0; u < kDepth - 1; ++u) {
         issue(tile_c(u), stage_c(u), pbuf[u], svbuf[u], bvbuf[u]);
@@ -508,6 +533,11 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         dmax = fmaxf(dmax, key != 0ull ? key_value(key) : -__builtin_inff());
         dmax = mh::wave_max_f32(dmax);
         out[1] = mh::argmax_key(dmax, 0u);
+        // as tagged words
+#pragma unroll
+        for (int j = 0; j < kSlotWords; ++j) {
+            out[j] = pack_word(out[j], tag, static_cast<uint32_t>(out[j]) & kRowMask);
+        }
         // word j of this workgroup at slot j * kGrid + workgroup
         if (blockIdx.x != last) {
             if (lane < kSlotWords) {
@@ -532,7 +562,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
 
     // ---- finisher (the last workgroup: every other one has started).  Wave
     // b takes batch row b: it reads the other workgroups' words (polling the
-    // ones not yet written), clears them, and forms the greatest lower bound,
+    // ones without this launch's tag), clears them, and forms the greatest lower bound,
     // the greatest dropped upper bound and the candidates.  The argmax row is
     // always a candidate unless a dropped bound reaches the lower bound, so a
     // single candidate is the answer; several are recomputed in chunk order;
@@ -563,10 +593,10 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
     uint32_t pend = 0;
 #pragma unroll
     for (int j = 0; j < kWords; ++j) {
-        // missing workgroups read as 1: high word 0 (the least key), low word
-        // nonzero, never a candidate
-        v[j] = word_valid(j) ? __hip_atomic_load(sl + word_at(j), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1ull;
-        pend |= (v[j] == 0ull ? 1u : 0u) << j;
+        // missing workgroups read as the least value with no candidate
+        v[j] = word_valid(j) ? __hip_atomic_load(sl + word_at(j), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                             : pack_word(0ull, tag, 0u);
+        pend |= (word_tag(v[j]) != tag ? 1u : 0u) << j;
     }
     uint32_t spins = 0;
     while (__any(pend != 0u) && ++spins < kSpinLimit) {
@@ -580,7 +610,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         }
 #pragma unroll
         for (int j = 0; j < kWords; ++j) {
-            if (v[j] != 0ull) {
+            if (word_tag(v[j]) == tag) {
                 pend &= ~(1u << j);
             }
         }
@@ -595,6 +625,10 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         olb = max(olb, static_cast<uint32_t>(v[j] >> 32));
         odu = max(odu, static_cast<uint32_t>(v[kPerKind + j] >> 32));
     }
+    if (b == 0u && lane == 0) {  // every workgroup has read the count by now (or the wait expired)
+        __hip_atomic_store(a.slots + static_cast<size_t>(B) * kArgSlots, launches + 1ull, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
     const float lb = key_value(static_cast<unsigned long long>(mh::wave_max_u32(olb)) << 32);
     const float dmax = key_value(static_cast<unsigned long long>(mh::wave_max_u32(odu)) << 32);
     // a candidate's bf16 upper bound reaches lb: one compare of the high word
@@ -603,13 +637,14 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
     uint32_t* const cand = stg[wave];
     uint32_t nc = 0;
     auto collect = [&](unsigned long long key, bool valid) {
-        const bool take = valid && static_cast<uint32_t>(key) != 0u && static_cast<uint32_t>(key >> 32) >= thr;
+        const bool take = valid && (static_cast<uint32_t>(key) & kRowMask) != 0u &&
+                          static_cast<uint32_t>(key >> 32) >= thr;
         const unsigned long long m = __ballot(take);
         if (m != 0ull) {  // uniform: most words hold no candidate
             if (take) {
                 cand[nc + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u))] =
-                    ~static_cast<uint32_t>(key);
+                    ~static_cast<uint32_t>(key) & kRowMask;
             }
             nc += static_cast<uint32_t>(__popcll(m));
         }
@@ -693,7 +728,7 @@ int gemv_mfma(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint64_
               uint32_t batch, hipStream_t stream) {
     const uint32_t K = w->in_features;
     if (batch < 2 || batch > static_cast<uint32_t>(kMaxB) || w->group_size != 64u || K % (64u * kStageGroups) != 0 ||
-        K > kMaxK || w->out_features % kTileRows != 0 || !mh::aligned(x, 16) || !mh::aligned(w->codes, 8) ||
+        K > kMaxK || w->out_features % kTileRows != 0 || w->out_features > kRowMask || !mh::aligned(x, 16) || !mh::aligned(w->codes, 8) ||
         !mh::aligned(w->scales, 8) || !mh::aligned(w->biases, 8) ||
         (y != nullptr && !mh::aligned(y, 8)) || (slots != nullptr && ids == nullptr)) {
         return MH_ERR_UNSUPPORTED;

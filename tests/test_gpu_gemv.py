@@ -32,11 +32,10 @@ def _bf16_ulp(v):
 
 def assert_scratch(scratch, n, k, batch, launches):
     """The finisher's slots are left zero; the last word counts the
-    chunk-order kernels' finisher launches (the matrix-core kernel's
-    finisher keeps no count)."""
+    finisher's launches (chunk-order and matrix-core kernels alike)."""
     sc = from_dev(scratch, np.uint64)
     assert not sc[:-1].any()
-    assert int(sc[-1]) == (0 if _mfma_path(n, k, batch) else launches)
+    assert int(sc[-1]) == launches
 
 
 def assert_logits(got, want, n, k, batch, gs=64):
@@ -223,6 +222,48 @@ def test_argmax_ignores_keys_of_earlier_launches(dev, orc):
         hip.gemv_quant_argmax(w, xd, None, scratch, ids, 1)
         assert int(from_dev(ids, np.uint32)[0]) == want
         assert_scratch(scratch, n, k, 1, launch + 1)
+    assert hip.device_status(clear=True) == 0
+
+
+def test_mfma_argmax_ignores_untagged_words(dev, orc):
+    """The matrix-core finisher takes only words with its launch's tag.
+    Before each launch every slot of every batch row is filled from the host
+    with words that would decide the argmax if taken (the greatest lower
+    bound and candidates of the wrong rows): before the first launch random
+    words whose tag is not 1, before the next ones the previous launch's tag.
+    The finisher reads some slots before their workgroup publishes, so it
+    meets the planted words; the ids stay the oracle's, the slots are left
+    zero and the launch count advances."""
+    rng = np.random.default_rng(4343)
+    n, k, batch = 65536, 2048, 8
+    h = layout.synth_quant(rng, n, k, 4)
+    x = layout.synth_bf16(rng, (batch, k))
+    want = [orc.argmax_bf16(row) for row in orc.gemv_quant(h, x, batch)]
+    w, keep = dev_quant(h)
+    xd = to_dev(x)
+    scratch = zeros_dev((hip.argmax_scratch_words(batch),), np.uint64)
+    ids = empty_dev((batch,), np.uint32)
+    hip.device_status(clear=True)
+    # the slots the finisher reads: word j of workgroup g (< 255) of batch
+    # row r at r * ARGMAX_SLOTS + 256 j + g, six words per workgroup
+    used = np.array([r * hip.ARGMAX_SLOTS + 256 * j + g for r in range(batch) for j in range(6)
+                     for g in range(255)])
+    for launch in range(3):
+        sc = from_dev(scratch, np.uint64).copy()
+        assert int(sc[-1]) == launch
+        if launch == 0:
+            junk = rng.integers(0, 2**63, used.size, dtype=np.uint64)
+            tags = (junk >> np.uint64(24)) & np.uint64(0xFF)
+            junk[tags == 1] ^= np.uint64(1 << 25)  # never this launch's tag
+            sc[used] = junk
+        else:
+            # the greatest finite value, the previous launch's tag, row 65535
+            stale = np.uint64((launch - 1) % 255 + 1)
+            sc[used] = (np.uint64(0xFF7F0000) << np.uint64(32)) | (stale << np.uint64(24)) | np.uint64(0xFF0000)
+        scratch.copy_(to_dev(sc))
+        hip.gemv_quant_argmax(w, xd, None, scratch, ids, batch)
+        assert [int(v) for v in from_dev(ids, np.uint32)] == want
+        assert_scratch(scratch, n, k, batch, launch + 1)
     assert hip.device_status(clear=True) == 0
 
 
