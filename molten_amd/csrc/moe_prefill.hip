@@ -180,9 +180,13 @@ __global__ __launch_bounds__(256) void k_silu_mul(const uint16_t* gate, const ui
 
 // out[t, c] = bf16( sum_r f32(bf16(w[t,r] * sorted[slotpos[t,r], c])) ), r
 // ascending from +0; eight columns per thread.
+// TK = topk: a token's slot positions and weights are read together, then
+// its TK rows' pieces together (two round trips, not 2 TK), and summed in
+// slot order.
+template <int TK>
 __global__ __launch_bounds__(256) void k_combine(const uint16_t* sorted, const uint32_t* slotpos,
                                                  const uint16_t* w, uint16_t* out, uint32_t m,
-                                                 uint32_t h, uint32_t topk, uint32_t n_sorted) {
+                                                 uint32_t h, uint32_t n_sorted) {
     const uint32_t h8 = h / 8;
     const size_t total = static_cast<size_t>(m) * h8;
     for (size_t t = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
@@ -191,15 +195,25 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t* sorted, const u
         float acc[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-        for (uint32_t r = 0; r < topk; ++r) {
-            const uint32_t p = min(slotpos[static_cast<size_t>(tok) * topk + r], n_sorted - 1);
-            const float wr = mh::bf16_to_f32(w[static_cast<size_t>(tok) * topk + r]);
-            const uint4 v = reinterpret_cast<const uint4*>(sorted + static_cast<size_t>(p) * h)[c];
-            const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+        uint32_t p[TK];
+        float wr[TK];
+#pragma unroll
+        for (int r = 0; r < TK; ++r) {
+            p[r] = min(slotpos[static_cast<size_t>(tok) * TK + r], n_sorted - 1);
+            wr[r] = mh::bf16_to_f32(w[static_cast<size_t>(tok) * TK + r]);
+        }
+        uint4 v[TK];
+#pragma unroll
+        for (int r = 0; r < TK; ++r) {
+            v[r] = reinterpret_cast<const uint4*>(sorted + static_cast<size_t>(p[r]) * h)[c];
+        }
+#pragma unroll
+        for (int r = 0; r < TK; ++r) {
+            const uint32_t u[4] = {v[r].x, v[r].y, v[r].z, v[r].w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                acc[2 * j] = acc[2 * j] + mh::round_bf16(wr * mh::bf16lo(u[j]));
-                acc[2 * j + 1] = acc[2 * j + 1] + mh::round_bf16(wr * mh::bf16hi(u[j]));
+                acc[2 * j] = acc[2 * j] + mh::round_bf16(wr[r] * mh::bf16lo(u[j]));
+                acc[2 * j + 1] = acc[2 * j + 1] + mh::round_bf16(wr[r] * mh::bf16hi(u[j]));
             }
         }
         uint32_t o[4];
@@ -638,8 +652,18 @@ int mh_moe_combine_rows(const uint16_t* sorted, const uint32_t* slotpos, const u
     MH_ENSURE(mh::aligned(sorted, 16) && mh::aligned(out, 16), MH_ERR_ALIGN,
               "mh_moe_combine_rows: rows must be 16-byte aligned");
     if (m == 0) return MH_OK;
-    hipLaunchKernelGGL(k_combine, dim3(grid_for(static_cast<size_t>(m) * h / 8)), dim3(256), 0,
-                       mh::as_stream(stream), sorted, slotpos, weights, out, m, h, topk, m * topk);
+    const dim3 grid(grid_for(static_cast<size_t>(m) * h / 8));
+    const hipStream_t st = mh::as_stream(stream);
+#define MH_COMBINE(TK)                                                                                   \
+    case TK:                                                                                             \
+        hipLaunchKernelGGL(k_combine<TK>, grid, dim3(256), 0, st, sorted, slotpos, weights, out, m, h, m * TK); \
+        break;
+    switch (topk) {
+        MH_COMBINE(1) MH_COMBINE(2) MH_COMBINE(3) MH_COMBINE(4)
+        MH_COMBINE(5) MH_COMBINE(6) MH_COMBINE(7) MH_COMBINE(8)
+        default: break;
+    }
+#undef MH_COMBINE
     return mh::launch_status("mh_moe_combine_rows");
 }
 
