@@ -33,7 +33,8 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 
-# Algorithmic bytes per step.
+# Algorithmic bytes per step: every weight byte (codes, scales, biases) read
+# once, plus the inputs and outputs.
 BYTES = {
     "config1": 2_367_488,
     "config2": 75_632_644,

@@ -5,7 +5,7 @@
  * This header is the drop-in boundary.  Each launcher replaces one operator
  * wrapper of the reference's Rust/Metal operator layer; the replaced wrapper
  * is cited as file:line under /root/reference.  The Rust side binds these
- * with a thin `src/hip.rs` and keeps the operator
+ * with a thin `src/hip.rs` of extern "C" declarations and keeps the operator
  * signatures of the src/kernels/ modules.
  *
  * Conventions

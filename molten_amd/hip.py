@@ -5,8 +5,8 @@ Each function mirrors one operator wrapper of the reference's Rust layer
 name, same argument order and meaning, and it raises `MoltenError` where the
 reference's `ensure!` would return an error.  Tensors are torch tensors on
 the GPU (only their device pointers cross the C ABI) or plain integer device
-addresses.  This is the Python counterpart of the Rust `src/hip.rs` binding
-shown in INTEGRATION.md.
+addresses.  This is the Python counterpart of a Rust `src/hip.rs` binding
+(extern "C" declarations of the same functions).
 
 The library must be built (molten_amd/libmolten_hip.so); importing this
 module without it raises: there is no CPU fallback.
