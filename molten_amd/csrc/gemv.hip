@@ -317,6 +317,8 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
         mh::x_words_to_f32(xw, xr, xs);
         if (BITS == 4) {
             mh::q4_scale_x(xr);
+        } else {
+            mh::q6_scale_x(xr);
         }
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
@@ -357,7 +359,12 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
             for (int r = 0; r < R; ++r) {
                 const uint32_t rr = FAST ? grp * R + r : min(static_cast<uint32_t>(grp * R + r), nrows - 1u);
                 const uint2 w = sbp[rr * G + gc];
-                const float p = ch[r].dot(xr);
+                float p;
+                if constexpr (BITS == 6) {
+                    p = ch[r].dot_s(xr);  // x scaled by q6_scale_x above
+                } else {
+                    p = ch[r].dot(xr);
+                }
                 const float hv = __builtin_fmaf(__uint_as_float(w.x), p, __uint_as_float(w.y) * xs);
                 tw[(grp * R + r) * 64 + lane] = live ? hv : 0.0f;
             }

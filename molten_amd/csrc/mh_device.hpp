@@ -405,6 +405,46 @@ __device__ __forceinline__ float q6_chunk_dot(const uint32_t (&w)[6], const floa
     return p;
 }
 
+// The same with x pre-scaled by q6_scale_x (positions 4j + 3 times 1/4,
+// exact).  Of every 3 bytes (4 codes), code 4j sits in bits 0-5 of the first
+// byte and code 4j + 3 in bits 2-7 of the third: both are converted straight
+// from their byte of the word masked once (v_cvt_f32_ubyte: q and 4q), the
+// two codes between them with a field extract and a conversion.  q x and
+// (4q)(x / 4) are the same reals, so the chain equals fma(q_k, x_k, p) in
+// ascending k with one VALU op less for half the codes.
+__host__ __device__ constexpr uint32_t q6_byte_mask(int d) {
+    uint32_t m = 0;
+    for (int k = 0; k < 4; ++k) {
+        const int b = 4 * d + k;
+        m |= (b % 3 == 0 ? 0x3fu : (b % 3 == 2 ? 0xfcu : 0u)) << (8 * k);
+    }
+    return m;
+}
+__device__ __forceinline__ float q6_chunk_dot_s(const uint32_t (&w)[6], const float* xr) {
+    uint32_t m[6];
+#pragma unroll
+    for (int d = 0; d < 6; ++d) {
+        m[d] = opaque(w[d] & q6_byte_mask(d));
+    }
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const int bit = 6 * i;
+        const int d = bit >> 5;
+        const int o = bit & 31;
+        float v;
+        if ((bit & 7) == 0 || (bit & 7) == 2) {
+            v = ubyte_f32(m[(bit >> 3) >> 2], (bit >> 3) & 3);
+        } else if (o + 6 <= 32) {
+            v = static_cast<float>((w[d] >> o) & 63u);
+        } else {
+            v = static_cast<float>(__builtin_amdgcn_alignbit(w[d + 1], w[d], o) & 63u);
+        }
+        p = __builtin_fmaf(v, xr[i], p);
+    }
+    return p;
+}
+
 // A lane's 32-element bf16 chunk of x: the raw words (16-byte loads when the
 // chunk is aligned), then as f32 plus the ascending sum.  Split so a kernel
 // can issue its weight loads before it waits for x.
@@ -456,6 +496,14 @@ __device__ __forceinline__ void load_x_chunk(const uint16_t* xp, float (&xr)[32]
     uint32_t xw[16];
     load_x_words(xp, xw);
     x_words_to_f32(xw, xr, xs);
+}
+
+// Scale a raw x chunk for q6_chunk_dot_s: positions 4j + 3 times 1/4 (exact).
+__device__ __forceinline__ void q6_scale_x(float (&xr)[32]) {
+#pragma unroll
+    for (int i = 3; i < 32; i += 4) {
+        xr[i] = xr[i] * 0.25f;
+    }
 }
 
 // Scale a raw x chunk for q4_chunk_dot: odd positions times 1/16 (exact).
@@ -515,6 +563,7 @@ struct Chunk<6> {
         w[0] = a.x; w[1] = a.y; w[2] = b.x; w[3] = b.y; w[4] = c.x; w[5] = c.y;
     }
     __device__ __forceinline__ float dot(const float* xr) const { return q6_chunk_dot(w, xr); }
+    __device__ __forceinline__ float dot_s(const float* xr) const { return q6_chunk_dot_s(w, xr); }
 };
 
 template <>
