@@ -11,13 +11,18 @@
 namespace {
 
 // Row ids[t] of the table into out[t, :].  Workgroup (x, t): one wave, lane
-// l dequantizes chunk 64 x + l (32 codes) of token t's row.
+// l dequantizes chunk 64 x + l (32 codes) of token t's row.  A wave whose 64
+// chunks are all in the row passes its 4 KB through the LDS, so that each
+// store instruction writes 1 KB contiguous instead of 16 bytes per lane at a
+// 64-byte stride.
 __global__ __launch_bounds__(64) void k_gather_rows_q6(const uint32_t* codes, const uint16_t* scales,
                                                        const uint16_t* biases, const uint32_t* ids, uint16_t* out,
                                                        uint32_t k, uint32_t n_rows) {
+    __shared__ uint4 tr[4 * 64];  // the wave's 16-byte pieces in row order
     const uint32_t c = blockIdx.x * 64u + threadIdx.x;
     const uint32_t t = blockIdx.y;
     const uint32_t C = k / 32u;
+    const bool full = blockIdx.x * 64u + 64u <= C;  // uniform
     if (c >= C) {
         return;
     }
@@ -32,6 +37,19 @@ __global__ __launch_bounds__(64) void k_gather_rows_q6(const uint32_t* codes, co
     const float b = mh::bf16_to_f32(biases[static_cast<size_t>(row) * groups + c / 2u]);
     uint32_t packed[16];
     mh::dequant_chunk<6>(ch.w, s, b, packed);
+    if (full) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            tr[4u * threadIdx.x + q] = make_uint4(packed[4 * q], packed[4 * q + 1], packed[4 * q + 2], packed[4 * q + 3]);
+        }
+        __builtin_amdgcn_wave_barrier();
+        uint4* row = reinterpret_cast<uint4*>(out + static_cast<size_t>(t) * k + 2048u * blockIdx.x);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            row[64u * j + threadIdx.x] = tr[64u * j + threadIdx.x];
+        }
+        return;
+    }
     uint4* dst = reinterpret_cast<uint4*>(out + static_cast<size_t>(t) * k + 32u * c);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
