@@ -752,9 +752,15 @@ int gemv_common(const char* op, const mh_quant_weights* w, const uint16_t* x, ui
 // ------------------------------------------------------------- dequant ---
 
 template <int BITS>
+// Thread t dequantizes chunk t of the [n, C] chunks, whose 32 values are
+// out[32 t .. 32 t + 31]: a wave's 64 chunks are 4 KB contiguous, which a
+// full wave passes through the LDS so that each store instruction writes
+// 1 KB contiguous (16 bytes per lane at a 64-byte stride otherwise).
 __global__ __launch_bounds__(256) void k_dequant(const uint32_t* codes, const uint16_t* scales,
                                                  const uint16_t* biases, uint16_t* out,
                                                  uint32_t n, uint32_t k, uint32_t gs) {
+    __shared__ uint4 tr[4][4 * 64];  // per wave: its 16-byte pieces in output order
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t C = k / 32u;
     const size_t total = static_cast<size_t>(n) * C;
     const uint32_t row_words = k * BITS / 32u;
@@ -770,6 +776,21 @@ __global__ __launch_bounds__(256) void k_dequant(const uint32_t* codes, const ui
         const float b = mh::bf16_to_f32(biases[static_cast<size_t>(row) * groups + g]);
         uint32_t packed[16];
         mh::dequant_chunk<BITS>(ch.w, s, b, packed);
+        const size_t t0 = t - lane;
+        if (t0 + 64u <= total) {  // uniform: a full wave
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                tr[wave][4u * lane + q] = make_uint4(packed[4 * q], packed[4 * q + 1], packed[4 * q + 2], packed[4 * q + 3]);
+            }
+            __builtin_amdgcn_wave_barrier();
+            uint4* base = reinterpret_cast<uint4*>(out + 32u * t0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                base[64u * j + lane] = tr[wave][64u * j + lane];
+            }
+            __builtin_amdgcn_wave_barrier();  // the next round's writes after these reads
+            continue;
+        }
         uint4* dst = reinterpret_cast<uint4*>(out + static_cast<size_t>(row) * k + 32u * c);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
