@@ -250,10 +250,12 @@ constexpr int kMaxGroups = 64;  // K / group size <= 2048 / 32
 // FAST: K == 2048, group size 64 and N a multiple of kBlockRows (every lane
 // owns a chunk, 32 groups per row, no partial block).  ARGMAX: per-lane
 // bests, a DPP wave argmax, then the finisher (or the reference's atomic
-// max).
-template <int BITS, bool FAST, bool ARGMAX, int NG>
+// max).  WV: waves per workgroup (2 only without the argmax, whose
+// publication and collector take 4).
+template <int BITS, bool FAST, bool ARGMAX, int NG, int WV = kWaves>
 __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
     static_assert(NG == 1 || NG == 2, "one or two 4-row groups per block");
+    static_assert(WV == kWaves || (WV == 2 && !ARGMAX), "two-wave workgroups only without the argmax");
     constexpr int R = kGroupRows, BR = NG * R;
     constexpr int GM = FAST ? 32 : kMaxGroups;     // staged groups per row
     constexpr int NSB = BR * GM / 128;              // scale / bias word loads per lane
@@ -273,7 +275,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
     const uint32_t gc = FAST ? static_cast<uint32_t>(lane) / 2u : (32u * c) / a.gs;
     const uint32_t row_bytes = FAST ? 2048u * BITS / 8u : a.row_words * 4u;
     const uint32_t n_blocks = (N + BR - 1) / BR;
-    const uint32_t stride = gridDim.x * kWaves;
+    const uint32_t stride = gridDim.x * WV;
 
     uint32_t xw[16];
     if (wave == 0) {
@@ -306,7 +308,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
     // the first block's loads go out unconditionally (a wave past the last
     // block re-reads it; only the last workgroup can have one), so that no
     // path without them meets the x conversion's wait
-    const uint32_t blk0 = blockIdx.x * kWaves + wave;
+    const uint32_t blk0 = blockIdx.x * WV + wave;
     issue(min(blk0, n_blocks - 1u));
 
     // x: wave 0 converts, every wave reads after the barrier
@@ -565,7 +567,7 @@ constexpr int kWgPerCu = 4;
 
 template <typename K>
 int launch(K kernel, const GemvArgs& a, uint32_t grid, size_t lds, hipStream_t stream,
-           const char* name) {
+           const char* name, uint32_t threads = kThreads) {
     if (lds > 64u * 1024u) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -574,7 +576,7 @@ int launch(K kernel, const GemvArgs& a, uint32_t grid, size_t lds, hipStream_t s
             return mh::hip_error(e, name);
         }
     }
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), lds, stream, a);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(threads), lds, stream, a);
     return mh::launch_status(name);
 }
 
@@ -666,7 +668,20 @@ int launch_rows(const GemvArgs& a, hipStream_t stream) {
     const bool small = blocks8 < static_cast<uint32_t>(mh::cu_count()) * 4u * kWaves;
     const bool fast = a.k == 2048u && a.gs == 64u && a.n % (small ? kGroupRows : kBlockRows) == 0u;
     if (small) {
-        const uint32_t grid = grid_for((a.n + kGroupRows - 1) / kGroupRows, kRowsGridCap);
+        // between one and four 4-row blocks per CU (no argmax): two-wave
+        // workgroups, so the blocks spread over twice the CUs (2048 x 2048:
+        // 3.17 -> 3.08 us; fewer or more blocks measured slower that way)
+        const uint32_t units = (a.n + kGroupRows - 1) / kGroupRows;
+        const uint32_t cus = static_cast<uint32_t>(mh::cu_count());
+        if constexpr (!ARGMAX) {
+            if (units >= cus && units <= 4u * cus) {
+                const uint32_t want = (units + 1u) / 2u;
+                const uint32_t grid = want < kRowsGridCap ? want : kRowsGridCap;
+                return fast ? launch(k_gemv_rows<BITS, true, false, 1, 2>, a, grid, 0, stream, "k_gemv_rows", 128u)
+                            : launch(k_gemv_rows<BITS, false, false, 1, 2>, a, grid, 0, stream, "k_gemv_rows", 128u);
+            }
+        }
+        const uint32_t grid = grid_for(units, kRowsGridCap);
         return fast ? launch(k_gemv_rows<BITS, true, ARGMAX, 1>, a, grid, 0, stream, "k_gemv_rows")
                     : launch(k_gemv_rows<BITS, false, ARGMAX, 1>, a, grid, 0, stream, "k_gemv_rows");
     }
