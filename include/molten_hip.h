@@ -175,13 +175,17 @@ int mh_gemv_head_argmax(const mh_quant_weights* w, const uint16_t* x, uint64_t* 
  * the slots, writes the token ids and re-zeroes the slots, so no two
  * workgroups contend on one atomic.  scratch: MH_ARGMAX_SCRATCH_WORDS(batch)
  * u64 words, zeroed before the first call; the slots are left zero and the
- * last word counts the finisher's launches (every published key carries a
- * tag of the count, so a key written late after an expired wait is never
- * taken for a later launch's); calls that overlap on one scratch buffer
- * race.  When the
+ * last word counts the finisher's launches in bits 0..62 (every published
+ * key carries a tag of the count, so a key an earlier launch's workgroup
+ * wrote before that launch's collector gave up is never taken for a later
+ * launch's); calls that overlap on one scratch buffer race.  When the
  * collector's bounded wait expires the ids are 0xffffffff and
- * MH_STATUS_ARGMAX_WAIT is set.  No reference counterpart (BASELINE configs
- * 2 and 5 store the logits; molten's head stores none). */
+ * MH_STATUS_ARGMAX_WAIT is set; the collector then also sets bit 63 of the
+ * count word, because a workgroup that started only after it gave up
+ * publishes under the next launch's tag: the next launch reports the same
+ * way (ids 0xffffffff, the status bit), re-zeroes the slots and clears the
+ * bit, and the launch after it is exact again.  No reference counterpart
+ * (BASELINE configs 2 and 5 store the logits; molten's head stores none). */
 #define MH_ARGMAX_SLOTS 2048u
 #define MH_ARGMAX_SCRATCH_WORDS(batch) (MH_ARGMAX_SLOTS * (batch) + 1u)
 int mh_gemv_quant_argmax(const mh_quant_weights* w, const uint16_t* x, uint16_t* y,

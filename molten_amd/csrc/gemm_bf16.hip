@@ -200,14 +200,12 @@ int gemm_nt(const char* op, const uint16_t* a, const uint16_t* b, uint16_t* c, u
                            b, c, m, n, k);
         return mh::launch_status(op);
     }
-    static bool attr_set = false;
-    if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_nt),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLds));
-        if (e != hipSuccess) {
-            return mh::hip_error(e, op);
-        }
-        attr_set = true;
+    // set on every tiled launch (a cheap host call): no shared flag for
+    // concurrent callers to race on, and right on every device
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_nt),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLds));
+    if (e != hipSuccess) {
+        return mh::hip_error(e, op);
     }
     NtArgs p{};
     p.a = a;

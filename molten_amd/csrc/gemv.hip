@@ -69,11 +69,20 @@ __device__ __forceinline__ void amax_if_greater(unsigned long long* p, unsigned 
 // tag derived from the launch count (the scratch word after the slots, read
 // at kernel start and bumped by the collector at its end).  The collector
 // accepts only slots that carry this launch's tag, so a key that a unit of an
-// earlier launch wrote late (after that launch's collector gave up waiting)
-// is never taken for a later launch's, and a zero slot (tag 0) is never a
-// key.
+// earlier launch wrote before that launch's collector gave up is never taken
+// for a later launch's, and a zero slot (tag 0) is never a key.
+//
+// A unit that reads the count only after the collector gave up and bumped it
+// (it started that late) publishes under the next launch's tag, which no tag
+// can tell apart.  So a collector whose wait expired also sets kPoison in the
+// count word: the next launch's collector then treats its own result as lost
+// too (ids 0xffffffff, MH_STATUS_ARGMAX_WAIT), re-zeroes every slot and
+// clears the bit.  Stream order ends every unit of a launch before the next
+// launch starts, so a launch after that one is clean again.
+constexpr unsigned long long kPoison = 1ull << 63;
+
 __device__ __forceinline__ unsigned long long launch_tag(unsigned long long launches) {
-    return (launches % 0xffffull + 1ull) << 48;
+    return ((launches & ~kPoison) % 0xffffull + 1ull) << 48;
 }
 
 __device__ __forceinline__ unsigned long long key48(unsigned long long key64) {
@@ -106,6 +115,8 @@ __device__ void collect_keys(const GemvArgs& a, uint32_t n_units, const unsigned
     static_assert(kPer <= 32, "pending mask is 32 bits");
     const int lane = threadIdx.x & (mh::kWave - 1), wave = threadIdx.x / mh::kWave;
     const unsigned long long tag = launch_tag(launches);
+    const bool poisoned = (launches & kPoison) != 0ull;
+    bool expired = false;  // uniform: some row's wait expired in this launch
     for (int b = 0; b < B; ++b) {
         unsigned long long* sl = a.slots + static_cast<size_t>(b) * kArgSlots + threadIdx.x;
         unsigned long long v[kPer];
@@ -143,7 +154,9 @@ __device__ void collect_keys(const GemvArgs& a, uint32_t n_units, const unsigned
             }
         }
         m = mh::wave_max_u64(m);
-        const bool any_lost = __syncthreads_or(lost) != 0;
+        const bool row_expired = __syncthreads_or(lost) != 0;
+        expired = expired || row_expired;
+        const bool any_lost = row_expired || poisoned;
         if (any_lost && threadIdx.x == 0 && a.status != nullptr) {
             __hip_atomic_fetch_or(a.status, MH_STATUS_ARGMAX_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -162,7 +175,8 @@ __device__ void collect_keys(const GemvArgs& a, uint32_t n_units, const unsigned
         __syncthreads();
     }
     if (threadIdx.x == 0 && a.launches != nullptr) {
-        __hip_atomic_store(a.launches, launches + 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.launches, ((launches & ~kPoison) + 1ull) | (expired ? kPoison : 0ull), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 

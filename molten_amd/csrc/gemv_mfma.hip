@@ -201,6 +201,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
     __shared__ float m_lb[B][kWaves * 4], m_u1[B][kWaves * 4], m_du[B][kWaves * 4];
     __shared__ uint32_t m_r1[B][kWaves * 4];
     __shared__ unsigned long long own[B][kSlotWords];
+    __shared__ uint32_t fin_expired, fin_arrived;  // the finisher waves' expired waits, arrivals
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -404,7 +405,10 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
     const unsigned long long launches =
         (static_cast<unsigned long long>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(launches_v >> 32))) << 32) |
         __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(launches_v));
-    const uint32_t tag = static_cast<uint32_t>(launches % 255ull) + 1u;
+    // bit 63 of the count word: the previous launch's wait expired (see the
+    // finisher)
+    const bool poisoned = (launches >> 63) != 0ull;
+    const uint32_t tag = static_cast<uint32_t>((launches & ~(1ull << 63)) % 255ull) + 1u;
 #pragma unroll
     for (int u = 0; u < kDepth - 1; ++u) {
         issue(tile_c(u), stage_c(u), pbuf[u], svbuf[u], bvbuf[u]);
@@ -567,6 +571,10 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
     // always a candidate unless a dropped bound reaches the lower bound, so a
     // single candidate is the answer; several are recomputed in chunk order;
     // otherwise every row is.
+    if (threadIdx.x == 0) {
+        fin_expired = 0u;
+        fin_arrived = 0u;
+    }
     __syncthreads();
     if (wave >= B) {
         return;
@@ -615,7 +623,11 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
             }
         }
     }
-    const bool lost = __any(pend != 0u);
+    // an expired wait, or one in the previous launch: a workgroup that read
+    // the count only after that finisher bumped it published under this
+    // launch's tag, so this launch's words cannot be trusted either
+    const bool expired = __any(pend != 0u);
+    const bool lost = expired || poisoned;
     // lower bounds (kind 0) and dropped bounds (kind 1): maxima of the keys'
     // orderable high words
     uint32_t olb = lane == 0 ? static_cast<uint32_t>(own[b][0] >> 32) : 0u;
@@ -625,9 +637,25 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         olb = max(olb, static_cast<uint32_t>(v[j] >> 32));
         odu = max(odu, static_cast<uint32_t>(v[kPerKind + j] >> 32));
     }
-    if (b == 0u && lane == 0) {  // every workgroup has read the count by now (or the wait expired)
-        __hip_atomic_store(a.slots + static_cast<size_t>(B) * kArgSlots, launches + 1ull, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+    // every workgroup has read the count by now, unless a wait expired: then
+    // the count carries the poison bit for the next launch.  The finisher
+    // waves report to wave 0 through the LDS (they are resident together, so
+    // its wait ends); wave 0 alone writes the word.
+    if (lane == 0) {
+        if (expired) {
+            __hip_atomic_fetch_or(&fin_expired, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        __hip_atomic_fetch_add(&fin_arrived, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (b == 0u) {
+            while (__hip_atomic_load(&fin_arrived, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+                   static_cast<uint32_t>(B)) {
+                __builtin_amdgcn_s_sleep(1);
+            }
+            const bool any = __hip_atomic_load(&fin_expired, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u;
+            __hip_atomic_store(a.slots + static_cast<size_t>(B) * kArgSlots,
+                               ((launches & ~(1ull << 63)) + 1ull) | (any ? 1ull << 63 : 0ull), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
     const float lb = key_value(static_cast<unsigned long long>(mh::wave_max_u32(olb)) << 32);
     const float dmax = key_value(static_cast<unsigned long long>(mh::wave_max_u32(odu)) << 32);

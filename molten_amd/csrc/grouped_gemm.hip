@@ -13,8 +13,9 @@
 //     of one column that a lane feeds to the MFMA) and reuses every fragment
 //     for BM/32 row blocks;
 //   * the A tile (with the ids_sorted row gather fused into the load) is
-//     staged once per workgroup in double-buffered LDS, 64 k at a time, row
-//     pitch 72 bf16 (conflict-free 16-byte reads);
+//     staged once per workgroup in a 3-stage LDS ring filled by
+//     direct-to-LDS loads, 64 k at a time, XOR-swizzled rows (conflict-free
+//     16-byte reads);
 //   * k is permuted identically for A and B inside each 64-k block: lane
 //     half h and MFMA step j use k = 32h + 8j + t, so a lane's codes for a
 //     block are one 16-byte load.

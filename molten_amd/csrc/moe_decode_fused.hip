@@ -31,6 +31,8 @@
 //
 // Replaces the decode sequence of src/lfm.rs:967-1011 (router_addnorm_route,
 // gemv_gather_act, gemv_gather_down_combine4).
+#include <atomic>
+
 #include "mh_device.hpp"
 #include "mh_host.hpp"
 #include "mh_route.hpp"
@@ -71,6 +73,7 @@ struct FusedArgs {
     uint16_t* act;         // [topk, NI]
     uint16_t* out;         // [K]
     uint32_t* scratch;     // launch counts, tagged logits, tagged activation triples
+    uint32_t* status;      // device status word (MH_STATUS_*), or null
     uint64_t* stamps;      // per wave kStamps words of phase timestamps (STAMPS kernels only)
     uint32_t E, K, NI, gs;
 };
@@ -473,6 +476,11 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
         __syncthreads();
         stamp<STAMPS>(a, gw, lane, ST_EXCHANGED);
         ok = ok && bad_l == 0u;
+        // an expired wait (logits or activations): NaN outputs, and the
+        // status bit the host reads (one store per workgroup)
+        if (!ok && threadIdx.x == 0 && a.status != nullptr) {
+            __hip_atomic_fetch_or(a.status, MH_STATUS_DECODE_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         if (has_out) {
             float h[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -502,6 +510,38 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_fused(FusedArgs a) {
         }
         stamp<STAMPS>(a, gw, lane, ST_OUT);
     }
+}
+
+// Whether one workgroup of this instantiation fits a CU on the current
+// device (its registers and LDS), asked once per device: with fewer than one
+// resident workgroup per CU the kGrid workgroups would not all run at once
+// and the exchange waits could only expire.
+constexpr int kOccDevices = 64;
+template <typename WT, int TK, int EB, bool ST>
+bool fits_one_per_cu() {
+    static std::atomic<int> fits[kOccDevices];  // 0 unknown, 1 yes, 2 no
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kOccDevices) {
+        return false;
+    }
+    int f = fits[dev].load(std::memory_order_relaxed);
+    if (f == 0) {
+        int blocks = 0;
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &blocks, reinterpret_cast<const void*>(k_moe_decode_fused<WT, TK, EB, ST>), kThreads, 0);
+        f = e == hipSuccess && blocks >= 1 ? 1 : 2;
+        fits[dev].store(f, std::memory_order_relaxed);
+    }
+    return f == 1;
+}
+
+template <typename WT, int TK, int EB, bool ST>
+int launch_fused(const FusedArgs& a, hipStream_t stream) {
+    if (!fits_one_per_cu<WT, TK, EB, ST>()) {
+        return MH_ERR_UNSUPPORTED;
+    }
+    hipLaunchKernelGGL((k_moe_decode_fused<WT, TK, EB, ST>), dim3(kGrid), dim3(kThreads), 0, stream, a);
+    return mh::launch_status("k_moe_decode_fused");
 }
 
 }  // namespace
@@ -535,13 +575,14 @@ int moe_decode_fused(const void* router, int router_dtype, const float* bias, in
     a.uc = up->codes; a.usc = up->scales; a.ubi = up->biases;
     a.dc = down->codes; a.dsc = down->scales; a.dbi = down->biases;
     a.logits = logits; a.ids = ids; a.weights = weights; a.act = act; a.out = out; a.scratch = scratch;
+    a.status = mh::status_word();
     a.stamps = stamps;
     a.E = n_experts; a.K = K; a.NI = NI; a.gs = gate->group_size;
     const bool f32 = router_dtype == MH_DTYPE_F32;
     const bool eb1 = n_experts <= 64u;  // one expert per lane in the routing
-#define MH_FUSED_LAUNCH_ST(TK, EB, ST)                                                                            \
-    if (f32) hipLaunchKernelGGL((k_moe_decode_fused<float, TK, EB, ST>), dim3(kGrid), dim3(kThreads), 0, stream, a); \
-    else hipLaunchKernelGGL((k_moe_decode_fused<uint16_t, TK, EB, ST>), dim3(kGrid), dim3(kThreads), 0, stream, a);
+#define MH_FUSED_LAUNCH_ST(TK, EB, ST)                                    \
+    if (f32) return launch_fused<float, TK, EB, ST>(a, stream);             \
+    else return launch_fused<uint16_t, TK, EB, ST>(a, stream);
 #define MH_FUSED_LAUNCH_EB(TK, EB)          \
     if (stamps) { MH_FUSED_LAUNCH_ST(TK, EB, true) } \
     else { MH_FUSED_LAUNCH_ST(TK, EB, false) }
@@ -549,15 +590,14 @@ int moe_decode_fused(const void* router, int router_dtype, const float* bias, in
     if (eb1) { MH_FUSED_LAUNCH_EB(TK, 1) } \
     else { MH_FUSED_LAUNCH_EB(TK, 4) }
     switch (topk) {
-        case 1: MH_FUSED_LAUNCH(1) break;
-        case 2: MH_FUSED_LAUNCH(2) break;
-        case 3: MH_FUSED_LAUNCH(3) break;
-        default: MH_FUSED_LAUNCH(4) break;
+        case 1: MH_FUSED_LAUNCH(1)
+        case 2: MH_FUSED_LAUNCH(2)
+        case 3: MH_FUSED_LAUNCH(3)
+        default: MH_FUSED_LAUNCH(4)
     }
 #undef MH_FUSED_LAUNCH_ST
 #undef MH_FUSED_LAUNCH_EB
 #undef MH_FUSED_LAUNCH
-    return mh::launch_status("k_moe_decode_fused");
 }
 
 }  // namespace mh

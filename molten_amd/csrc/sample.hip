@@ -166,9 +166,15 @@ __device__ __forceinline__ float smp_kfloat(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// exp(w - m) in 2^-40 fixed point, truncated (w <= m: at most 2^40).
+// exp(w - m) in 2^-40 fixed point, truncated (w <= m: at most 2^40).  w - m
+// is NaN when both are the same infinity (every logit -inf, or the maximum
+// +inf): the token then has the maximum's mass exp(0); a NaN w or m has none.
 __device__ __forceinline__ unsigned long long smp_mass(float w, float m) {
-    return static_cast<unsigned long long>(mh::expf_fixed(w - m) * 1099511627776.0f);
+    float d = w - m;
+    if (d != d) {
+        d = w == m ? 0.0f : -__builtin_inff();
+    }
+    return static_cast<unsigned long long>(mh::expf_fixed(d) * 1099511627776.0f);
 }
 
 // The least integer >= top_p * z (top_p in (0, 1), exact).

@@ -450,8 +450,15 @@ static inline float smp_kfloat(uint32_t k) {
     return v;
 }
 
+/* w - m is NaN when both are the same infinity (every logit -inf, or the
+ * maximum +inf): the token then has the maximum's mass exp(0); a NaN w or m
+ * has none.  So the masses stay in [0, 2^40] for every input. */
 uint64_t orc_mass_fixed(float w, float m) {
-    return (uint64_t)(orc_expf(w - m) * 1099511627776.0f);  /* 2^40, truncated */
+    float d = w - m;
+    if (d != d) {
+        d = w == m ? 0.0f : -INFINITY;
+    }
+    return (uint64_t)(orc_expf(d) * 1099511627776.0f);  /* 2^40, truncated */
 }
 
 /* The least integer T >= top_p * z (top_p in (0, 1), exact). */

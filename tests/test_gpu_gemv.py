@@ -60,6 +60,8 @@ def assert_logits(got, want, n, k, batch, gs=64):
     (1536, 2048, 1),   # expert gate/up shape
     (2048, 1536, 1),   # expert down shape (48 live lanes)
     (300, 2048, 1),    # ragged last row group
+    (1030, 2048, 1),   # two-wave workgroups (one to four 4-row blocks per CU), a partial last block
+    (2050, 1536, 1),   # the same below K = 2048 (48 live lanes), partial last block
     (96, 11776, 1),    # dense down width: split-K path
     (2048, 11776, 1),  # the dense FFN down projection
     (37, 4160, 1),     # split-K: ragged rows, 130 chunks (a partial slab)
@@ -222,6 +224,51 @@ def test_argmax_ignores_keys_of_earlier_launches(dev, orc):
         hip.gemv_quant_argmax(w, xd, None, scratch, ids, 1)
         assert int(from_dev(ids, np.uint32)[0]) == want
         assert_scratch(scratch, n, k, 1, launch + 1)
+    assert hip.device_status(clear=True) == 0
+
+
+@pytest.mark.parametrize("bits,batch", [(4, 1), (6, 1), (4, 8)])
+def test_argmax_after_expired_wait_is_reported(dev, orc, bits, batch):
+    """The state an expired collector wait leaves (planted from the host): a
+    slot word carrying the *current* launch's tag with the largest key (what
+    a workgroup that started only after that collector gave up publishes)
+    and bit 63 of the count word.  Such a word cannot be told from a fresh
+    one, so the launch reports its result lost: ids 0xffffffff and
+    MH_STATUS_ARGMAX_WAIT; it leaves the slots zero and the count advanced
+    with the bit cleared, and the next launch is exact again."""
+    _log(f"argmax after expired wait bits={bits} batch={batch}")
+    rng = np.random.default_rng(4545 + bits + batch)
+    n, k = 65536 if batch > 1 else 8192, 2048
+    h = layout.synth_quant(rng, n, k, bits)
+    x = layout.synth_bf16(rng, (batch, k))
+    want = [orc.argmax_bf16(row) for row in orc.gemv_quant(h, x, batch)]
+    w, keep = dev_quant(h)
+    xd = to_dev(x)
+    scratch = zeros_dev((hip.argmax_scratch_words(batch),), np.uint64)
+    ids = empty_dev((batch,), np.uint32)
+    hip.device_status(clear=True)
+    hip.gemv_quant_argmax(w, xd, None, scratch, ids, batch)
+    assert from_dev(ids, np.uint32).tolist() == want
+    sc = from_dev(scratch, np.uint64).copy()
+    assert int(sc[-1]) == 1
+    if batch == 1:
+        # chunk-order finisher: tag of count 1, the largest 48-bit key, slot 5
+        sc[5] = np.uint64((((1 % 0xFFFF) + 1) << 48) | 0xFFFFFFFFFFFF)
+    else:
+        # matrix-core finisher: workgroup 7's lower bound, the greatest finite
+        # value under count 1's tag, in every batch row
+        for r in range(batch):
+            sc[r * hip.ARGMAX_SLOTS + 7] = ((np.uint64(0xFF7F0000) << np.uint64(32)) |
+                                            (np.uint64(1 % 255 + 1) << np.uint64(24)) | np.uint64(0xFFFFFF))
+    sc[-1] = np.uint64(1) | np.uint64(1 << 63)
+    scratch.copy_(to_dev(sc))
+    hip.gemv_quant_argmax(w, xd, None, scratch, ids, batch)
+    assert from_dev(ids, np.uint32).tolist() == [0xFFFFFFFF] * batch
+    assert hip.device_status(clear=True) & hip.STATUS_ARGMAX_WAIT
+    assert_scratch(scratch, n, k, batch, 2)
+    hip.gemv_quant_argmax(w, xd, None, scratch, ids, batch)
+    assert from_dev(ids, np.uint32).tolist() == want
+    assert_scratch(scratch, n, k, batch, 3)
     assert hip.device_status(clear=True) == 0
 
 
@@ -388,3 +435,48 @@ def test_mfma_argmax_near_ties(dev, orc, bits):
         h.biases[dst] = h.biases[top]
         h.codes[dst, (7 * j + 1) % words] ^= np.uint32(1 << (3 * j))
     _argmax_case(dev, orc, h, x, batch)
+
+
+@pytest.mark.parametrize("tie", [False, True])
+def test_model_head_128000_rows(dev, orc, tie):
+    """The reference model's own LM head: Q6 128000 x 2048 at batch 1
+    (vocab 128000, src/lfm.rs:22-42, through gemv_head_argmax,
+    src/kernels/lfm.rs:826-844), past the 65536 rows of the BASELINE configs.
+    Both entry points: mh_gemv_quant_argmax (logits bit-exact, id) and the
+    reference pair mh_gemv_head_argmax + mh_token_tail.  With `tie` the
+    winning row is copied to rows 65535 and 65536 and to row 127999 (the
+    rows on both sides of the 65536-row boundary and the last row), and the
+    original winner is made smaller: the lowest copy, 65535, must win."""
+    _log(f"model head 128000x2048 q6 tie={tie}")
+    rng = np.random.default_rng(128000 + tie)
+    n, k = 128000, 2048
+    h = layout.synth_quant(rng, n, k, 6)
+    x = layout.synth_bf16(rng, (1, k))
+    if tie:
+        top = orc.argmax_bf16(orc.gemv_quant(h, x, 1)[0])
+        for dst in (65535, 65536, 127999):
+            h.codes[dst] = h.codes[top]
+            h.scales[dst] = h.scales[top]
+            h.biases[dst] = h.biases[top]
+        if top not in (65535, 65536, 127999):
+            h.codes[top] = 0
+    logits = orc.gemv_quant(h, x, 1)
+    want = orc.argmax_bf16(logits[0])
+    if tie:
+        assert want == 65535
+    w, keep = dev_quant(h)
+    xd = to_dev(x)
+    y = empty_dev((1, n), np.uint16)
+    scratch = zeros_dev((hip.argmax_scratch_words(1),), np.uint64)
+    ids = empty_dev((1,), np.uint32)
+    for call in range(2):
+        hip.gemv_quant_argmax(w, xd, y, scratch, ids, 1)
+        assert int(from_dev(ids, np.uint32)[0]) == want
+        assert_scratch(scratch, n, k, 1, call + 1)
+    assert_logits(from_dev(y, np.uint16), logits, n, k, 1)
+    best = zeros_dev((1,), np.uint64)
+    tok = empty_dev((1,), np.uint32)
+    hip.gemv_head_argmax(w, xd, best, 1)
+    hip.token_tail(best, tok, 1)
+    assert int(from_dev(tok, np.uint32)[0]) == want
+    assert int(from_dev(best, np.uint64)[0]) == 0

@@ -274,3 +274,41 @@ def test_route_special_values_match_serial_scan(dev, orc, e):
         want_ids, want_w = orc.route(logits, bias, topk, mode)
         np.testing.assert_array_equal(from_dev(ids, np.uint32), want_ids)
         np.testing.assert_array_equal(from_dev(w, np.uint16), want_w)
+
+
+def test_moe_decode_expired_wait_is_reported(dev, orc):
+    """The single-launch decode step's bounded waits give up when one
+    workgroup's launch count (planted from the host) is ahead of the others':
+    its logits and activations carry an epoch no other workgroup waits for,
+    so every wait runs to its bound and the kernel still ends normally.  The
+    output is NaN and MH_STATUS_DECODE_WAIT is set; after the caller re-zeroes
+    the scratch the next step is bit-exact again."""
+    e, h, i, topk = 8, 512, 256, 2
+    _log(f"moe decode expired wait e={e} h={h} i={i} topk={topk}")
+    rng = np.random.default_rng(808)
+    gate, up, down = moe_weights(rng, e, h, i)
+    dg, kg = dev_quant(gate)
+    du, ku = dev_quant(up)
+    dd, kd = dev_quant(down)
+    router = router_weights(rng, e, h, False)
+    rd = to_dev(router)
+    x = layout.synth_bf16(rng, (1, h))[0]
+    out = empty_dev((h,), np.uint16)
+    logits = empty_dev((e,), np.float32)
+    ids = empty_dev((topk,), np.uint32)
+    wt = empty_dev((topk,), np.uint16)
+    act = empty_dev((topk, i), np.uint16)
+    words = np.zeros(hip.MOE_DECODE_SCRATCH_WORDS, np.uint32)
+    words[5] = 100  # workgroup 5's launch count
+    scratch = to_dev(words)
+    hip.device_status(clear=True)
+    hip.moe_decode(rd, None, dg, du, dd, e, topk, to_dev(x), out, logits, ids, wt, act, scratch, mode=1)
+    got = from_dev(out, np.uint16)
+    assert (got == 0x7FC0).all(), got[:8]
+    assert hip.device_status(clear=True) & hip.STATUS_DECODE_WAIT
+    scratch.zero_()
+    hip.moe_decode(rd, None, dg, du, dd, e, topk, to_dev(x), out, logits, ids, wt, act, scratch, mode=1)
+    want = orc.moe_decode(router, None, 1, gate, up, down, e, topk, h, i, x)
+    np.testing.assert_array_equal(from_dev(out, np.uint16), want["out"])
+    assert hip.device_status(clear=True) == 0
+    del kg, ku, kd

@@ -127,3 +127,25 @@ def test_sample_mark_sets_the_bit(dev):
     for t in (0, 31, 32, 127999):
         want[t >> 5] |= np.uint32(1 << (t & 31))
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("n,top_k,top_p", [(128000, 0, 0.9), (128000, 40, 0.5), (4096, 0, 1e-6)])
+def test_sample_draw_all_minus_inf(dev, orc, n, top_k, top_p):
+    """Every logit -inf with top-k / top-p on: the masses are defined (every
+    token the maximum's), the kept set is every token and the draw's key is
+    the oracle's, which is the temperature draw's (token 0)."""
+    logits = np.full(n, 0xFF80, np.uint16)
+    seen = np.zeros((n + 31) // 32, np.uint32)
+    ws_bytes = hip.sample_workspace_bytes(n)
+    ws = to_dev(np.zeros(ws_bytes, np.uint8))
+    dl, ds = to_dev(logits), to_dev(seen)
+    for call in range(2):
+        p = hip.sample_params(1.0, 17, call, 1.0, top_k, top_p)
+        want, _ = orc.sample_draw(logits, None, p.inv_temp, 1.0, False, top_k, p.top_p, 17, call)
+        assert want == orc.sample_gumbel(logits, None, p.inv_temp, 1.0, False, 17, call)
+        best = to_dev(np.zeros(1, np.uint64))
+        hip.sample_draw(dl, n, ds, p, best, ws, ws_bytes)
+        got = int(from_dev(best, np.uint64)[0])
+        assert got == want, (call, hex(got), hex(want))
+        assert (~got) & 0xFFFFFFFF == 0
+        assert not from_dev(ws, np.uint8)[:hip.SAMPLE_ZERO_BYTES].any()

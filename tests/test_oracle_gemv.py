@@ -101,14 +101,15 @@ def test_gemv_rows_subset(orc, rng):
     np.testing.assert_array_equal(orc.gemv_quant_rows(h, x, rows, 2), y[:, rows])
 
 
-@pytest.mark.parametrize("bits", [4, 6])
+@pytest.mark.parametrize("bits", [4, 6, 8])
 def test_dequant_is_one_rounding(orc, rng, bits):
     h = layout.synth_quant(rng, 16, 256, bits)
     deq = orc.dequant_bf16(h)
     q = layout.unpack_codes(h.codes, bits, 256).astype(np.float64)
+    assert q.max() > (1 << (bits - 1))  # the codes reach the upper half of the range
     s = np.repeat(bf(h.scales), 64, axis=1).astype(np.float64)
     b = np.repeat(bf(h.biases), 64, axis=1).astype(np.float64)
-    # s*q is exact in f64 (8-bit q, 8-bit s); + b then one rounding to f32 is
+    # s*q is exact in f64 (q < 256, 8-bit s); + b then one rounding to f32 is
     # the fma (f64 sum exact here), then RNE to bf16
     want = layout.f32_to_bf16((s * q + b).astype(np.float32))
     np.testing.assert_array_equal(deq, want)

@@ -221,3 +221,31 @@ def test_kept_draw_follows_renormalized_softmax(orc):
     assert counts[p == 0].sum() == 0
     chi2 = float(((counts[kept] - n * p[kept]) ** 2 / (n * p[kept])).sum())
     assert chi2 < 25.0, (chi2, counts / n, p)  # df 3
+
+
+def test_mass_of_infinite_and_nan_logits(orc):
+    """w - m is NaN when both are the same infinity: the token then has the
+    maximum's mass exp(0) = 2^40; a NaN w or m has none (so the top-p masses
+    stay in [0, 2^40] for every input)."""
+    inf = float("inf")
+    assert orc.mass_fixed(-inf, -inf) == 1 << 40
+    assert orc.mass_fixed(inf, inf) == 1 << 40
+    assert orc.mass_fixed(-inf, 0.0) == 0
+    assert orc.mass_fixed(1.0, inf) == 0
+    assert orc.mass_fixed(float("nan"), 0.0) == 0
+    assert orc.mass_fixed(0.0, float("nan")) == 0
+    assert orc.mass_fixed(0.0, 0.0) == 1 << 40
+
+
+@pytest.mark.parametrize("top_k,top_p", [(0, 0.9), (40, 0.5), (0, 1e-6)])
+def test_all_minus_inf_logits_draw_like_the_temperature_draw(orc, top_k, top_p):
+    """Every logit -inf: every token has the same key and mass, so top-k and
+    top-p keep them all and the kept-set draw is the temperature draw (token
+    0: every w + G is -inf and ties go to the lower id)."""
+    n = 4096
+    logits = np.full(n, 0xFF80, np.uint16)  # bf16 -inf
+    for pos in range(3):
+        key, tau = orc.sample_draw(logits, None, 1.0, 1.0, False, top_k, top_p, 5, pos)
+        assert key == orc.sample_gumbel(logits, None, 1.0, 1.0, False, 5, pos)
+        assert _token(key) == 0
+        assert tau == int(_fkey(np.float32(-np.inf)))
