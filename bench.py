@@ -268,7 +268,7 @@ def timeline_config3(torch, hip, dev, gen, launches):
     """Config 3's decode step run `launches` times on the single-launch path
     with per-wave phase timestamps (100 MHz clock), each launch separately
     synchronized.  Per phase: the 10th / 50th / 90th percentile and the
-    maximum over the 2048 waves of (stamp - the launch's earliest start), in
+    maximum over the launch's waves of (stamp - the launch's earliest start), in
     us, each the median over launches; and the share of workgroups whose XCD
     equals their index mod 8 (the round-robin dispatch the step assumes)."""
     import numpy as np
@@ -282,7 +282,7 @@ def timeline_config3(torch, hip, dev, gen, launches):
     wt = torch.empty(topk, dtype=torch.int16, device=dev)
     act = torch.empty((topk, I), dtype=torch.int16, device=dev)
     scratch = torch.zeros(hip.MOE_DECODE_SCRATCH_WORDS, dtype=torch.int32, device=dev)
-    nwaves = 256 * 8
+    nwaves = hip.MOE_DECODE_STAMP_WAVES
     stamps = torch.zeros(nwaves * hip.MOE_DECODE_STAMPS, dtype=torch.int64, device=dev)
     per = []
     xcc_ok = []
@@ -303,7 +303,7 @@ def timeline_config3(torch, hip, dev, gen, launches):
             rows.append([float(np.percentile(v, 10)), float(np.percentile(v, 50)), float(np.percentile(v, 90)),
                          float(v.max())] if v.size else [float("nan")] * 4)
         per.append(rows)
-        wg_xcc = st[::8, 9]
+        wg_xcc = st[::8, 9]  # 8 waves per workgroup
         xcc_ok.append(float(np.mean(wg_xcc == (np.arange(256) % 8))))
     med = np.median(np.array(per), axis=0)
     del sets

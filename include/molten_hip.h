@@ -363,13 +363,15 @@ int mh_moe_decode(const void* router, int router_dtype, const float* bias, int m
 
 
 /* Measurement only (no reference counterpart): mh_moe_decode on the
- * single-launch path with phase timestamps.  Lane 0 of each of the launch's
- * 2048 waves writes MH_MOE_DECODE_STAMPS u64 words into `stamps` (wave w at
- * w * MH_MOE_DECODE_STAMPS): the 100 MHz constant clock at wave start,
- * router row stored, experts chosen, first gate/up loads issued, first and
- * last activation triple published, down loads issued, activations all in,
- * output stored; word 9 the XCD the workgroup ran on.  Outputs are
- * mh_moe_decode's.  MH_ERR_UNSUPPORTED where the step runs as three launches. */
+ * single-launch path with phase timestamps.  `stamps` holds
+ * MH_MOE_DECODE_STAMP_WAVES x MH_MOE_DECODE_STAMPS u64 words; lane 0 of each
+ * of the launch's waves w writes its words at w * MH_MOE_DECODE_STAMPS: the
+ * 100 MHz constant clock at wave start, router row stored, experts chosen,
+ * first gate/up loads issued, first and last activation triple published,
+ * down loads issued, activations all in, output stored; word 9 the XCD the
+ * workgroup ran on.  Outputs are mh_moe_decode's.  MH_ERR_UNSUPPORTED where
+ * the step runs as three launches. */
+#define MH_MOE_DECODE_STAMP_WAVES 2048u
 #define MH_MOE_DECODE_STAMPS 10u
 int mh_moe_decode_stamped(const void* router, int router_dtype, const float* bias, int mode, float eps,
                           const mh_quant_weights* gate, const mh_quant_weights* up, const mh_quant_weights* down,

@@ -97,10 +97,20 @@ __device__ __forceinline__ void publish_key(const GemvArgs& a, uint32_t b, uint3
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// The launch count, read at kernel start by every workgroup of a finisher
-// launch (the collector only bumps it after every unit has published).
+// The launch count, read by every workgroup of a finisher launch before it
+// publishes (the collector only bumps it after every unit has published).
 __device__ __forceinline__ unsigned long long read_launches(const GemvArgs& a) {
     return a.launches != nullptr ? __hip_atomic_load(a.launches, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+}
+
+// The same where a.launches is never null (the batch-1 kernel's argmax
+// launches): no branch, so the load's wait falls where the value is used
+// instead of at a merge right after it.
+// The address goes through an opaque register so the value stays a vector
+// register: a uniform load is moved to scalar registers right after it, which
+// waits for every load issued before it.
+__device__ __forceinline__ unsigned long long read_launches_nn(const GemvArgs& a) {
+    return __hip_atomic_load(a.launches + mh::opaque(0u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Run by the whole collector workgroup.  own[b]: the collector's own key.
@@ -284,7 +294,6 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
     const uint32_t G = FAST ? 32u : a.groups;
     const bool live = FAST || lane < static_cast<int>(C);
     const uint32_t c = live ? lane : 0u;
-    const unsigned long long launches = ARGMAX ? read_launches(a) : 0ull;
     const uint32_t code_off = c * BITS * 4u;
     const uint32_t gc = FAST ? static_cast<uint32_t>(lane) / 2u : (32u * c) / a.gs;
     const uint32_t row_bytes = FAST ? 2048u * BITS / 8u : a.row_words * 4u;
@@ -324,6 +333,9 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
     // path without them meets the x conversion's wait
     const uint32_t blk0 = blockIdx.x * WV + wave;
     issue(min(blk0, n_blocks - 1u));
+    // the launch count behind the block's loads: needed only at the end
+    asm volatile("" ::: "memory");
+    const unsigned long long launches = ARGMAX ? read_launches_nn(a) : 0ull;
 
     // x: wave 0 converts, every wave reads after the barrier
     float xr[32];
@@ -763,8 +775,10 @@ int gemv_common(const char* op, const mh_quant_weights* w, const uint16_t* x, ui
     a.gs = w->group_size;
     a.row_words = w->in_features * w->bits / 32u;
     a.groups = w->in_features / w->group_size;
+    // the count word of a finisher launch; in the atomic-max mode (whose
+    // kernels read it but never use it) a readable word: the keys
     a.launches = finisher ? reinterpret_cast<unsigned long long*>(best) + static_cast<size_t>(batch) * kArgSlots
-                          : nullptr;
+                          : reinterpret_cast<unsigned long long*>(best);
     a.status = mh::status_word();
     const hipStream_t s = mh::as_stream(stream);
     // batch > 1 without the reference's atomic-max key: the matrix-core

@@ -448,8 +448,12 @@ __device__ __forceinline__ float q6_chunk_dot_s(const uint32_t (&w)[6], const fl
 // A lane's 32-element bf16 chunk of x: the raw words (16-byte loads when the
 // chunk is aligned), then as f32 plus the ascending sum.  Split so a kernel
 // can issue its weight loads before it waits for x.
+// The alignment is lane 0's: every caller offsets lanes by multiples of 64
+// bytes, so the test is uniform and compiles to a scalar branch (a per-lane
+// test made both paths masked blocks whose merge waited for the loads).
 __device__ __forceinline__ void load_x_words(const uint16_t* xp, uint32_t (&xw)[16]) {
-    if ((reinterpret_cast<uintptr_t>(xp) & 15u) == 0) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(xp)));
+    if ((lo & 15u) == 0) {
         const uint4* xv = reinterpret_cast<const uint4*>(xp);
         const uint4 v0 = xv[0], v1 = xv[1], v2 = xv[2], v3 = xv[3];
         const uint4 v[4] = {v0, v1, v2, v3};
@@ -462,6 +466,18 @@ __device__ __forceinline__ void load_x_words(const uint16_t* xp, uint32_t (&xw)[
         for (int q = 0; q < 16; ++q) {
             xw[q] = static_cast<uint32_t>(xp[2 * q]) | (static_cast<uint32_t>(xp[2 * q + 1]) << 16);
         }
+    }
+}
+
+// The same for a chunk known to be 16-byte aligned (the host checks x): no
+// branch, so no merge of two load paths' registers (whose copies wait for the
+// data) between the loads and their first use.
+__device__ __forceinline__ void load_x_words_a16(const uint16_t* xp, uint32_t (&xw)[16]) {
+    const uint4* xv = reinterpret_cast<const uint4*>(xp);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint4 v = xv[q];
+        xw[4 * q] = v.x; xw[4 * q + 1] = v.y; xw[4 * q + 2] = v.z; xw[4 * q + 3] = v.w;
     }
 }
 

@@ -54,6 +54,7 @@ constexpr uint32_t kMaxAct = 8192;  // bf16 activations staged per workgroup (16
 constexpr uint32_t kMaxTriples = ((kMaxAct + 2u) / 3u + 1u) / 2u * 2u;  // ceil(kMaxAct / 3), rounded up to even
 constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr int kReadsPerThread = (kMaxTriples / 2 + kThreads - 1) / kThreads;  // 16-byte reads
+static_assert(kGrid * kWaves <= MH_MOE_DECODE_STAMP_WAVES, "stamp buffer");
 static_assert(kMaxTriples % 2 == 0 && 3u * kMaxTriples >= kMaxAct && mh::kMaxExperts <= kGrid &&
                   kActWords + 2u * kMaxTriples <= MH_MOE_DECODE_SCRATCH_WORDS,
               "scratch layout");

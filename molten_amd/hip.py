@@ -526,13 +526,14 @@ def moe_decode(router, bias, gate: QuantWeights, up: QuantWeights, down: QuantWe
 
 
 MOE_DECODE_STAMPS = 10  # MH_MOE_DECODE_STAMPS
+MOE_DECODE_STAMP_WAVES = 2048  # MH_MOE_DECODE_STAMP_WAVES
 
 
 def moe_decode_stamped(router, bias, gate: QuantWeights, up: QuantWeights, down: QuantWeights,
                        n_experts: int, topk: int, x, out, logits, ids, weights, act, scratch, stamps,
                        mode: int = ROUTE_SIGMOID_BIAS, eps: float = 1e-6, stream=None) -> None:
     """moe_decode on the single-launch path with per-wave phase timestamps
-    (measurement only): stamps u64 [2048 * MOE_DECODE_STAMPS]."""
+    (measurement only): stamps u64 [MOE_DECODE_STAMP_WAVES * MOE_DECODE_STAMPS]."""
     check(load().mh_moe_decode_stamped(_ptr(router), _dtype_of(router), _ptr(bias), mode, eps,
                                        _qref(gate), _qref(up), _qref(down), n_experts, topk, _ptr(x),
                                        _ptr(out), _ptr(logits), _ptr(ids), _ptr(weights), _ptr(act),

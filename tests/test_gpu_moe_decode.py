@@ -312,3 +312,116 @@ def test_moe_decode_expired_wait_is_reported(dev, orc):
     np.testing.assert_array_equal(from_dev(out, np.uint16), want["out"])
     assert hip.device_status(clear=True) == 0
     del kg, ku, kd
+
+
+def _prefix_experts(h, n_exp, rows_per_expert):
+    """The first n_exp experts of stacked HostQuant h (a view of its rows)."""
+    n = n_exp * rows_per_expert
+    return layout.HostQuant(h.codes[:n], h.scales[:n], h.biases[:n], n, h.k, h.group_size, h.bits)
+
+
+@pytest.mark.parametrize("n_exp,mode", [(32, 1), (48, 0), (5, 1)])
+def test_moe_decode_config3_shape_fewer_experts(dev, orc, experts, n_exp, mode):
+    """d_model 2048, intermediate 1536, top-4 over fewer than 64 experts
+    (the single launch with router workgroups past E idle), both routing
+    modes, bit-exact over repeated steps."""
+    _log(f"moe decode config-3 shape with {n_exp} experts mode={mode}")
+    gate, up, down = (_prefix_experts(experts["h"][0], n_exp, I), _prefix_experts(experts["h"][1], n_exp, I),
+                      _prefix_experts(experts["h"][2], n_exp, H))
+    dg, kg = dev_quant(gate)
+    du, ku = dev_quant(up)
+    dd, kd = dev_quant(down)
+    rng = np.random.default_rng(900 + n_exp)
+    router = router_weights(rng, n_exp, H, False)
+    bias = rng.normal(0, 0.05, n_exp).astype(np.float32) if mode == 0 else None
+    rd = to_dev(router)
+    bd = None if bias is None else to_dev(bias)
+    out = empty_dev((H,), np.uint16)
+    logits = empty_dev((n_exp,), np.float32)
+    ids = empty_dev((TOPK,), np.uint32)
+    wt = empty_dev((TOPK,), np.uint16)
+    act = empty_dev((TOPK, I), np.uint16)
+    scratch = zeros_dev((hip.MOE_DECODE_SCRATCH_WORDS,), np.uint32)
+    for trial in range(3):
+        x = layout.synth_bf16(rng, (1, H))[0]
+        hip.moe_decode(rd, bd, dg, du, dd, n_exp, TOPK, to_dev(x), out, logits, ids, wt, act, scratch, mode=mode)
+        want = orc.moe_decode(router, bias, mode, gate, up, down, n_exp, TOPK, H, I, x)
+        assert from_dev(ids, np.uint32).tolist() == want["ids"].tolist()
+        np.testing.assert_array_equal(from_dev(logits, np.float32), want["logits"])
+        np.testing.assert_array_equal(from_dev(wt, np.uint16), want["w"])
+        np.testing.assert_array_equal(from_dev(act, np.uint16), want["act"])
+        np.testing.assert_array_equal(from_dev(out, np.uint16), want["out"])
+        _check_scratch(from_dev(scratch, np.uint32), trial + 1)
+    del kg, ku, kd
+
+
+def test_moe_decode_alternating_shapes_share_scratch(dev, orc, experts):
+    """Single-launch steps at config 3's shape and at a small shape alternate
+    on one scratch buffer: the launch counts stay in lockstep and every step
+    is bit-exact."""
+    _log("moe decode alternating shapes on one scratch")
+    gate, up, down = experts["h"]
+    dg, du, dd = experts["d"]
+    rng = np.random.default_rng(4242)
+    router = router_weights(rng, E, H, False)
+    rd = to_dev(router)
+    e2, h2, i2, k2 = 8, 512, 256, 2
+    g2, u2, d2 = moe_weights(rng, e2, h2, i2)
+    dg2, kg = dev_quant(g2)
+    du2, ku = dev_quant(u2)
+    dd2, kd = dev_quant(d2)
+    router2 = router_weights(rng, e2, h2, False)
+    rd2 = to_dev(router2)
+    scratch = zeros_dev((hip.MOE_DECODE_SCRATCH_WORDS,), np.uint32)
+    for trial in range(4):
+        if trial % 2 == 0:
+            x = layout.synth_bf16(rng, (1, H))[0]
+            out, logits = empty_dev((H,), np.uint16), empty_dev((E,), np.float32)
+            ids, wt, act = empty_dev((TOPK,), np.uint32), empty_dev((TOPK,), np.uint16), empty_dev((TOPK, I), np.uint16)
+            hip.moe_decode(rd, None, dg, du, dd, E, TOPK, to_dev(x), out, logits, ids, wt, act, scratch, mode=1)
+            want = orc.moe_decode(router, None, 1, gate, up, down, E, TOPK, H, I, x)
+        else:
+            x = layout.synth_bf16(rng, (1, h2))[0]
+            out, logits = empty_dev((h2,), np.uint16), empty_dev((e2,), np.float32)
+            ids, wt, act = empty_dev((k2,), np.uint32), empty_dev((k2,), np.uint16), empty_dev((k2, i2), np.uint16)
+            hip.moe_decode(rd2, None, dg2, du2, dd2, e2, k2, to_dev(x), out, logits, ids, wt, act, scratch, mode=1)
+            want = orc.moe_decode(router2, None, 1, g2, u2, d2, e2, k2, h2, i2, x)
+        assert from_dev(ids, np.uint32).tolist() == want["ids"].tolist()
+        np.testing.assert_array_equal(from_dev(act, np.uint16).reshape(want["act"].shape), want["act"])
+        np.testing.assert_array_equal(from_dev(out, np.uint16), want["out"])
+        _check_scratch(from_dev(scratch, np.uint32), trial + 1)
+    del kg, ku, kd
+
+
+def test_moe_decode_config3_expired_wait_is_reported(dev, orc, experts):
+    """The single-launch decode step at config 3's shape with workgroup 5's
+    launch count planted ahead from the host: its router row and
+    activations carry an epoch no other workgroup waits for, so the bounded
+    waits give up and the kernel ends normally.  Every output is NaN and
+    MH_STATUS_DECODE_WAIT is set; after the caller re-zeroes the scratch the
+    next step is bit-exact again."""
+    _log("moe decode config-3 shape, planted launch count")
+    gate, up, down = experts["h"]
+    dg, du, dd = experts["d"]
+    rng = np.random.default_rng(809)
+    router = router_weights(rng, E, H, False)
+    rd = to_dev(router)
+    x = layout.synth_bf16(rng, (1, H))[0]
+    out = empty_dev((H,), np.uint16)
+    logits = empty_dev((E,), np.float32)
+    ids = empty_dev((TOPK,), np.uint32)
+    wt = empty_dev((TOPK,), np.uint16)
+    act = empty_dev((TOPK, I), np.uint16)
+    words = np.zeros(hip.MOE_DECODE_SCRATCH_WORDS, np.uint32)
+    words[5] = 100
+    scratch = to_dev(words)
+    hip.device_status(clear=True)
+    hip.moe_decode(rd, None, dg, du, dd, E, TOPK, to_dev(x), out, logits, ids, wt, act, scratch, mode=1)
+    got = from_dev(out, np.uint16)
+    assert (got == 0x7FC0).all(), got[:8]
+    assert hip.device_status(clear=True) & hip.STATUS_DECODE_WAIT
+    scratch.zero_()
+    hip.moe_decode(rd, None, dg, du, dd, E, TOPK, to_dev(x), out, logits, ids, wt, act, scratch, mode=1)
+    want = orc.moe_decode(router, None, 1, gate, up, down, E, TOPK, H, I, x)
+    np.testing.assert_array_equal(from_dev(out, np.uint16), want["out"])
+    assert hip.device_status(clear=True) == 0
