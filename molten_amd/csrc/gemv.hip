@@ -333,9 +333,12 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
     // path without them meets the x conversion's wait
     const uint32_t blk0 = blockIdx.x * WV + wave;
     issue(min(blk0, n_blocks - 1u));
-    // the launch count behind the block's loads: needed only at the end
+    // the launch count behind the block's loads, needed only at the end and
+    // only by wave 0 (the publisher; it hands the count to the collector's
+    // other waves through the LDS): one device-coherent read of the word per
+    // workgroup, not per wave
     asm volatile("" ::: "memory");
-    const unsigned long long launches = ARGMAX ? read_launches_nn(a) : 0ull;
+    unsigned long long launches = ARGMAX && wave == 0 ? read_launches_nn(a) : 0ull;
 
     // x: wave 0 converts, every wave reads after the barrier
     float xr[32];
@@ -437,7 +440,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
     // atomic per workgroup)
     const unsigned long long key = wave_argmax_key(lbv, lbi);
     __shared__ unsigned long long wk[kWaves];
-    __shared__ unsigned long long own[1];
+    __shared__ unsigned long long own[2];  // the collector's own key, the launch count
     if (lane == 0) {
         wk[wave] = key;
     }
@@ -452,6 +455,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
                 publish_key(a, 0, blockIdx.x, launch_tag(launches), t);
             } else {
                 own[0] = t;
+                own[1] = launches;
             }
         }
     }
@@ -459,6 +463,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
         return;
     }
     __syncthreads();
+    launches = own[1];
     collect_keys<1>(a, last, own, launches);
 }
 

@@ -10,7 +10,9 @@ import sys
 import tempfile
 import time
 
-import numpy as np
+sys.modules["torch"] = None  # no torch in this process: its HIP runtime stays out
+
+import numpy as np  # noqa: E402
 
 ROOT = pathlib.Path(__file__).resolve().parent.parent
 sys.path.insert(0, str(ROOT))
@@ -39,6 +41,7 @@ def d2h(lib, src, shape, dtype):
 
 def main(bits: int) -> None:
     lib = hip.load()
+    assert all("torch" not in p for p in hip.hip_runtimes()), hip.hip_runtimes()
     rng = np.random.default_rng(bits)
     n, k = 24576, 2048  # Q6 codes 37.7 MB: three 16 MB staging chunks
     h = layout.synth_quant(rng, n, k, bits)
