@@ -304,7 +304,8 @@ def timeline_config3(torch, hip, dev, gen, launches):
                          float(v.max())] if v.size else [float("nan")] * 4)
         per.append(rows)
         wg_xcc = st[::8, 9]  # 8 waves per workgroup
-        xcc_ok.append(float(np.mean(wg_xcc == (np.arange(256) % 8))))
+        # on the XCD of workgroup (index % 8): round-robin dispatch
+        xcc_ok.append(float(np.mean(wg_xcc == wg_xcc[np.arange(256) % 8])))
     med = np.median(np.array(per), axis=0)
     del sets
     return {"phases_us_p10_p50_p90_max": {name: [round(x, 2) for x in med[i]]
@@ -392,6 +393,60 @@ def measure_ceilings(torch, dev, steps, warmup):
     out["bf16_mfma_32x32x16"] = dict(value=round(tf, 1), unit="TFLOP/s", us=round(ms * 1e3, 1),
                                      frac_of_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4),
                                      launch=f"{wg} x 4 waves, 8 independent accumulators per wave")
+    # store-to-visible latency of an 8-byte word between workgroups (the
+    # fused decode step's exchanges): p50 / p90 over the consumers of 20
+    # launches per mode, in ns
+    import numpy as np
+
+    lib.mhc_exchange.argtypes = [vp, vp, u32, ctypes.c_uint64, ctypes.c_int, u32, u32, vp]
+    words = torch.zeros(64, dtype=torch.int64, device=dev)
+    xo = torch.zeros(256 * 4, dtype=torch.int64, device=dev)
+    lat = {"same_xcd_plain_store": [], "same_xcd_coherent_store": [], "cross_xcd_coherent_store": []}
+    rr = []
+    value = 1
+    for mode in (0, 1):
+        for _ in range(20):
+            value += 1
+            xo.zero_()
+            assert lib.mhc_exchange(words.data_ptr(), xo.data_ptr(), 256, value, mode, 300, 1 << 16, stream()) == 0
+            torch.cuda.synchronize()
+            o = xo.cpu().numpy().reshape(256, 4)
+            # same XCD as workgroup (index % 8): round-robin dispatch (the
+            # XCD numbering itself need not equal index % 8)
+            rr.append(float(np.mean(o[:, 0] == o[np.arange(256) % 8, 0])))
+            for b in range(8, 256):
+                for col, producer, key in ((1, b % 8, "same_xcd_plain_store" if mode == 0 else "same_xcd_coherent_store"),
+                                           (2, (b + 1) % 8, "cross_xcd_coherent_store")):
+                    if col == 2 and mode == 0:
+                        continue
+                    if o[b, col] != 0:
+                        lat[key].append((int(o[b, col]) - int(o[producer, 3])) * 10.0)
+    for key, v in lat.items():
+        v = np.array(v)
+        out[f"exchange_{key}"] = dict(p50_ns=round(float(np.percentile(v, 50)), 0) if v.size else None,
+                                      p90_ns=round(float(np.percentile(v, 90)), 0) if v.size else None,
+                                      seen=int(v.size), of=20 * 248)
+    out["exchange_xcd_round_robin_share"] = round(float(np.mean(rr)), 4)
+    del words, xo
+    # the vendor library's bf16 GEMM (torch.bmm / torch.mm: hipBLASLt) on
+    # config 4's per-expert shapes and on one dense shape, bf16 operands
+    # already in memory (no dequantization, no row gather): what a plain
+    # bf16 GEMM reaches at these sizes
+    for key, e, m, kk, n in (("vendor_bf16_bmm_64x256x2048x3072", 64, 256, 2048, 3072),
+                             ("vendor_bf16_bmm_64x256x1536x2048", 64, 256, 1536, 2048),
+                             ("vendor_bf16_mm_4096x2048x11776", 1, 4096, 2048, 11776)):
+        a = torch.randn(e, m, kk, device=dev, dtype=torch.bfloat16)
+        b = torch.randn(e, kk, n, device=dev, dtype=torch.bfloat16)  # contiguous right operand
+        c = torch.empty(e, m, n, device=dev, dtype=torch.bfloat16)
+        if e == 1:
+            a2, b2, c2 = a[0], b[0], c[0]
+            ms = timed(torch, lambda i: torch.mm(a2, b2, out=c2), max(4, steps // 10), 2)
+        else:
+            ms = timed(torch, lambda i: torch.bmm(a, b, out=c), max(4, steps // 10), 2)
+        tf = 2.0 * e * m * n * kk / (ms * 1e-3) / 1e12
+        out[key] = dict(value=round(tf, 1), unit="TFLOP/s", us=round(ms * 1e3, 1),
+                        frac_of_bf16_peak=round(tf / BF16_PEAK_TFLOPS, 4))
+        del a, b, c
     return out
 
 
@@ -644,7 +699,7 @@ def main() -> int:
             grouped_gemm_only_ms=round(ms4g, 4),
             frac_of_bf16_peak=round(FLOPS_CONFIG4 / (ms4g * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
 
-    log("ceilings: streaming read, bf16 matrix cores")
+    log("ceilings: streaming read, bf16 matrix cores, exchange latency, the vendor bf16 GEMM")
     ceilings = measure_ceilings(torch, dev, min(steps, 100), min(warmup, 5))
 
     cpu = None

@@ -31,6 +31,20 @@ int mhc_copy(const void* src, void* dst, size_t bytes, uint32_t grid, void* stre
  * in a practically impossible case. */
 int mhc_mfma(float* out, uint32_t workgroups, uint32_t iters, void* stream);
 
+/* Store-to-visible latency between workgroups (the cost of one exchange of
+ * the fused decode step's kind): `workgroups` (> 8) workgroups of 64
+ * threads; workgroups 0..7 (one per XCD) store `value` into words[8 p]
+ * (`words`: 64 u64, 8-byte aligned) `delay` ticks of the 100 MHz clock
+ * after they start -- mode 0 with a plain store (it stays in the XCD's L2),
+ * mode 1 device-coherent -- and every other workgroup w polls words[8 (w %
+ * 8)] (its XCD's producer) and, in mode 1, words[8 ((w + 1) % 8)] (another
+ * XCD's) with L2-coherent loads, at most `spins` times each.  out: 4 u64 per
+ * workgroup: the XCD it ran on, the clock at which each of the two words
+ * was seen (0: not within `spins` polls), and for producers the clock of
+ * the store.  Pass a value the words do not hold yet (a launch counter). */
+int mhc_exchange(uint64_t* words, uint64_t* out, uint32_t workgroups, uint64_t value, int mode, uint32_t delay,
+                 uint32_t spins, void* stream);
+
 /* The bf16 FLOPs of one mhc_mfma launch. */
 uint64_t mhc_mfma_flops(uint32_t workgroups, uint32_t iters);
 

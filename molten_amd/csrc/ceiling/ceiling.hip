@@ -96,6 +96,61 @@ int status() {
     return e == hipSuccess ? 0 : static_cast<int>(e);
 }
 
+// Store-to-visible latency of one 8-byte word between workgroups.
+// Workgroups 0..7 (one per XCD under the round-robin dispatch) are
+// producers: each waits `delay` ticks of the 100 MHz constant clock after it
+// starts, then stores `value` to its own word (a plain store, which stays in
+// its XCD's L2, for mode 0; a device-coherent store for mode 1) and records
+// the clock.  Every other workgroup polls, with L2-coherent loads, the word
+// of producer (its index % 8) -- the same XCD -- and in mode 1 also that of
+// producer (its index + 1) % 8 -- another XCD -- until it holds `value`,
+// and records the clock when it does (0 if `spins` polls pass first).
+// out[4 wg + 0]: the XCD the workgroup ran on; producers: out[4 wg + 3] the
+// store's clock; consumers: out[4 wg + 1], out[4 wg + 2] the two times seen.
+__device__ __forceinline__ uint64_t clock100() {
+    return wall_clock64();
+}
+
+__global__ __launch_bounds__(64) void k_exchange(uint64_t* words, uint64_t* out, uint64_t value, int mode,
+                                                 uint32_t delay, uint32_t spins) {
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    const uint64_t t0 = clock100();
+    const uint32_t b = blockIdx.x;
+    const int lane = threadIdx.x;
+    if (lane == 0) {
+        out[4u * b] = xcc & 0xfu;
+    }
+    if (b < 8u) {
+        while (clock100() < t0 + delay) {
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (lane == 0) {
+            const uint64_t ts = clock100();
+            if (mode == 0) {
+                __hip_atomic_store(words + 8u * b, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            } else {
+                __hip_atomic_store(words + 8u * b, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            out[4u * b + 3u] = ts;
+        }
+        return;
+    }
+    // lane 0: this XCD's producer; lane 1 (mode 1): the next XCD's
+    if (lane < (mode == 0 ? 1 : 2)) {
+        const uint32_t pw = (b + static_cast<uint32_t>(lane)) % 8u;
+        uint64_t seen = 0;
+        for (uint32_t i = 0; i < spins; ++i) {
+            const uint64_t v = __hip_atomic_load(words + 8u * pw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (v == value) {
+                seen = clock100();
+                break;
+            }
+        }
+        out[4u * b + 1u + static_cast<uint32_t>(lane)] = seen;
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -134,6 +189,17 @@ int mhc_mfma(float* out, uint32_t workgroups, uint32_t iters, void* stream) {
         return -1;
     }
     hipLaunchKernelGGL(k_mfma, dim3(workgroups), dim3(256), 0, static_cast<hipStream_t>(stream), out, iters);
+    return status();
+}
+
+int mhc_exchange(uint64_t* words, uint64_t* out, uint32_t workgroups, uint64_t value, int mode, uint32_t delay,
+                 uint32_t spins, void* stream) {
+    if (words == nullptr || out == nullptr || workgroups <= 8u || (mode != 0 && mode != 1) ||
+        reinterpret_cast<uintptr_t>(words) % 8 != 0 || spins == 0) {
+        return -1;
+    }
+    hipLaunchKernelGGL(k_exchange, dim3(workgroups), dim3(64), 0, static_cast<hipStream_t>(stream), words, out, value,
+                       mode, delay, spins);
     return status();
 }
 
