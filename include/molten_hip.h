@@ -191,6 +191,23 @@ int mh_gemv_head_argmax(const mh_quant_weights* w, const uint16_t* x, uint64_t* 
 int mh_gemv_quant_argmax(const mh_quant_weights* w, const uint16_t* x, uint16_t* y,
                          uint64_t* scratch, uint32_t* ids, uint32_t batch, mh_stream_t stream);
 
+/* Measurement only (no reference counterpart): mh_gemv_quant_argmax at batch
+ * 1 with phase timestamps, for the heads whose every wave computes one
+ * 8-row block (K 2048, group 64, N a multiple of 8 from 16 x 8 rows per CU
+ * up to 65536 rows: 32768..65536 on a 256-CU part; otherwise
+ * MH_ERR_UNSUPPORTED).  `stamps` holds
+ * MH_GEMV_STAMP_WAVES x MH_GEMV_STAMPS u64 words; lane 0 of each of the
+ * launch's waves w (workgroup w / 4) writes its words at w * MH_GEMV_STAMPS:
+ * the 100 MHz constant clock at wave start, block loads issued, x shared,
+ * row values stored, workgroup keys merged, workgroup key published (wave 0
+ * of every workgroup but the collector), slots collected and ids written
+ * (the collector's waves); word 7 the XCD the workgroup ran on.  Outputs are
+ * mh_gemv_quant_argmax's. */
+#define MH_GEMV_STAMP_WAVES 8192u
+#define MH_GEMV_STAMPS 8u
+int mh_gemv_quant_argmax_stamped(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint64_t* scratch,
+                                 uint32_t* ids, uint64_t* stamps, mh_stream_t stream);
+
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): mh_gemv_quant_argmax with its finisher scratch held by

@@ -39,8 +39,32 @@ struct GemvArgs {
     uint32_t* ids;              // [batch] tokens written by the finisher
     unsigned long long* launches;  // the finisher's launch count (after the slots), or null
     uint32_t* status;           // device status word (MH_STATUS_*), or null
+    uint64_t* stamps;           // per wave MH_GEMV_STAMPS phase words (stamped kernels only)
     uint32_t n, k, gs, row_words, groups;
 };
+
+// Phase timestamps of the batch-1 head (the 100 MHz constant clock), lane 0
+// of every wave, stamped instantiation only.
+enum GemvStamp {
+    GS_START = 0,      // the wave began
+    GS_ISSUED = 1,     // its block's loads (and wave 0's count read) issued
+    GS_X = 2,          // x converted and shared (after the workgroup barrier)
+    GS_ROWS = 3,       // the block's row values computed and stored
+    GS_KEYS = 4,       // the workgroup's wave keys in the LDS (after its barrier)
+    GS_PUBLISHED = 5,  // wave 0: the workgroup's key published (not the collector)
+    GS_COLLECTED = 6,  // collector workgroup: every slot read, the ids written
+    GS_XCC = 7         // the XCD the workgroup ran on
+};
+static_assert(GS_XCC + 1 == MH_GEMV_STAMPS, "stamp words");
+
+template <bool ST>
+__device__ __forceinline__ void gemv_stamp(const GemvArgs& a, uint32_t gw, int lane, int which) {
+    if constexpr (ST) {
+        if (lane == 0) {
+            a.stamps[static_cast<size_t>(gw) * MH_GEMV_STAMPS + which] = wall_clock64();
+        }
+    }
+}
 
 __device__ __forceinline__ unsigned long long amax(unsigned long long* p, unsigned long long v) {
     return __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -275,8 +299,8 @@ constexpr int kMaxGroups = 64;  // K / group size <= 2048 / 32
 // owns a chunk, 32 groups per row, no partial block).  ARGMAX: per-lane
 // bests, a DPP wave argmax, then the finisher (or the reference's atomic
 // max).  WV: waves per workgroup (2 only without the argmax, whose
-// publication and collector take 4).
-template <int BITS, bool FAST, bool ARGMAX, int NG, int WV = kWaves>
+// publication and collector take 4).  ST: phase timestamps (measurement).
+template <int BITS, bool FAST, bool ARGMAX, int NG, int WV = kWaves, bool ST = false>
 __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
     static_assert(NG == 1 || NG == 2, "one or two 4-row groups per block");
     static_assert(WV == kWaves || (WV == 2 && !ARGMAX), "two-wave workgroups only without the argmax");
@@ -299,6 +323,15 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
     const uint32_t row_bytes = FAST ? 2048u * BITS / 8u : a.row_words * 4u;
     const uint32_t n_blocks = (N + BR - 1) / BR;
     const uint32_t stride = gridDim.x * WV;
+    const uint32_t gw = blockIdx.x * WV + wave;
+    gemv_stamp<ST>(a, gw, lane, GS_START);
+    if constexpr (ST) {
+        if (lane == 0) {
+            uint32_t xcc;
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+            a.stamps[static_cast<size_t>(gw) * MH_GEMV_STAMPS + GS_XCC] = xcc & 0xfu;
+        }
+    }
 
     uint32_t xw[16];
     if (wave == 0) {
@@ -339,6 +372,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
     // workgroup, not per wave
     asm volatile("" ::: "memory");
     unsigned long long launches = ARGMAX && wave == 0 ? read_launches_nn(a) : 0ull;
+    gemv_stamp<ST>(a, gw, lane, GS_ISSUED);
 
     // x: wave 0 converts, every wave reads after the barrier
     float xr[32];
@@ -369,6 +403,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
         }
         xs = xsl[lane];
     }
+    gemv_stamp<ST>(a, gw, lane, GS_X);
 
     uint4* sb = sbl[wave];
     float* tw = tl[wave];
@@ -433,6 +468,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
         issue(blk);
         process(blk);
     }
+    gemv_stamp<ST>(a, gw, lane, GS_ROWS);
     if (!ARGMAX) {
         return;
     }
@@ -445,6 +481,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
         wk[wave] = key;
     }
     __syncthreads();
+    gemv_stamp<ST>(a, gw, lane, GS_KEYS);
     const uint32_t last = gridDim.x - 1;
     if (wave == 0) {
         const unsigned long long t = mh::wave_max_u64(lane < kWaves ? wk[lane < kWaves ? lane : 0] : 0ull);
@@ -458,6 +495,9 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
                 own[1] = launches;
             }
         }
+        if (blockIdx.x != last) {
+            gemv_stamp<ST>(a, gw, lane, GS_PUBLISHED);
+        }
     }
     if (a.slots == nullptr || blockIdx.x != last) {
         return;
@@ -465,6 +505,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
     __syncthreads();
     launches = own[1];
     collect_keys<1>(a, last, own, launches);
+    gemv_stamp<ST>(a, gw, lane, GS_COLLECTED);
 }
 
 // Row values (wave-uniform) of one row group of the staged kernel: store and
@@ -721,6 +762,21 @@ int launch_rows(const GemvArgs& a, hipStream_t stream) {
                 : launch(k_gemv_rows<BITS, false, ARGMAX, 2>, a, grid, 0, stream, "k_gemv_rows");
 }
 
+// The stamped head: batch 1 with the finisher, only where launch_rows takes
+// k_gemv_rows<BITS, true, true, 2> (K 2048, group 64, N a multiple of 8 and
+// at least the chip's SIMDs x 32 rows, at most one block per wave).
+template <int BITS>
+int launch_rows_stamped(const GemvArgs& a, hipStream_t stream) {
+    const uint32_t blocks8 = (a.n + kBlockRows - 1) / kBlockRows;
+    const bool small = blocks8 < static_cast<uint32_t>(mh::cu_count()) * 4u * kWaves;
+    const bool fast = a.k == 2048u && a.gs == 64u && a.n % kBlockRows == 0u;
+    if (small || !fast || blocks8 > kRowsGridCap * kWaves) {
+        return MH_ERR_UNSUPPORTED;
+    }
+    return launch(k_gemv_rows<BITS, true, true, 2, kWaves, true>, a, grid_for(blocks8, kRowsGridCap), 0, stream,
+                  "k_gemv_rows");
+}
+
 template <int BITS>
 int dispatch_gemv(const GemvArgs& a, uint32_t batch, hipStream_t stream) {
     switch (batch) {
@@ -750,7 +806,7 @@ constexpr size_t kMaxLds = 160u * 1024u;
 
 int gemv_common(const char* op, const mh_quant_weights* w, const uint16_t* x, uint16_t* y,
                 uint64_t* best, bool finisher, uint32_t* ids, uint32_t batch,
-                mh_stream_t stream) {
+                mh_stream_t stream, uint64_t* stamps = nullptr) {
     MH_TRY(mh::check_quant(w, op));
     MH_ENSURE(x != nullptr, MH_ERR_INVALID, "%s: x is NULL", op);
     MH_ENSURE(batch >= 1 && batch <= 8, MH_ERR_UNSUPPORTED, "%s: batch %u not in 1..8", op, batch);
@@ -786,6 +842,15 @@ int gemv_common(const char* op, const mh_quant_weights* w, const uint16_t* x, ui
                           : reinterpret_cast<unsigned long long*>(best);
     a.status = mh::status_word();
     const hipStream_t s = mh::as_stream(stream);
+    if (stamps != nullptr) {
+        a.stamps = stamps;
+        const int rc = w->bits == 4 ? launch_rows_stamped<4>(a, s) : w->bits == 6 ? launch_rows_stamped<6>(a, s)
+                                                                                  : MH_ERR_UNSUPPORTED;
+        MH_ENSURE(rc != MH_ERR_UNSUPPORTED || batch != 1, MH_ERR_UNSUPPORTED,
+                  "%s: %u x %u Q%u is not the batch-1 head's one-block-per-wave shape", op, w->out_features,
+                  w->in_features, w->bits);
+        return rc;
+    }
     // batch > 1 without the reference's atomic-max key: the matrix-core
     // kernel where its shape limits allow
     if (batch > 1 && (finisher || best == nullptr)) {
@@ -1013,6 +1078,15 @@ int mh_gemv_quant_argmax(const mh_quant_weights* w, const uint16_t* x, uint16_t*
     MH_ENSURE(scratch != nullptr && ids != nullptr, MH_ERR_INVALID,
               "mh_gemv_quant_argmax: scratch/ids is NULL");
     return gemv_common("mh_gemv_quant_argmax", w, x, y, scratch, true, ids, batch, stream);
+}
+
+int mh_gemv_quant_argmax_stamped(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint64_t* scratch,
+                                 uint32_t* ids, uint64_t* stamps, mh_stream_t stream) {
+    const char* op = "mh_gemv_quant_argmax_stamped";
+    MH_ENSURE(scratch != nullptr && ids != nullptr, MH_ERR_INVALID, "%s: scratch/ids is NULL", op);
+    MH_ENSURE(stamps != nullptr && mh::aligned(stamps, 8), MH_ERR_INVALID, "%s: stamps NULL or not 8-byte aligned",
+              op);
+    return gemv_common(op, w, x, y, scratch, true, ids, 1, stream, stamps);
 }
 
 int mh_token_tail(uint64_t* best, uint32_t* out_tok, uint32_t batch, mh_stream_t stream) {

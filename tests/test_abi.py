@@ -109,6 +109,10 @@ def test_argmax_arguments():
     assert ei.value.code == hip.MH_ERR_ALIGN
     with pytest.raises(hip.MoltenError):  # scratch without ids
         hip.gemv_quant_argmax(_qw(), 0x4000, 0x5000, 0x6000, None, stream=0)
+    with pytest.raises(hip.MoltenError):  # no stamp buffer
+        hip.gemv_quant_argmax_stamped(_qw(), 0x4000, 0x5000, 0x6000, 0x7000, None, stream=0)
+    with pytest.raises(hip.MoltenError):  # stamps not 8-byte aligned
+        hip.gemv_quant_argmax_stamped(_qw(), 0x4000, 0x5000, 0x6000, 0x7000, 0x8004, stream=0)
     with pytest.raises(hip.MoltenError):
         hip.token_tail(0x6000, 0x7000, batch=0, stream=0)
     with pytest.raises(hip.MoltenError):
@@ -254,3 +258,8 @@ def test_python_mirrors_of_header_constants():
 
     assert hip.SAMPLE_ZERO_BYTES == define("MH_SAMPLE_ZERO_BYTES")
     assert hip.ARGMAX_SLOTS == define("MH_ARGMAX_SLOTS")
+    assert hip.MOE_DECODE_SCRATCH_WORDS == define("MH_MOE_DECODE_SCRATCH_WORDS")
+    assert hip.MOE_DECODE_STAMP_WAVES == define("MH_MOE_DECODE_STAMP_WAVES")
+    assert hip.MOE_DECODE_STAMPS == define("MH_MOE_DECODE_STAMPS")
+    assert hip.GEMV_STAMP_WAVES == define("MH_GEMV_STAMP_WAVES")
+    assert hip.GEMV_STAMPS == define("MH_GEMV_STAMPS")

@@ -381,6 +381,43 @@ def test_lm_head_full_size(dev, orc, bits, batch):
     assert got_ids.tolist() == [orc.argmax_bf16(want[b]) for b in range(batch)]
 
 
+@pytest.mark.parametrize("bits", [4, 6])
+def test_stamped_head_matches_oracle(dev, orc, bits):
+    """The measurement instantiation of the batch-1 head (phase timestamps)
+    computes what the product kernel does: logits bit-exact, the oracle's id,
+    the scratch re-zeroed and counted; every wave of the launch stamps its
+    phases in order, wave 0 of every workgroup but the last publishes, and
+    only the last workgroup's waves stamp the collection."""
+    _log(f"stamped head bits={bits}")
+    rng = np.random.default_rng(4242 + bits)
+    n, k = 32768, 2048
+    h = layout.synth_quant(rng, n, k, bits)
+    x = layout.synth_bf16(rng, (1, k))
+    w, keep = dev_quant(h)
+    want = orc.gemv_quant(h, x, 1)
+    y = empty_dev((1, n), np.uint16)
+    scratch = zeros_dev((hip.argmax_scratch_words(1),), np.uint64)
+    ids = empty_dev((1,), np.uint32)
+    stamps = zeros_dev((hip.GEMV_STAMP_WAVES * hip.GEMV_STAMPS,), np.uint64)
+    for call in range(2):
+        hip.gemv_quant_argmax_stamped(w, to_dev(x), y, scratch, ids, stamps)
+        np.testing.assert_array_equal(from_dev(y, np.uint16), want)
+        assert from_dev(ids, np.uint32).tolist() == [orc.argmax_bf16(want[0])]
+        assert_scratch(scratch, n, k, 1, call + 1)
+    st = from_dev(stamps, np.uint64).reshape(hip.GEMV_STAMP_WAVES, hip.GEMV_STAMPS).astype(np.int64)
+    waves = n // 8  # one 8-row block per wave
+    assert not st[waves:].any()
+    st = st[:waves]
+    assert (st[:, :5] > 0).all()
+    assert (np.diff(st[:, :5], axis=1) >= 0).all()
+    wg = np.arange(waves) // 4
+    last = wg == wg.max()
+    pub = (np.arange(waves) % 4 == 0) & ~last
+    assert (st[pub, 5] >= st[pub, 4]).all() and not st[~pub, 5].any()
+    assert (st[last, 6] >= st[last, 4]).all() and not st[~last, 6].any()
+    assert (st[:, 7] < 16).all()
+
+
 def _argmax_case(dev, orc, h, x, batch):
     w, keep = dev_quant(h)
     logits = orc.gemv_quant(h, x, batch)
