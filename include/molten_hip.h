@@ -505,7 +505,12 @@ int mh_gemm_q4_grouped_gu_act(const uint16_t* x, const uint32_t* ids_sorted, uin
  * (no allocation): router -> route -> sort -> maps -> gate/up+SwiGLU ->
  * down -> combine.  out bf16 [m, d_model].  The workspace holds the
  * intermediates below; mh_moe_prefill_workspace returns its size and (if
- * offsets != NULL) each region's byte offset. */
+ * offsets != NULL) each region's byte offset.  With a bf16 router of at most
+ * 64 experts and d_model 1024 or 2048 the router runs on the matrix cores:
+ * the logits region then holds the chunk-order logit of every expert that
+ * could reach a token's top-k (every chosen one among them) and, for the
+ * others, an approximation within 2^-12 sum |x w| + 2^-138 of it; ids and
+ * weights are the chunk-order routing's either way. */
 enum {
     MH_PREFILL_WS_LOGITS = 0, MH_PREFILL_WS_IDS, MH_PREFILL_WS_GW, MH_PREFILL_WS_COUNTS,
     MH_PREFILL_WS_OFFSETS, MH_PREFILL_WS_IDS_SORTED, MH_PREFILL_WS_SLOTPOS,

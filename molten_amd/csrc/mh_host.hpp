@@ -51,12 +51,21 @@ int check_quant_dequant(const mh_quant_weights* w, const char* op);
 // the totals), their per-expert prefix, then the stable scatter, counts,
 // offsets and both block maps (three launches).
 constexpr uint32_t kPrefillRouteBlock = 16;  // tokens per routing block (histogram row)
+// routed: ids, gw and hb's block rows are already written (route_mma), only
+// the prefix and the scatter run.
 int moe_route_sort_maps(const float* logits, const float* bias, int mode, float eps, uint32_t m,
                         uint32_t e, uint32_t topk, uint32_t* ids, uint16_t* gw, uint32_t* hb,
                         uint32_t* counts, uint32_t* offsets, uint32_t* gu_off, uint32_t* dn_off,
                         uint32_t* ids_sorted, uint32_t* slotpos, uint32_t* gu, uint32_t max_gu, uint32_t* dn,
                         uint32_t max_dn, uint32_t bm, uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n,
-                        uint32_t dn_n, mh_stream_t stream);
+                        uint32_t dn_n, mh_stream_t stream, bool routed = false);
+// The prefill router and top-k on the matrix cores with exact routing
+// (moe_route_mma.hip): logits (chunk-order values for every candidate), ids,
+// gw and the routing blocks' expert histograms hb, for a bf16 router.
+bool route_mma_fits(const void* w, int w_dtype, const uint16_t* x, uint32_t e, uint32_t k, uint32_t topk);
+int route_mma(const uint16_t* x, const uint16_t* w, const float* bias, int mode, float eps, uint32_t m, uint32_t e,
+              uint32_t k, uint32_t topk, float* logits, uint32_t* ids, uint16_t* gw, uint32_t* hb,
+              hipStream_t stream);
 int moe_sort_maps(const uint32_t* ids, uint32_t s, uint32_t e, uint32_t topk, uint32_t* counts,
                   uint32_t* offsets, uint32_t* gu_off, uint32_t* dn_off, uint32_t* ids_sorted,
                   uint32_t* slotpos, uint32_t* gu, uint32_t max_gu, uint32_t* dn, uint32_t max_dn,

@@ -567,7 +567,7 @@ int moe_route_sort_maps(const float* logits, const float* bias, int mode, float 
                         uint32_t* counts, uint32_t* offsets, uint32_t* gu_off, uint32_t* dn_off,
                         uint32_t* ids_sorted, uint32_t* slotpos, uint32_t* gu, uint32_t max_gu, uint32_t* dn,
                         uint32_t max_dn, uint32_t bm, uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n,
-                        uint32_t dn_n, mh_stream_t stream) {
+                        uint32_t dn_n, mh_stream_t stream, bool routed) {
     static_assert(kRouteBlock * mh::kMaxTopk <= 256, "a block's slots, one per thread");
     MH_ENSURE(e >= 1 && e <= static_cast<uint32_t>(mh::kMaxExperts) && topk >= 1 &&
                   topk <= static_cast<uint32_t>(mh::kMaxTopk) && topk <= e,
@@ -585,13 +585,15 @@ int moe_route_sort_maps(const float* logits, const float* bias, int mode, float 
                                eps, ids, gw, hb);                                                           \
         }                                                                                                   \
         break;
-    switch (topk) {
-        MH_ROUTE_HIST(1) MH_ROUTE_HIST(2) MH_ROUTE_HIST(3) MH_ROUTE_HIST(4)
-        MH_ROUTE_HIST(5) MH_ROUTE_HIST(6) MH_ROUTE_HIST(7) MH_ROUTE_HIST(8)
-        default: break;
+    if (!routed) {
+        switch (topk) {
+            MH_ROUTE_HIST(1) MH_ROUTE_HIST(2) MH_ROUTE_HIST(3) MH_ROUTE_HIST(4)
+            MH_ROUTE_HIST(5) MH_ROUTE_HIST(6) MH_ROUTE_HIST(7) MH_ROUTE_HIST(8)
+            default: break;
+        }
+        MH_TRY(mh::launch_status("k_route_hist"));
     }
 #undef MH_ROUTE_HIST
-    MH_TRY(mh::launch_status("k_route_hist"));
     uint32_t* tot = hb + static_cast<size_t>(nblk) * e;
     hipLaunchKernelGGL(k_hist_prefix, dim3(e), dim3(256), 0, st, hb, tot, nblk, e);
     MH_TRY(mh::launch_status("k_hist_prefix"));

@@ -123,11 +123,22 @@ int mh_moe_prefill(const void* router, int router_dtype, const float* bias, int 
 
     // the block histograms of the routing live in the down GEMM's output
     // region until that GEMM runs
-    MH_TRY(mh::router_prefill_logits(x, router, router_dtype, logits, m, d_model, n_experts, stream));
+    // a bf16 router: logits and top-k in one launch on the matrix cores
+    // (moe_route_mma.hip; the routing exact), else the chunk-order logits of
+    // every expert, then the top-k
+    const bool mma = mh::route_mma_fits(router, router_dtype, x, n_experts, d_model, topk);
+    if (mma) {
+        MH_ENSURE(mode == MH_ROUTE_SIGMOID_BIAS || mode == MH_ROUTE_SOFTMAX, MH_ERR_INVALID, "%s: mode %d", op,
+                  mode);
+        MH_TRY(mh::route_mma(x, static_cast<const uint16_t*>(router), bias, mode, eps, m, n_experts, d_model, topk,
+                             logits, ids, gw, reinterpret_cast<uint32_t*>(ed), mh::as_stream(stream)));
+    } else {
+        MH_TRY(mh::router_prefill_logits(x, router, router_dtype, logits, m, d_model, n_experts, stream));
+    }
     MH_TRY(mh::moe_route_sort_maps(logits, bias, mode, eps, m, n_experts, topk, ids, gw,
                                    reinterpret_cast<uint32_t*>(ed), counts, offsets, gu_off, dn_off,
                                    ids_sorted, slotpos, gu_map, l.max_gu, dn_map, l.max_dn, kBM, kGuBN,
-                                   kDnBN, n_inter, d_model, stream));
+                                   kDnBN, n_inter, d_model, stream, mma));
     MH_TRY(mh_gemm_q4_grouped_gu_act(x, ids_sorted, m, gate, up, act, gu_map, l.max_gu, s, n_inter,
                                      kBM, kGuBN, stream));
     MH_TRY(mh_gemm_q4_grouped(act, down, ed, dn_map, l.max_dn, s, d_model, kBM, kDnBN, stream));

@@ -61,6 +61,8 @@ uint16_t orc_f32_to_bf16(float f);
  * GPU can reproduce it bit for bit.  Pinned: max error vs float64 exp over a
  * dense sweep (tests/test_oracle_math.py). */
 float orc_expf(float x);
+/* max over floats z of (max_{t <= z} s(t)) - s(z), s(z) = 1 / (1 + orc_expf(-z)) */
+double orc_sigmoid_max_drop(void);
 
 /* ---- a2 / a3: unpack and pack (lfm.metal:102-109, :186-199;
  *      quant_nax.metal:2947-2953, :2975-2986) --------------------------------

@@ -48,6 +48,8 @@ def lib() -> ctypes.CDLL:
         _lib.orc_f32_to_bf16.argtypes = [ctypes.c_float]
         _lib.orc_expf.restype = ctypes.c_float
         _lib.orc_expf.argtypes = [ctypes.c_float]
+        _lib.orc_sigmoid_max_drop.restype = ctypes.c_double
+        _lib.orc_sigmoid_max_drop.argtypes = []
         _lib.orc_argmax_bf16.restype = ctypes.c_uint32
         _lib.orc_argmax_key.restype = ctypes.c_uint64
         _lib.orc_argmax_key.argtypes = [ctypes.c_float, ctypes.c_uint32]
@@ -94,6 +96,13 @@ def f32_to_bf16(f: float) -> int:
 
 def expf(x: float) -> float:
     return lib().orc_expf(x)
+
+
+def sigmoid_max_drop() -> float:
+    """Largest drop of 1 / (1 + expf(-z)) below its running maximum over
+    every float z in increasing order (the routing score's monotonicity
+    defect)."""
+    return lib().orc_sigmoid_max_drop()
 
 
 def expf_array(x: np.ndarray) -> np.ndarray:

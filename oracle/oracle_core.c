@@ -623,6 +623,46 @@ void orc_gemv_dense(const void* w, int w_is_f32, const uint16_t* x, uint32_t m,
 
 /* ------------------------------------------------------------ routing --- */
 
+/* Largest drop of the sigmoid score s(z) = 1 / (1 + orc_expf(-z)) (route_one's
+ * mode 0) below its running maximum, over every float z from -inf to +inf in
+ * increasing order: the monotonicity defect a bound on s must allow for
+ * (0 would mean non-decreasing).  Chunks in parallel, each keeping its max,
+ * min and internal drop; a chunk's drop under an earlier running maximum M is
+ * max(internal, M - min). */
+double orc_sigmoid_max_drop(void) {
+    const int64_t half = (int64_t)0x7f800001;  /* -inf .. -0, then +0 .. +inf */
+    const int64_t total = 2 * half;
+    enum { CH = 8192 };
+    float cmax[CH], cmin[CH];
+    double cdrop[CH];
+#pragma omp parallel for schedule(dynamic, 16)
+    for (int ch = 0; ch < CH; ++ch) {
+        const int64_t lo = total * ch / CH, hi = total * (ch + 1) / CH;
+        float run = -1.0f, mn = 2.0f;
+        double drop = 0.0;
+        for (int64_t i = lo; i < hi; ++i) {
+            const uint32_t u = i < half ? (uint32_t)(0xff800000u - (uint32_t)i) : (uint32_t)(i - half);
+            float z;
+            memcpy(&z, &u, 4);
+            const float sv = 1.0f / (1.0f + orc_expf(-z));
+            if (sv < run && (double)run - sv > drop) drop = (double)run - sv;
+            if (sv > run) run = sv;
+            if (sv < mn) mn = sv;
+        }
+        cmax[ch] = run;
+        cmin[ch] = mn;
+        cdrop[ch] = drop;
+    }
+    double d = 0.0;
+    float m = -1.0f;
+    for (int ch = 0; ch < CH; ++ch) {
+        if (cdrop[ch] > d) d = cdrop[ch];
+        if ((double)m - cmin[ch] > d) d = (double)m - cmin[ch];
+        if (cmax[ch] > m) m = cmax[ch];
+    }
+    return d;
+}
+
 static void route_one(const float* z, const float* bias, uint32_t e, uint32_t topk,
                       int mode, float eps, uint32_t* ids, uint16_t* w) {
     float s[256];

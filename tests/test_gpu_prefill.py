@@ -275,6 +275,15 @@ def test_moe_prefill_bf16_router_routing(dev, orc, m, e, h, mode):
     x = layout.synth_bf16(rng, (m, h))
     x[5] = 0
     x[9, 100] = 0x7f80
+    # a token of bf16 denormals (logits in the f32 subnormal range) and one
+    # with a few denormal elements among normal ones
+    x[3] = rng.integers(1, 0x80, h).astype(np.uint16) | (rng.integers(0, 2, h).astype(np.uint16) << 15)
+    x[4, ::7] = rng.integers(1, 0x80, len(x[4, ::7])).astype(np.uint16)
+    # one normal element of 2^-120 among denormals: the denormals carry a
+    # part of every logit far above the bound's 2^-138, so a matrix core that
+    # flushed them would leave the stored approximations outside the bound
+    x[6] = rng.integers(1, 0x80, h).astype(np.uint16) | (rng.integers(0, 2, h).astype(np.uint16) << 15)
+    x[6, 0] = 0x0380
     dg, _ = dev_quant(gate)
     du, _ = dev_quant(up)
     dd, _ = dev_quant(down)
@@ -294,6 +303,17 @@ def test_moe_prefill_bf16_router_routing(dev, orc, m, e, h, mode):
     rows = np.arange(m)[:, None]
     np.testing.assert_array_equal(lg[rows, ids].view(np.uint32), z[rows, ids].view(np.uint32),
                                   err_msg="chosen logits")
+    # the logits not recomputed (the matrix-core router's, bf16 routers of
+    # <= 64 experts) lie within its bound 2^-12 sum |x w| + 2^-138 of the
+    # chunk-order values
+    xf = layout.bf16_to_f32(x).astype(np.float64)
+    rf = layout.bf16_to_f32(r).astype(np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        c = np.abs(xf) @ np.abs(rf).T
+        err = np.abs(lg.astype(np.float64) - z.astype(np.float64))
+    fin = np.isfinite(c) & np.isfinite(z)
+    bad = fin & ~(err <= c * 2.0 ** -12 + 2.0 ** -138)
+    assert not bad.any(), (np.argwhere(bad)[:5], err[bad][:5], c[bad][:5])
 
 
 def _dense_map(m, n, bm=128, bn=64):

@@ -74,6 +74,17 @@ def test_expf_special_values(orc):
         assert abs(orc.expf(v) - math.exp(v)) <= 2 ** -149
 
 
+def test_sigmoid_score_drops_at_most_half_ulp(orc):
+    """The sigmoid routing score 1 / (1 + expf(-z)) over every float z in
+    increasing order never falls more than 2^-24 below its running maximum
+    (exhaustive, 4.3e9 values; the defect comes from the exp's reduction
+    boundaries).  The matrix-core prefill router widens its score bounds by
+    this amount; the test also checks the drop is not zero, i.e. that the
+    scan does see the function's defect."""
+    d = orc.sigmoid_max_drop()
+    assert 0.0 < d <= 2.0 ** -24, d
+
+
 def test_unpack_known_answers(orc):
     np.testing.assert_array_equal(orc.unpack(np.array([0x76543210], np.uint32), 4, 8),
                                   np.arange(8))
