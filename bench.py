@@ -662,7 +662,7 @@ def main() -> int:
     ap.add_argument("--head-timeline", type=int, default=0,
                     help="only print the per-phase timelines of the batch-1 heads (configs 2 and 5) over "
                          "this many launches (device timestamps), then exit")
-    ap.add_argument("--only", choices=("config2", "config3", "config4"), default=None,
+    ap.add_argument("--only", choices=("config2", "config3", "config4", "config5"), default=None,
                     help="only time this workload, print its line and exit (for profiler runs)")
     ap.add_argument("--eager", action="store_true",
                     help="launch the timed steps directly instead of replaying a graph "
@@ -708,6 +708,12 @@ def main() -> int:
         ms2 = bench_lm_head(torch, hip, dev, gen, 4, 1, steps, warmup, copies=5)
         print(json.dumps({"only": "config2_lm_head_q4_argmax", "ms_per_step": round(ms2, 5),
                           "GB/s": round(BYTES["config2"] / (ms2 * 1e-3) / 1e9, 1)}), flush=True)
+        return 0
+    if args.only == "config5":
+        for batch in (1, 8):
+            ms5 = bench_lm_head(torch, hip, dev, gen, 6, batch, steps, warmup, copies=4)
+            print(json.dumps({"only": f"config5_b{batch}_q6_lm_head_argmax", "ms_per_step": round(ms5, 5),
+                              "GB/s": round(BYTES[f"config5_b{batch}"] / (ms5 * 1e-3) / 1e9, 1)}), flush=True)
         return 0
     if args.only == "config3":
         ms3 = bench_config3(torch, hip, dev, gen, steps, warmup)
