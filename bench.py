@@ -536,9 +536,10 @@ def cpu_baselines(budget_s: float, threads_all: int):
     affine dequant semantics, f32 accumulation, OpenMP over output rows /
     expert rows) on the host cores, every BASELINE config at 1 thread and at
     `threads_all` threads, each timed for about budget_s seconds.  Config 4
-    runs the whole prefill step (router, sort, gate/up + SwiGLU, down,
-    combine) for a stated subset of tokens (their expert rows only) and is
-    reported in FLOP/s of the rows computed."""
+    times the oracle's grouped GEMMs alone (gate, up and down of `ne`
+    experts x 256 rows, the config's mean rows per expert: one expert at 1
+    thread, one per thread at `threads_all`), not the router, sort and
+    combine around them, and is reported in FLOP/s of those rows."""
     import numpy as np
 
     from molten_amd import layout
