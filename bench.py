@@ -314,9 +314,11 @@ def timeline_config3(torch, hip, dev, gen, launches):
 
 
 HEAD_PHASES = ("start", "loads_issued", "x_shared", "rows_stored", "keys_merged", "key_published", "collected")
+HEAD8_PHASES = ("start", "x_staged", "main_loop_done", "summary_published", "finisher_words_read",
+                "finisher_id_written")
 
 
-def timeline_head(torch, hip, dev, gen, bits, launches, copies):
+def timeline_head(torch, hip, dev, gen, bits, launches, copies, batch=1):
     """The batch-1 head (65536 x 2048, Q4 or Q6, logits + argmax id) launched
     `launches` times back to back on rotating weight copies, each launch with
     per-wave phase timestamps (100 MHz clock) in a buffer of its own.  Per
@@ -331,44 +333,59 @@ def timeline_head(torch, hip, dev, gen, bits, launches, copies):
 
     n, k = 65536, 2048
     ws = make_quant(torch, n, k, bits, copies, dev, gen)
-    x = bf16_randn(torch, (1, k), dev, gen)
-    y = torch.empty((1, n), dtype=torch.int16, device=dev)
-    scratch = torch.zeros(hip.argmax_scratch_words(1), dtype=torch.int64, device=dev)
-    ids = torch.empty(1, dtype=torch.int32, device=dev)
+    x = bf16_randn(torch, (batch, k), dev, gen)
+    y = torch.empty((batch, n), dtype=torch.int16, device=dev)
+    scratch = torch.zeros(hip.argmax_scratch_words(batch), dtype=torch.int64, device=dev)
+    ids = torch.empty(batch, dtype=torch.int32, device=dev)
     nw, nst = hip.GEMV_STAMP_WAVES, hip.GEMV_STAMPS
     stamps = torch.zeros((launches + 2, nw * nst), dtype=torch.int64, device=dev)
     for i in range(3):  # warm-up
-        hip.gemv_quant_argmax_stamped(ws[i % copies][0], x, y, scratch, ids, stamps[0])
+        hip.gemv_quant_argmax_stamped(ws[i % copies][0], x, y, scratch, ids, stamps[0], batch)
     stamps.zero_()
     torch.cuda.synchronize()
     for i in range(launches + 2):  # back to back, as a replay runs them
-        hip.gemv_quant_argmax_stamped(ws[i % copies][0], x, y, scratch, ids, stamps[i])
+        hip.gemv_quant_argmax_stamped(ws[i % copies][0], x, y, scratch, ids, stamps[i], batch)
     torch.cuda.synchronize()
     allst = stamps.cpu().numpy().reshape(launches + 2, nw, nst)[2:]
+    names = HEAD_PHASES if batch == 1 else HEAD8_PHASES
     per, scal = [], []
     for st in allst:
+        st = st[st[:, 0] != 0]  # the launch's waves
         t0 = st[:, 0].min()
-        rel = (st[:, :7].astype(np.float64) - t0) / 100.0
+        rel = (st[:, :len(names)].astype(np.float64) - t0) / 100.0
         rows = []
-        for ph in range(7):
+        for ph in range(len(names)):
             v = rel[:, ph][st[:, ph] != 0]
             rows.append([float(np.percentile(v, 10)), float(np.percentile(v, 50)), float(np.percentile(v, 90)),
                          float(v.max())] if v.size else [float("nan")] * 4)
         per.append(rows)
         starts = np.sort(rel[:, 0])
-        first_done = rel[:, 4][st[:, 4] != 0].min()
-        gen1 = starts[starts < first_done]
-        last_pub = rel[:, 5][st[:, 5] != 0].max()
-        coll = rel[:, 6][st[:, 6] != 0].max()
-        scal.append([gen1.size, gen1.max(), starts.max(), last_pub, coll, coll - last_pub])
+        if batch == 1:
+            first_done = rel[:, 4][st[:, 4] != 0].min()
+            gen1 = starts[starts < first_done]
+            last_pub = rel[:, 5][st[:, 5] != 0].max()
+            coll = rel[:, 6][st[:, 6] != 0].max()
+            scal.append([gen1.size, gen1.max(), starts.max(), last_pub, coll, coll - last_pub])
+        else:
+            last_pub = rel[:, 3][st[:, 3] != 0].max()
+            words = rel[:, 4][st[:, 4] != 0].max()
+            end = rel[:, 5][st[:, 5] != 0].max()
+            scal.append([len(starts), starts.max(), last_pub, words - last_pub, end - words, end])
     med = np.median(np.array(per), axis=0)
     ms = np.median(np.array(scal), axis=0)
     del ws
-    return {"phases_us_p10_p50_p90_max": {name: [round(v, 2) for v in med[i]] for i, name in enumerate(HEAD_PHASES)},
-            "first_generation_waves": int(ms[0]), "first_generation_last_start_us": round(float(ms[1]), 2),
-            "last_start_us": round(float(ms[2]), 2), "last_key_published_us": round(float(ms[3]), 2),
-            "collector_end_us": round(float(ms[4]), 2), "collector_detection_us": round(float(ms[5]), 2),
-            "waves": nw, "launches": launches}
+    out = {"phases_us_p10_p50_p90_max": {name: [round(v, 2) for v in med[i]] for i, name in enumerate(names)}}
+    if batch == 1:
+        out.update(first_generation_waves=int(ms[0]), first_generation_last_start_us=round(float(ms[1]), 2),
+                   last_start_us=round(float(ms[2]), 2), last_key_published_us=round(float(ms[3]), 2),
+                   collector_end_us=round(float(ms[4]), 2), collector_detection_us=round(float(ms[5]), 2))
+    else:
+        out.update(waves_started=int(ms[0]), last_start_us=round(float(ms[1]), 2),
+                   last_summary_published_us=round(float(ms[2]), 2),
+                   finisher_detection_us=round(float(ms[3]), 2), finisher_collect_recompute_us=round(float(ms[4]), 2),
+                   end_us=round(float(ms[5]), 2))
+    out.update(launches=launches)
+    return out
 
 
 def bench_config4(torch, hip, dev, gen, steps, warmup):
@@ -661,7 +678,7 @@ def main() -> int:
                     help="only print the per-phase timeline of config 3's decode step over this many "
                          "launches (device timestamps), then exit")
     ap.add_argument("--head-timeline", type=int, default=0,
-                    help="only print the per-phase timelines of the batch-1 heads (configs 2 and 5) over "
+                    help="only print the per-phase timelines of the heads (configs 2, 5 b=1 and 5 b=8) over "
                          "this many launches (device timestamps), then exit")
     ap.add_argument("--only", choices=("config2", "config3", "config4", "config5"), default=None,
                     help="only time this workload, print its line and exit (for profiler runs)")
@@ -692,9 +709,11 @@ def main() -> int:
         return 0
 
     if args.head_timeline > 0:
-        for name, bits, copies in (("config2_q4_lm_head_argmax", 4, 5), ("config5_b1_q6_lm_head_argmax", 6, 4)):
+        for name, bits, copies, batch in (("config2_q4_lm_head_argmax", 4, 5, 1),
+                                          ("config5_b1_q6_lm_head_argmax", 6, 4, 1),
+                                          ("config5_b8_q6_lm_head_argmax", 6, 4, 8)):
             print(json.dumps({"timeline": name, **timeline_head(torch, hip, dev, gen, bits, args.head_timeline,
-                                                                copies)}), flush=True)
+                                                                copies, batch)}), flush=True)
         return 0
 
     if args.only is not None and args.calibrate_copy_mib > 0:

@@ -191,22 +191,27 @@ int mh_gemv_head_argmax(const mh_quant_weights* w, const uint16_t* x, uint64_t* 
 int mh_gemv_quant_argmax(const mh_quant_weights* w, const uint16_t* x, uint16_t* y,
                          uint64_t* scratch, uint32_t* ids, uint32_t batch, mh_stream_t stream);
 
-/* Measurement only (no reference counterpart): mh_gemv_quant_argmax at batch
- * 1 with phase timestamps, for the heads whose every wave computes one
- * 8-row block (K 2048, group 64, N a multiple of 8 from 16 x 8 rows per CU
- * up to 65536 rows: 32768..65536 on a 256-CU part; otherwise
- * MH_ERR_UNSUPPORTED).  `stamps` holds
- * MH_GEMV_STAMP_WAVES x MH_GEMV_STAMPS u64 words; lane 0 of each of the
- * launch's waves w (workgroup w / 4) writes its words at w * MH_GEMV_STAMPS:
- * the 100 MHz constant clock at wave start, block loads issued, x shared,
- * row values stored, workgroup keys merged, workgroup key published (wave 0
- * of every workgroup but the collector), slots collected and ids written
- * (the collector's waves); word 7 the XCD the workgroup ran on.  Outputs are
- * mh_gemv_quant_argmax's. */
+/* Measurement only (no reference counterpart): mh_gemv_quant_argmax with
+ * phase timestamps for the measured head shapes; otherwise
+ * MH_ERR_UNSUPPORTED.  `stamps` holds MH_GEMV_STAMP_WAVES x MH_GEMV_STAMPS u64
+ * words; lane 0 of each of the launch's waves w writes its words at w *
+ * MH_GEMV_STAMPS, word 7 the XCD its workgroup ran on, the others the 100
+ * MHz constant clock:
+ *   batch 1 (the chunk-order kernel; K 2048, group 64, N a multiple of 8 from
+ *   16 x 8 rows per CU up to 65536 rows: 32768..65536 on a 256-CU part; 4
+ *   waves per workgroup, one 8-row block per wave): wave start, block loads
+ *   issued, x shared, row values stored, workgroup keys merged, workgroup key
+ *   published (wave 0 of every workgroup but the collector), slots collected
+ *   and ids written (the collector's waves);
+ *   batch 8 (the matrix-core kernel: 256 workgroups of 8 waves): wave start,
+ *   x staged, main loop done, batch row b's summary published (waves b < 8),
+ *   then in the finisher (the last workgroup) wave b: every workgroup's words
+ *   read, row b's id written.
+ * Outputs are mh_gemv_quant_argmax's. */
 #define MH_GEMV_STAMP_WAVES 8192u
 #define MH_GEMV_STAMPS 8u
 int mh_gemv_quant_argmax_stamped(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint64_t* scratch,
-                                 uint32_t* ids, uint64_t* stamps, mh_stream_t stream);
+                                 uint32_t* ids, uint32_t batch, uint64_t* stamps, mh_stream_t stream);
 
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

@@ -844,10 +844,15 @@ int gemv_common(const char* op, const mh_quant_weights* w, const uint16_t* x, ui
     const hipStream_t s = mh::as_stream(stream);
     if (stamps != nullptr) {
         a.stamps = stamps;
-        const int rc = w->bits == 4 ? launch_rows_stamped<4>(a, s) : w->bits == 6 ? launch_rows_stamped<6>(a, s)
-                                                                                  : MH_ERR_UNSUPPORTED;
-        MH_ENSURE(rc != MH_ERR_UNSUPPORTED || batch != 1, MH_ERR_UNSUPPORTED,
-                  "%s: %u x %u Q%u is not the batch-1 head's one-block-per-wave shape", op, w->out_features,
+        int rc = MH_ERR_UNSUPPORTED;
+        if (batch == 1u) {
+            rc = w->bits == 4 ? launch_rows_stamped<4>(a, s) : w->bits == 6 ? launch_rows_stamped<6>(a, s)
+                                                                             : MH_ERR_UNSUPPORTED;
+        } else if (batch == 8u) {
+            rc = mh::gemv_mfma(w, x, y, best, ids, batch, s, stamps);
+        }
+        MH_ENSURE(rc != MH_ERR_UNSUPPORTED, MH_ERR_UNSUPPORTED,
+                  "%s: batch %u, %u x %u Q%u is not a measured head shape", op, batch, w->out_features,
                   w->in_features, w->bits);
         return rc;
     }
@@ -1081,12 +1086,13 @@ int mh_gemv_quant_argmax(const mh_quant_weights* w, const uint16_t* x, uint16_t*
 }
 
 int mh_gemv_quant_argmax_stamped(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint64_t* scratch,
-                                 uint32_t* ids, uint64_t* stamps, mh_stream_t stream) {
+                                 uint32_t* ids, uint32_t batch, uint64_t* stamps, mh_stream_t stream) {
     const char* op = "mh_gemv_quant_argmax_stamped";
     MH_ENSURE(scratch != nullptr && ids != nullptr, MH_ERR_INVALID, "%s: scratch/ids is NULL", op);
     MH_ENSURE(stamps != nullptr && mh::aligned(stamps, 8), MH_ERR_INVALID, "%s: stamps NULL or not 8-byte aligned",
               op);
-    return gemv_common(op, w, x, y, scratch, true, ids, 1, stream, stamps);
+    MH_ENSURE(batch == 1u || batch == 8u, MH_ERR_UNSUPPORTED, "%s: batch %u (1 or 8)", op, batch);
+    return gemv_common(op, w, x, y, scratch, true, ids, batch, stream, stamps);
 }
 
 int mh_token_tail(uint64_t* best, uint32_t* out_tok, uint32_t batch, mh_stream_t stream) {

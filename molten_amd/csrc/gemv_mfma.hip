@@ -57,8 +57,31 @@ struct MfmaArgs {
     unsigned long long* slots;  // [batch][kArgSlots] finisher scratch, or null (no argmax)
     uint32_t* ids;              // [batch]
     uint32_t* status;           // device status word (MH_STATUS_*), or null
+    uint64_t* stamps;           // per wave MH_GEMV_STAMPS phase words (stamped kernels only)
     uint32_t n, k, groups, row_bytes;
 };
+
+// Phase timestamps (the 100 MHz constant clock), lane 0 of every wave,
+// stamped instantiation only.
+enum MfmaStamp {
+    MS_START = 0,      // the wave began
+    MS_X = 1,          // x, its group sums and sum |x| in the LDS (the barrier after them)
+    MS_LOOP = 2,       // the wave's main loop (its tiles) done
+    MS_SUMMARY = 3,    // waves b < B: batch row b's summary published (or kept, the finisher)
+    MS_WORDS = 4,      // finisher wave b: every workgroup's words read
+    MS_ID = 5,         // finisher wave b: batch row b's id written
+    MS_XCC = 7         // the XCD the workgroup ran on
+};
+static_assert(MS_XCC + 1 == MH_GEMV_STAMPS, "stamp words");
+
+template <bool ST>
+__device__ __forceinline__ void mfma_stamp(const MfmaArgs& a, uint32_t gw, int lane, int which) {
+    if constexpr (ST) {
+        if (lane == 0) {
+            a.stamps[static_cast<size_t>(gw) * MH_GEMV_STAMPS + which] = wall_clock64();
+        }
+    }
+}
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -187,7 +210,7 @@ struct StageShape {
     static constexpr int kStrideWords = BITS == 6 ? 100 : 68;           // LDS row stride
 };
 
-template <int BITS, int B>
+template <int BITS, int B, bool ST = false>
 __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
     constexpr int PW = BITS == 6 ? 12 : 8;  // bytes of a lane's piece of a group
     using SS = StageShape<BITS>;
@@ -205,6 +228,15 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t gw = blockIdx.x * kWaves + static_cast<uint32_t>(wave);
+    mfma_stamp<ST>(a, gw, lane, MS_START);
+    if constexpr (ST) {
+        if (lane == 0) {
+            uint32_t xcc;
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+            a.stamps[static_cast<size_t>(gw) * MH_GEMV_STAMPS + MS_XCC] = xcc & 0xfu;
+        }
+    }
     const uint32_t q = static_cast<uint32_t>(lane) >> 4;  // lane quarter
     const uint32_t n = static_cast<uint32_t>(lane) & 15u;  // B column (batch row)
     const bool col = n < static_cast<uint32_t>(B);
@@ -452,6 +484,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         }
     }
     __syncthreads();
+    mfma_stamp<ST>(a, gw, lane, MS_X);
 
     for (uint32_t s0 = 0; s0 < n_stages; s0 += kDepth) {
 #pragma unroll
@@ -474,6 +507,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
             }
         }
     }
+    mfma_stamp<ST>(a, gw, lane, MS_LOOP);
     if (a.slots == nullptr) {
         return;
     }
@@ -559,6 +593,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
                 own[b][j] = out[j];
             }
         }
+        mfma_stamp<ST>(a, gw, lane, MS_SUMMARY);
     }
     if (blockIdx.x != last) {
         return;
@@ -623,6 +658,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
             }
         }
     }
+    mfma_stamp<ST>(a, gw, lane, MS_WORDS);
     // an expired wait, or one in the previous launch: a workgroup that read
     // the count only after that finisher bumped it published under this
     // launch's tag, so this launch's words cannot be trusted either
@@ -718,6 +754,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
             __hip_atomic_fetch_or(a.status, MH_STATUS_ARGMAX_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+    mfma_stamp<ST>(a, gw, lane, MS_ID);
     // clear the words for the next launch (last: no later load waits on them)
 #pragma unroll
     for (int j = 0; j < kWords; ++j) {
@@ -729,12 +766,19 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
 
 template <int BITS, int B>
 int launch(const MfmaArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL((k_gemv_mfma<BITS, B>), dim3(kGrid), dim3(kThreads), 0, stream, a);
+    if (a.stamps != nullptr) {
+        hipLaunchKernelGGL((k_gemv_mfma<BITS, B, true>), dim3(kGrid), dim3(kThreads), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((k_gemv_mfma<BITS, B>), dim3(kGrid), dim3(kThreads), 0, stream, a);
+    }
     return mh::launch_status("k_gemv_mfma");
 }
 
 template <int BITS>
 int dispatch(const MfmaArgs& a, uint32_t batch, hipStream_t stream) {
+    if (a.stamps != nullptr) {  // the measured shape only: the stamped instantiations are batch 8
+        return batch == 8u ? launch<BITS, 8>(a, stream) : MH_ERR_UNSUPPORTED;
+    }
     switch (batch) {
         case 2: return launch<BITS, 2>(a, stream);
         case 3: return launch<BITS, 3>(a, stream);
@@ -753,7 +797,7 @@ namespace mh {
 // Batched head GEMV on the matrix cores; MH_ERR_UNSUPPORTED when the shape
 // needs the staged chunk-order kernel (the caller then uses it).
 int gemv_mfma(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint64_t* slots, uint32_t* ids,
-              uint32_t batch, hipStream_t stream) {
+              uint32_t batch, hipStream_t stream, uint64_t* stamps) {
     const uint32_t K = w->in_features;
     if (batch < 2 || batch > static_cast<uint32_t>(kMaxB) || w->group_size != 64u || K % (64u * kStageGroups) != 0 ||
         K > kMaxK || w->out_features % kTileRows != 0 || w->out_features > kRowMask || !mh::aligned(x, 16) || !mh::aligned(w->codes, 8) ||
@@ -774,6 +818,7 @@ int gemv_mfma(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint64_
     a.groups = K / 64u;
     a.row_bytes = K * w->bits / 8u;
     a.status = mh::status_word();
+    a.stamps = stamps;
     return w->bits == 4 ? dispatch<4>(a, batch, stream) : dispatch<6>(a, batch, stream);
 }
 

@@ -79,8 +79,9 @@ int moe_decode_fused(const void* router, int router_dtype, const float* bias, in
 // Workgroups x waves of the fused decode step (the stamp buffer holds
 // kGrid * kWaves * MH_MOE_DECODE_STAMPS words).
 uint32_t moe_decode_fused_waves();
+// stamps: per-wave phase timestamps (measurement, batch 8 only), or null.
 int gemv_mfma(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint64_t* slots, uint32_t* ids,
-              uint32_t batch, hipStream_t stream);
+              uint32_t batch, hipStream_t stream, uint64_t* stamps = nullptr);
 int router_prefill_logits(const uint16_t* x, const void* w, int w_dtype, float* logits, uint32_t m,
                           uint32_t k, uint32_t e, mh_stream_t stream);
 

@@ -84,7 +84,7 @@ _SIGNATURES = {
     "mh_gemv_quant": [_qw, _vp, _vp, _u32, _vp],
     "mh_gemv_head_argmax": [_qw, _vp, _vp, _u32, _vp],
     "mh_gemv_quant_argmax": [_qw, _vp, _vp, _vp, _vp, _u32, _vp],
-    "mh_gemv_quant_argmax_stamped": [_qw, _vp, _vp, _vp, _vp, _vp, _vp],
+    "mh_gemv_quant_argmax_stamped": [_qw, _vp, _vp, _vp, _vp, _u32, _vp, _vp],
     "mh_gemv_quant_argmax_noalloc": [_qw, _vp, _vp, _vp, _u32, _vp],
     "mh_proj3_gemv_scatter": [_qw, _qw, _qw, _vp, _vp, _vp, _vp, _u32, _u32, _vp],
     "mh_conv3_gemv": [_qw, _vp, _vp, _vp, _vp, _vp, _vp],
@@ -318,11 +318,11 @@ GEMV_STAMP_WAVES = 8192  # MH_GEMV_STAMP_WAVES
 GEMV_STAMPS = 8  # MH_GEMV_STAMPS
 
 
-def gemv_quant_argmax_stamped(w: QuantWeights, x, y, scratch, ids, stamps, stream=None) -> None:
-    """gemv_quant_argmax at batch 1 with per-wave phase timestamps
+def gemv_quant_argmax_stamped(w: QuantWeights, x, y, scratch, ids, stamps, batch: int = 1, stream=None) -> None:
+    """gemv_quant_argmax at batch 1 or 8 with per-wave phase timestamps
     (measurement only): stamps u64 [GEMV_STAMP_WAVES * GEMV_STAMPS]."""
-    check(load().mh_gemv_quant_argmax_stamped(_qref(w), _ptr(x), _ptr(y), _ptr(scratch), _ptr(ids), _ptr(stamps),
-                                              _stream(stream)), "gemv_quant_argmax_stamped")
+    check(load().mh_gemv_quant_argmax_stamped(_qref(w), _ptr(x), _ptr(y), _ptr(scratch), _ptr(ids), batch,
+                                              _ptr(stamps), _stream(stream)), "gemv_quant_argmax_stamped")
 
 
 def token_tail(best, out_tok, batch: int = 1, stream=None) -> None:

@@ -113,6 +113,9 @@ def test_argmax_arguments():
         hip.gemv_quant_argmax_stamped(_qw(), 0x4000, 0x5000, 0x6000, 0x7000, None, stream=0)
     with pytest.raises(hip.MoltenError):  # stamps not 8-byte aligned
         hip.gemv_quant_argmax_stamped(_qw(), 0x4000, 0x5000, 0x6000, 0x7000, 0x8004, stream=0)
+    with pytest.raises(hip.MoltenError) as ei:  # a batch without a stamped kernel
+        hip.gemv_quant_argmax_stamped(_qw(), 0x4000, 0x5000, 0x6000, 0x7000, 0x8000, batch=3, stream=0)
+    assert ei.value.code == hip.MH_ERR_UNSUPPORTED
     with pytest.raises(hip.MoltenError):
         hip.token_tail(0x6000, 0x7000, batch=0, stream=0)
     with pytest.raises(hip.MoltenError):

@@ -400,7 +400,7 @@ def test_stamped_head_matches_oracle(dev, orc, bits):
     ids = empty_dev((1,), np.uint32)
     stamps = zeros_dev((hip.GEMV_STAMP_WAVES * hip.GEMV_STAMPS,), np.uint64)
     for call in range(2):
-        hip.gemv_quant_argmax_stamped(w, to_dev(x), y, scratch, ids, stamps)
+        hip.gemv_quant_argmax_stamped(w, to_dev(x), y, scratch, ids, stamps, 1)
         np.testing.assert_array_equal(from_dev(y, np.uint16), want)
         assert from_dev(ids, np.uint32).tolist() == [orc.argmax_bf16(want[0])]
         assert_scratch(scratch, n, k, 1, call + 1)
@@ -415,6 +415,42 @@ def test_stamped_head_matches_oracle(dev, orc, bits):
     pub = (np.arange(waves) % 4 == 0) & ~last
     assert (st[pub, 5] >= st[pub, 4]).all() and not st[~pub, 5].any()
     assert (st[last, 6] >= st[last, 4]).all() and not st[~last, 6].any()
+    assert (st[:, 7] < 16).all()
+
+
+@pytest.mark.parametrize("bits", [4, 6])
+def test_stamped_batch8_head_matches_oracle(dev, orc, bits):
+    """The measurement instantiation of the batch-8 matrix-core head: ids the
+    oracle's, logits within the kernel's tolerance, the scratch re-zeroed and
+    counted; every wave of the 256 x 8 launch stamps its start, x staging and
+    main loop in order, waves 0..7 of every workgroup their summary, and only
+    the last workgroup's waves 0..7 the finisher's two phases."""
+    _log(f"stamped batch-8 head bits={bits}")
+    rng = np.random.default_rng(4343 + bits)
+    n, k, batch = 8192, 2048, 8
+    h = layout.synth_quant(rng, n, k, bits)
+    x = layout.synth_bf16(rng, (batch, k))
+    w, keep = dev_quant(h)
+    want = orc.gemv_quant(h, x, batch)
+    y = empty_dev((batch, n), np.uint16)
+    scratch = zeros_dev((hip.argmax_scratch_words(batch),), np.uint64)
+    ids = empty_dev((batch,), np.uint32)
+    stamps = zeros_dev((hip.GEMV_STAMP_WAVES * hip.GEMV_STAMPS,), np.uint64)
+    for call in range(2):
+        hip.gemv_quant_argmax_stamped(w, to_dev(x), y, scratch, ids, stamps, batch)
+        assert from_dev(ids, np.uint32).tolist() == [orc.argmax_bf16(want[b]) for b in range(batch)]
+        assert_scratch(scratch, n, k, batch, call + 1)
+    assert_logits(from_dev(y, np.uint16), want, n, k, batch)
+    st = from_dev(stamps, np.uint64).reshape(hip.GEMV_STAMP_WAVES, hip.GEMV_STAMPS).astype(np.int64)
+    waves = 256 * 8
+    assert not st[waves:].any()
+    st = st[:waves]
+    assert (st[:, :3] > 0).all() and (np.diff(st[:, :3], axis=1) >= 0).all()
+    wave = np.arange(waves) % 8
+    last = np.arange(waves) // 8 == 255
+    assert (st[:, 3] >= st[:, 2]).all()
+    assert (st[:, 4:6] > 0).all(axis=1).tolist() == last.tolist()
+    assert (st[last, 5] >= st[last, 4]).all() and (st[last, 4] >= st[last, 3]).all()
     assert (st[:, 7] < 16).all()
 
 
