@@ -388,6 +388,51 @@ def timeline_head(torch, hip, dev, gen, bits, launches, copies, batch=1):
     return out
 
 
+def timeline_config4(torch, hip, dev, gen, launches):
+    """Config 4's prefill step run `launches` times back to back with the two
+    grouped GEMMs stamped per workgroup (start, end, block-map entry and its
+    rows).  Per GEMM (medians over launches): the span from the first start
+    to the last end, the workgroups' busy time over span x CUs (one workgroup
+    per CU at a time), and each workgroup's duration by its entry's 32-row
+    blocks (the passes: up to 8 blocks in one, 9..16 in two)."""
+    import numpy as np
+
+    E, H, I, topk, m = 64, 2048, 1536, 4, 4096
+    sets = [moe_set(torch, dev, gen) for _ in range(2)]
+    x = bf16_randn(torch, (m, H), dev, gen)
+    out = torch.empty((m, H), dtype=torch.int16, device=dev)
+    total, offs = hip.moe_prefill_workspace(m, E, topk, H, I)
+    ws = torch.zeros(total, dtype=torch.uint8, device=dev)
+    nst = 2 * hip.PREFILL_STAMP_WGS * hip.PREFILL_STAMPS
+    stamps = torch.zeros((launches + 1, nst), dtype=torch.int64, device=dev)
+    for i in range(launches + 1):
+        g, u, d, r = sets[i % len(sets)]
+        hip.moe_prefill_stamped(r, None, g[0], u[0], d[0], E, topk, x, m, out, ws, total, stamps[i],
+                                mode=hip.ROUTE_SOFTMAX)
+    torch.cuda.synchronize()
+    allst = stamps.cpu().numpy().reshape(launches + 1, 2, hip.PREFILL_STAMP_WGS, hip.PREFILL_STAMPS)[1:]
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    res = {}
+    for gi, name in ((0, "gate_up_swiglu"), (1, "down")):
+        spans, busy, by_rb = [], [], {}
+        for st in allst[:, gi]:
+            st = st[st[:, 0] != 0]
+            t0, t1 = st[:, 0].min(), st[:, 1].max()
+            dur = (st[:, 1] - st[:, 0]) / 100.0
+            spans.append((t1 - t0) / 100.0)
+            busy.append(float(dur.sum() / (cus * (t1 - t0) / 100.0)))
+            ent = st[:, 2] & 0xffffffff
+            rows = st[:, 2] >> 32
+            for rb, dv in zip(((rows + 31) // 32)[ent != 0xffffffff], dur[ent != 0xffffffff]):
+                by_rb.setdefault(int(rb), []).append(float(dv))
+        res[name] = {"workgroups": int((allst[0, gi][:, 0] != 0).sum()),
+                     "span_us": round(float(np.median(spans)), 1), "busy_over_span": round(float(np.median(busy)), 3),
+                     "us_by_row_blocks": {str(k): [round(float(np.median(v)), 1), len(v) // launches]
+                                          for k, v in sorted(by_rb.items())}}
+    del sets
+    return {**res, "launches": launches, "cus": cus}
+
+
 def bench_config4(torch, hip, dev, gen, steps, warmup):
     E, H, I, topk, m = 64, 2048, 1536, 4, 4096
     sets = [moe_set(torch, dev, gen) for _ in range(2)]
@@ -680,6 +725,9 @@ def main() -> int:
     ap.add_argument("--head-timeline", type=int, default=0,
                     help="only print the per-phase timelines of the heads (configs 2, 5 b=1 and 5 b=8) over "
                          "this many launches (device timestamps), then exit")
+    ap.add_argument("--gemm-timeline", type=int, default=0,
+                    help="only print the workgroup timelines of config 4's grouped GEMMs over this many "
+                         "prefill steps (device timestamps), then exit")
     ap.add_argument("--only", choices=("config2", "config3", "config4", "config5"), default=None,
                     help="only time this workload, print its line and exit (for profiler runs)")
     ap.add_argument("--eager", action="store_true",
@@ -708,6 +756,10 @@ def main() -> int:
                           **timeline_config3(torch, hip, dev, gen, args.timeline)}), flush=True)
         return 0
 
+    if args.gemm_timeline > 0:
+        print(json.dumps({"timeline": "config4_grouped_gemms",
+                          **timeline_config4(torch, hip, dev, gen, args.gemm_timeline)}), flush=True)
+        return 0
     if args.head_timeline > 0:
         for name, bits, copies, batch in (("config2_q4_lm_head_argmax", 4, 5, 1),
                                           ("config5_b1_q6_lm_head_argmax", 6, 4, 1),

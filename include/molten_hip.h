@@ -530,6 +530,23 @@ int mh_moe_prefill(const void* router, int router_dtype, const float* bias, int 
                    const uint16_t* x, uint32_t m, uint16_t* out, void* workspace,
                    size_t workspace_bytes, mh_stream_t stream);
 
+/* Measurement only (no reference counterpart): mh_moe_prefill with the two
+ * grouped GEMMs stamped per workgroup.  `stamps` holds 2 x
+ * MH_PREFILL_STAMP_WGS x MH_PREFILL_STAMPS u64 words (gate/up + SwiGLU, then
+ * down); workgroup g of a GEMM writes at g * MH_PREFILL_STAMPS: the 100 MHz
+ * constant clock at its start and at its end (after its last stores were
+ * issued), then its block-map entry (0xffffffff for a padding workgroup) |
+ * the entry's row count << 32.  Outputs are mh_moe_prefill's.
+ * MH_ERR_UNSUPPORTED where the GEMMs do not take the segment kernels or
+ * need more workgroups than the buffer holds. */
+#define MH_PREFILL_STAMP_WGS 4096u
+#define MH_PREFILL_STAMPS 4u
+int mh_moe_prefill_stamped(const void* router, int router_dtype, const float* bias, int mode, float eps,
+                           const mh_quant_weights* gate, const mh_quant_weights* up,
+                           const mh_quant_weights* down, uint32_t n_experts, uint32_t topk,
+                           const uint16_t* x, uint32_t m, uint16_t* out, void* workspace,
+                           size_t workspace_bytes, uint64_t* stamps, mh_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

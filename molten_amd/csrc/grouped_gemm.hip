@@ -61,6 +61,7 @@ struct GemmArgs {
     const uint4* blocks;     // block map; null: a dense product (entries computed)
     uint32_t k, n, s_rows, a_rows, w_rows;
     uint32_t dense_bm;       // rows per entry of a dense product (k_seg)
+    uint64_t* stamps;        // per workgroup MH_PREFILL_STAMPS words (stamped k_seg only), or null
 };
 
 // One Q4 word (8 codes, low nibble first) -> bf16(fma(s, q, b)) x 8.  High
@@ -818,16 +819,31 @@ __device__ uint32_t balanced_entry(const GemmArgs& a, uint32_t n_entries, uint32
     return g == 0xffffffffu ? n_entries : g * nt + j % nt;
 }
 
-template <int RBMAX, int NS, int NBW, int NMAT, bool GATHER, int EPI>
+// Workgroup stamps of the stamped k_seg (thread 0): the 100 MHz constant
+// clock at the start and at the end (after every wave's last store was
+// issued), and the workgroup's entry (0xffffffff: padding) | row count << 32.
+template <bool ST>
+__device__ __forceinline__ void seg_stamp(const GemmArgs& a, int which, uint64_t v) {
+    if constexpr (ST) {
+        if (threadIdx.x == 0) {
+            a.stamps[static_cast<size_t>(blockIdx.x) * MH_PREFILL_STAMPS + which] = v;
+        }
+    }
+}
+
+template <int RBMAX, int NS, int NBW, int NMAT, bool GATHER, int EPI, bool ST = false>
 __global__ __launch_bounds__(kSegWaves * 64, (SegLayout<RBMAX, NBW, NMAT, NS>::LDS <= 80 * 1024 ? 2 : 1))
 void k_seg(GemmArgs a, uint32_t n_entries) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lds0 = static_cast<uint32_t>((uintptr_t)((lds_ptr)lds));
+    seg_stamp<ST>(a, 0, wall_clock64());
     const uint32_t nt = a.n / (kSegWaves * NBW * 32u);
     const uint32_t ent = balanced_entry(a, n_entries, nt, lds, lane, wave);
     if (ent >= n_entries) {
+        seg_stamp<ST>(a, 2, 0xffffffffull);
+        seg_stamp<ST>(a, 1, wall_clock64());
         return;
     }
     uint4 blk;
@@ -838,7 +854,9 @@ void k_seg(GemmArgs a, uint32_t n_entries) {
         blk = a.blocks[ent];
     }
     const uint32_t m0 = blk.x, brow = blk.y, n0 = blk.z, m_end = blk.w;
+    seg_stamp<ST>(a, 2, ent | (static_cast<uint64_t>(m_end > m0 ? m_end - m0 : 0u) << 32));
     if (m0 >= m_end) {
+        seg_stamp<ST>(a, 1, wall_clock64());
         return;
     }
     const uint32_t nrb = (m_end - m0 + 31u) / 32u;
@@ -863,12 +881,29 @@ void k_seg(GemmArgs a, uint32_t n_entries) {
 #undef MH_SEG_CASE
         mp0 += rb * 32u;
     }
+    if constexpr (ST) {
+        __syncthreads();
+        seg_stamp<ST>(a, 1, wall_clock64());
+    }
 }
 
 template <int RBMAX, int NS, int NBW, int NMAT, bool GATHER, int EPI>
 int launch_seg(const GemmArgs& a, uint32_t n_blocks, hipStream_t s) {
     constexpr size_t lds = SegLayout<RBMAX, NBW, NMAT, NS>::LDS;
     static_assert(lds <= 160 * 1024, "LDS per workgroup");
+    if (a.stamps != nullptr) {
+        const uint32_t grid = grid_for_map(n_blocks, a.n / (kSegWaves * NBW * 32u));
+        MH_ENSURE(grid <= MH_PREFILL_STAMP_WGS, MH_ERR_UNSUPPORTED, "k_seg: %u workgroups exceed the stamp buffer",
+                  grid);
+        auto kst = k_seg<RBMAX, NS, NBW, NMAT, GATHER, EPI, true>;
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kst),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (e != hipSuccess) {
+            return mh::hip_error(e, "k_seg");
+        }
+        hipLaunchKernelGGL(kst, dim3(grid), dim3(kSegWaves * 64), lds, s, a, n_blocks);
+        return mh::launch_status("k_seg");
+    }
     auto kern = k_seg<RBMAX, NS, NBW, NMAT, GATHER, EPI>;
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -917,6 +952,14 @@ int dispatch(const GemmArgs& a, uint32_t n_blocks, uint32_t bm, uint32_t bn, hip
                      static_cast<uint64_t>(a.w_rows) * a.k / 2u < (1ull << 32) &&
                      static_cast<uint64_t>(a.s_rows) * a.n * 2u < (1ull << 32) &&
                      mh::aligned(a.out0, 16) && (a.out1 == nullptr || mh::aligned(a.out1, 16));
+    if (a.stamps != nullptr) {  // measurement: the segment kernels only
+        if constexpr (EPI == EPI_STORE) {
+            if (seg && bn == 256) return launch_seg<kSegRBMax, kSegStages, 2, 1, GATHER, EPI>(a, n_blocks, s);
+        } else {
+            if (seg && bn == 128) return launch_seg<kSegRBMax, kSegStages, 1, 2, GATHER, EPI>(a, n_blocks, s);
+        }
+        return mh::set_error(MH_ERR_UNSUPPORTED, "grouped GEMM: stamps need the segment kernel's tiles");
+    }
     if constexpr (EPI == EPI_STORE) {
         if (bm == 32 && bn == 64) return launch_t<32, 2, 1, GATHER, EPI>(a, n_blocks, s);
         if (bm == 128 && bn == 64) return launch_t<128, 2, 1, GATHER, EPI>(a, n_blocks, s);
@@ -969,6 +1012,29 @@ GemmArgs make_args(const uint16_t* a, const uint32_t* gather, uint32_t a_rows,
 }
 
 }  // namespace
+
+namespace mh {
+
+// The prefill step's two grouped GEMMs with workgroup stamps (measurement):
+// as mh_gemm_q4_grouped_gu_act and mh_gemm_q4_grouped, the segment kernels
+// only.
+int gemm_gu_act_stamped(const uint16_t* x, const uint32_t* ids_sorted, uint32_t x_rows, const mh_quant_weights* gate,
+                        const mh_quant_weights* up, uint16_t* act, const uint32_t* blocks, uint32_t n_blocks,
+                        uint32_t s_rows, uint32_t n, uint32_t bm, uint32_t bn, uint64_t* stamps, hipStream_t s) {
+    GemmArgs g = make_args(x, ids_sorted, x_rows, gate, up, act, nullptr, blocks, s_rows, n);
+    g.stamps = stamps;
+    return dispatch<true, EPI_SWIGLU>(g, n_blocks, bm, bn, s);
+}
+
+int gemm_grouped_stamped(const uint16_t* a, const mh_quant_weights* w, uint16_t* c, const uint32_t* blocks,
+                         uint32_t n_blocks, uint32_t s_rows, uint32_t n, uint32_t bm, uint32_t bn, uint64_t* stamps,
+                         hipStream_t s) {
+    GemmArgs g = make_args(a, nullptr, s_rows, w, nullptr, c, nullptr, blocks, s_rows, n);
+    g.stamps = stamps;
+    return dispatch<false, EPI_STORE>(g, n_blocks, bm, bn, s);
+}
+
+}  // namespace mh
 
 extern "C" {
 

@@ -79,6 +79,14 @@ int moe_decode_fused(const void* router, int router_dtype, const float* bias, in
 // Workgroups x waves of the fused decode step (the stamp buffer holds
 // kGrid * kWaves * MH_MOE_DECODE_STAMPS words).
 uint32_t moe_decode_fused_waves();
+// The prefill step's grouped GEMMs with workgroup stamps (grouped_gemm.hip;
+// measurement only, segment kernels only).
+int gemm_gu_act_stamped(const uint16_t* x, const uint32_t* ids_sorted, uint32_t x_rows, const mh_quant_weights* gate,
+                        const mh_quant_weights* up, uint16_t* act, const uint32_t* blocks, uint32_t n_blocks,
+                        uint32_t s_rows, uint32_t n, uint32_t bm, uint32_t bn, uint64_t* stamps, hipStream_t s);
+int gemm_grouped_stamped(const uint16_t* a, const mh_quant_weights* w, uint16_t* c, const uint32_t* blocks,
+                         uint32_t n_blocks, uint32_t s_rows, uint32_t n, uint32_t bm, uint32_t bn, uint64_t* stamps,
+                         hipStream_t s);
 // stamps: per-wave phase timestamps (measurement, batch 8 only), or null.
 int gemv_mfma(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint64_t* slots, uint32_t* ids,
               uint32_t batch, hipStream_t stream, uint64_t* stamps = nullptr);

@@ -73,12 +73,16 @@ size_t mh_moe_prefill_workspace(uint32_t m, uint32_t n_experts, uint32_t topk, u
     return l.total;
 }
 
-int mh_moe_prefill(const void* router, int router_dtype, const float* bias, int mode, float eps,
-                   const mh_quant_weights* gate, const mh_quant_weights* up,
-                   const mh_quant_weights* down, uint32_t n_experts, uint32_t topk,
-                   const uint16_t* x, uint32_t m, uint16_t* out, void* workspace,
-                   size_t workspace_bytes, mh_stream_t stream) {
-    const char* op = "mh_moe_prefill";
+}  // extern "C"
+
+namespace {
+
+// mh_moe_prefill, and with stamps != null its measured form (the two grouped
+// GEMMs with workgroup stamps).
+int prefill(const char* op, const void* router, int router_dtype, const float* bias, int mode, float eps,
+            const mh_quant_weights* gate, const mh_quant_weights* up, const mh_quant_weights* down,
+            uint32_t n_experts, uint32_t topk, const uint16_t* x, uint32_t m, uint16_t* out, void* workspace,
+            size_t workspace_bytes, mh_stream_t stream, uint64_t* stamps) {
     MH_ENSURE(gate && up && down && x && out && workspace && router, MH_ERR_INVALID,
               "%s: NULL argument", op);
     MH_ENSURE(m > 0, MH_ERR_INVALID, "%s: no tokens", op);
@@ -139,10 +143,43 @@ int mh_moe_prefill(const void* router, int router_dtype, const float* bias, int 
                                    reinterpret_cast<uint32_t*>(ed), counts, offsets, gu_off, dn_off,
                                    ids_sorted, slotpos, gu_map, l.max_gu, dn_map, l.max_dn, kBM, kGuBN,
                                    kDnBN, n_inter, d_model, stream, mma));
-    MH_TRY(mh_gemm_q4_grouped_gu_act(x, ids_sorted, m, gate, up, act, gu_map, l.max_gu, s, n_inter,
-                                     kBM, kGuBN, stream));
-    MH_TRY(mh_gemm_q4_grouped(act, down, ed, dn_map, l.max_dn, s, d_model, kBM, kDnBN, stream));
+    if (stamps != nullptr) {
+        const hipStream_t hs = mh::as_stream(stream);
+        MH_TRY(mh::gemm_gu_act_stamped(x, ids_sorted, m, gate, up, act, gu_map, l.max_gu, s, n_inter, kBM, kGuBN,
+                                       stamps, hs));
+        MH_TRY(mh::gemm_grouped_stamped(act, down, ed, dn_map, l.max_dn, s, d_model, kBM, kDnBN,
+                                        stamps + static_cast<size_t>(MH_PREFILL_STAMP_WGS) * MH_PREFILL_STAMPS, hs));
+    } else {
+        MH_TRY(mh_gemm_q4_grouped_gu_act(x, ids_sorted, m, gate, up, act, gu_map, l.max_gu, s, n_inter,
+                                         kBM, kGuBN, stream));
+        MH_TRY(mh_gemm_q4_grouped(act, down, ed, dn_map, l.max_dn, s, d_model, kBM, kDnBN, stream));
+    }
     return mh_moe_combine_rows(ed, slotpos, gw, out, m, d_model, topk, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int mh_moe_prefill(const void* router, int router_dtype, const float* bias, int mode, float eps,
+                   const mh_quant_weights* gate, const mh_quant_weights* up,
+                   const mh_quant_weights* down, uint32_t n_experts, uint32_t topk,
+                   const uint16_t* x, uint32_t m, uint16_t* out, void* workspace,
+                   size_t workspace_bytes, mh_stream_t stream) {
+    return prefill("mh_moe_prefill", router, router_dtype, bias, mode, eps, gate, up, down, n_experts, topk, x, m,
+                   out, workspace, workspace_bytes, stream, nullptr);
+}
+
+int mh_moe_prefill_stamped(const void* router, int router_dtype, const float* bias, int mode, float eps,
+                           const mh_quant_weights* gate, const mh_quant_weights* up,
+                           const mh_quant_weights* down, uint32_t n_experts, uint32_t topk,
+                           const uint16_t* x, uint32_t m, uint16_t* out, void* workspace,
+                           size_t workspace_bytes, uint64_t* stamps, mh_stream_t stream) {
+    const char* op = "mh_moe_prefill_stamped";
+    MH_ENSURE(stamps != nullptr && mh::aligned(stamps, 8), MH_ERR_INVALID, "%s: stamps NULL or not 8-byte aligned",
+              op);
+    return prefill(op, router, router_dtype, bias, mode, eps, gate, up, down, n_experts, topk, x, m, out, workspace,
+                   workspace_bytes, stream, stamps);
 }
 
 }  // extern "C"

@@ -138,6 +138,8 @@ _SIGNATURES = {
     "mh_moe_prefill_workspace": [_u32, _u32, _u32, _u32, _u32, ctypes.POINTER(_sz)],
     "mh_moe_prefill": [_vp, _i32, _vp, _i32, _f32, _qw, _qw, _qw, _u32, _u32, _vp, _u32, _vp,
                        _vp, _sz, _vp],
+    "mh_moe_prefill_stamped": [_vp, _i32, _vp, _i32, _f32, _qw, _qw, _qw, _u32, _u32, _vp, _u32, _vp,
+                               _vp, _sz, _vp, _vp],
 }
 _RESTYPES = {"mh_last_error": ctypes.c_char_p, "mh_version": ctypes.c_char_p,
              "mh_moe_prefill_workspace": ctypes.c_size_t, "mh_sample_workspace_bytes": ctypes.c_size_t, "mh_checkpoint_close": None,
@@ -681,3 +683,18 @@ def moe_prefill(router, bias, gate: QuantWeights, up: QuantWeights, down: QuantW
                                 _qref(gate), _qref(up), _qref(down), n_experts, topk, _ptr(x), m,
                                 _ptr(out), _ptr(workspace), workspace_bytes, _stream(stream)),
           "moe_prefill")
+
+
+PREFILL_STAMP_WGS = 4096  # MH_PREFILL_STAMP_WGS
+PREFILL_STAMPS = 4  # MH_PREFILL_STAMPS
+
+
+def moe_prefill_stamped(router, bias, gate: QuantWeights, up: QuantWeights, down: QuantWeights,
+                        n_experts: int, topk: int, x, m: int, out, workspace, workspace_bytes: int, stamps,
+                        mode: int = ROUTE_SIGMOID_BIAS, eps: float = 1e-6, stream=None) -> None:
+    """moe_prefill with the grouped GEMMs' workgroups stamped (measurement
+    only): stamps u64 [2 * PREFILL_STAMP_WGS * PREFILL_STAMPS]."""
+    check(load().mh_moe_prefill_stamped(_ptr(router), _dtype_of(router), _ptr(bias), mode, eps,
+                                        _qref(gate), _qref(up), _qref(down), n_experts, topk, _ptr(x), m,
+                                        _ptr(out), _ptr(workspace), workspace_bytes, _ptr(stamps), _stream(stream)),
+          "moe_prefill_stamped")

@@ -266,3 +266,5 @@ def test_python_mirrors_of_header_constants():
     assert hip.MOE_DECODE_STAMPS == define("MH_MOE_DECODE_STAMPS")
     assert hip.GEMV_STAMP_WAVES == define("MH_GEMV_STAMP_WAVES")
     assert hip.GEMV_STAMPS == define("MH_GEMV_STAMPS")
+    assert hip.PREFILL_STAMP_WGS == define("MH_PREFILL_STAMP_WGS")
+    assert hip.PREFILL_STAMPS == define("MH_PREFILL_STAMPS")

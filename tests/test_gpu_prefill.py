@@ -231,6 +231,53 @@ def _run_prefill(orc, m, mode, seed, sample=None):
     return got, want, mask
 
 
+def test_moe_prefill_stamped_matches_unstamped(dev, orc):
+    """The measurement form of the prefill step (grouped GEMMs stamped per
+    workgroup) gives the same bits as mh_moe_prefill; each GEMM's stamps form
+    one prefix of workgroups, each with its start before its end, and the
+    entries they name are exactly the block map's non-empty entries, once
+    each."""
+    _log("moe prefill stamped m=1024")
+    rng = np.random.default_rng(77)
+    E, H, I, topk, m = 64, 2048, 1536, 4, 1024
+    gate, up, down = moe_weights(rng, E, H, I)
+    router = router_weights(rng, E, H, f32=False)
+    x = to_dev(layout.synth_bf16(rng, (m, H)))
+    dg, kg = dev_quant(gate)
+    du, ku = dev_quant(up)
+    dd, kd = dev_quant(down)
+    total, offs = hip.moe_prefill_workspace(m, E, topk, H, I)
+    outs, wss = [], []
+    stamps = zeros_dev((2 * hip.PREFILL_STAMP_WGS * hip.PREFILL_STAMPS,), np.uint64)
+    for stamped in (False, True):
+        ws = zeros_dev((total // 4,), np.uint32)
+        out = zeros_dev((m, H), np.uint16)
+        r = to_dev(router)
+        if stamped:
+            hip.moe_prefill_stamped(r, None, dg, du, dd, E, topk, x, m, out, ws, total, stamps, mode=1)
+        else:
+            hip.moe_prefill(r, None, dg, du, dd, E, topk, x, m, out, ws, total, mode=1)
+        outs.append(from_dev(out, np.uint16))
+        wss.append(from_dev(ws, np.uint32).view(np.uint8))
+    np.testing.assert_array_equal(outs[1], outs[0])
+    st = from_dev(stamps, np.uint64).reshape(2, hip.PREFILL_STAMP_WGS, hip.PREFILL_STAMPS)
+    for g, key in ((0, "gu_map"), (1, "dn_map")):
+        o = offs[key]
+        nxt = min(v for v in offs.values() if v > o)
+        ents = wss[1][o:nxt].view(np.uint32).reshape(-1, 4)
+        live = set(int(i) for i in np.nonzero(ents[:, 3] > ents[:, 0])[0])
+        s_g = st[g]
+        n_wg = int((s_g[:, 0] != 0).sum())
+        assert n_wg > 0 and (s_g[:n_wg, 0] != 0).all() and not s_g[n_wg:].any()
+        assert (s_g[:n_wg, 1] >= s_g[:n_wg, 0]).all()
+        named = s_g[:n_wg, 2] & 0xffffffff
+        rows = s_g[:n_wg, 2] >> 32
+        real = named[(named != 0xffffffff) & (rows > 0)].astype(np.int64)
+        assert sorted(real.tolist()) == sorted(live)
+        assert (rows[named != 0xffffffff] == (ents[named[named != 0xffffffff].astype(np.int64), 3] -
+                                               ents[named[named != 0xffffffff].astype(np.int64), 0])).all()
+
+
 @pytest.mark.parametrize("mode", [1, 0])
 def test_moe_prefill_small(dev, orc, mode):
     _log(f"moe prefill m=256 mode={mode}")
