@@ -393,8 +393,9 @@ def timeline_config4(torch, hip, dev, gen, launches):
     grouped GEMMs stamped per workgroup (start, end, block-map entry and its
     rows).  Per GEMM (medians over launches): the span from the first start
     to the last end, the workgroups' busy time over span x CUs (one workgroup
-    per CU at a time), and each workgroup's duration by its entry's 32-row
-    blocks (the passes: up to 8 blocks in one, 9..16 in two)."""
+    per CU at a time), the time from a workgroup's start to its entry read
+    (workgroups with rows), and each workgroup's duration by its entry's
+    32-row blocks (the passes: up to 8 blocks in one, 9..16 in two)."""
     import numpy as np
 
     E, H, I, topk, m = 64, 2048, 1536, 4, 4096
@@ -414,7 +415,7 @@ def timeline_config4(torch, hip, dev, gen, launches):
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     res = {}
     for gi, name in ((0, "gate_up_swiglu"), (1, "down")):
-        spans, busy, by_rb = [], [], {}
+        spans, busy, by_rb, entry = [], [], {}, []
         for st in allst[:, gi]:
             st = st[st[:, 0] != 0]
             t0, t1 = st[:, 0].min(), st[:, 1].max()
@@ -425,8 +426,11 @@ def timeline_config4(torch, hip, dev, gen, launches):
             rows = st[:, 2] >> 32
             for rb, dv in zip(((rows + 31) // 32)[ent != 0xffffffff], dur[ent != 0xffffffff]):
                 by_rb.setdefault(int(rb), []).append(float(dv))
+            has = (ent != 0xffffffff) & (rows > 0)
+            entry.append(float(np.median((st[has, 3] - st[has, 0]) / 100.0)))
         res[name] = {"workgroups": int((allst[0, gi][:, 0] != 0).sum()),
                      "span_us": round(float(np.median(spans)), 1), "busy_over_span": round(float(np.median(busy)), 3),
+                     "entry_read_us": round(float(np.median(entry)), 2),
                      "us_by_row_blocks": {str(k): [round(float(np.median(v)), 1), len(v) // launches]
                                           for k, v in sorted(by_rb.items())}}
     del sets
@@ -448,6 +452,8 @@ def bench_config4(torch, hip, dev, gen, steps, warmup):
 
     ms_step = timed(torch, step, max(2, steps // 4), max(1, warmup // 4))
     # the two grouped GEMMs alone, replayed on the workspace of the last step
+    # through the public entry points (the reference-order maps, each
+    # workgroup ranking the map rows; the step reads the launch-ordered maps)
     g, u, d, r = sets[(max(2, steps // 4) + max(1, warmup // 4) - 1) % len(sets)]
     base = ws.data_ptr()
     s = m * topk

@@ -515,12 +515,16 @@ int mh_gemm_q4_grouped_gu_act(const uint16_t* x, const uint32_t* ids_sorted, uin
  * the logits region then holds the chunk-order logit of every expert that
  * could reach a token's top-k (every chosen one among them) and, for the
  * others, an approximation within 2^-12 sum |x w| + 2^-138 of it; ids and
- * weights are the chunk-order routing's either way. */
+ * weights are the chunk-order routing's either way.  GU_ORD / DN_ORD hold
+ * the two block maps' entries again in the grouped GEMMs' launch order
+ * (entry b for workgroup b, all-zero entries for workgroups without one;
+ * map rows ranked by row count, most first), when the map has at most 1024
+ * rows (else they are unused and the GEMMs rank the rows themselves). */
 enum {
     MH_PREFILL_WS_LOGITS = 0, MH_PREFILL_WS_IDS, MH_PREFILL_WS_GW, MH_PREFILL_WS_COUNTS,
     MH_PREFILL_WS_OFFSETS, MH_PREFILL_WS_IDS_SORTED, MH_PREFILL_WS_SLOTPOS,
     MH_PREFILL_WS_GU_OFF, MH_PREFILL_WS_DN_OFF, MH_PREFILL_WS_GU_MAP, MH_PREFILL_WS_DN_MAP,
-    MH_PREFILL_WS_ACT, MH_PREFILL_WS_ED, MH_PREFILL_WS_REGIONS
+    MH_PREFILL_WS_ACT, MH_PREFILL_WS_ED, MH_PREFILL_WS_GU_ORD, MH_PREFILL_WS_DN_ORD, MH_PREFILL_WS_REGIONS
 };
 size_t mh_moe_prefill_workspace(uint32_t m, uint32_t n_experts, uint32_t topk, uint32_t d_model,
                                 uint32_t n_inter, size_t* offsets);
@@ -534,9 +538,11 @@ int mh_moe_prefill(const void* router, int router_dtype, const float* bias, int 
  * grouped GEMMs stamped per workgroup.  `stamps` holds 2 x
  * MH_PREFILL_STAMP_WGS x MH_PREFILL_STAMPS u64 words (gate/up + SwiGLU, then
  * down); workgroup g of a GEMM writes at g * MH_PREFILL_STAMPS: the 100 MHz
- * constant clock at its start and at its end (after its last stores were
- * issued), then its block-map entry (0xffffffff for a padding workgroup) |
- * the entry's row count << 32.  Outputs are mh_moe_prefill's.
+ * constant clock at its start (word 0) and at its end (after its last stores
+ * were issued, word 1), its block-map entry (0xffffffff for a padding
+ * workgroup; with launch-ordered maps the index into GU_ORD / DN_ORD) | the
+ * entry's row count << 32 (word 2), and the clock once its entry was read
+ * (word 3; 0 for padding and empty entries).  Outputs are mh_moe_prefill's.
  * MH_ERR_UNSUPPORTED where the GEMMs do not take the segment kernels or
  * need more workgroups than the buffer holds. */
 #define MH_PREFILL_STAMP_WGS 4096u

@@ -61,6 +61,7 @@ struct GemmArgs {
     const uint4* blocks;     // block map; null: a dense product (entries computed)
     uint32_t k, n, s_rows, a_rows, w_rows;
     uint32_t dense_bm;       // rows per entry of a dense product (k_seg)
+    uint32_t ordered;        // k_seg: the map is in launch order (entry b for workgroup b)
     uint64_t* stamps;        // per workgroup MH_PREFILL_STAMPS words (stamped k_seg only), or null
 };
 
@@ -92,10 +93,7 @@ __device__ __forceinline__ uint32_t entry_of_block(uint32_t nt) {
     return ((j / nt) * 8u + x) * nt + j % nt;
 }
 
-inline uint32_t grid_for_map(uint32_t n_blocks, uint32_t nt) {
-    const uint32_t unit = 8u * nt;
-    return (n_blocks + unit - 1u) / unit * unit;
-}
+inline uint32_t grid_for_map(uint32_t n_blocks, uint32_t nt) { return mh::map_grid(n_blocks, nt); }
 constexpr int kStages = 3;  // LDS ring depth: two K-blocks in flight while one is consumed
 
 // Tile of BM rows x (NW * NBW * 32) columns per matrix; NW waves, wave w owns
@@ -785,8 +783,8 @@ __device__ uint32_t balanced_entry(const GemmArgs& a, uint32_t n_entries, uint32
     uint32_t* wts = reinterpret_cast<uint32_t*>(lds);  // [C] group weights
     __shared__ uint32_t s_group;
     const uint32_t C = (n_entries + nt - 1u) / nt;
-    const uint32_t x = blockIdx.x % 8u, j = blockIdx.x / 8u, slot = j / nt;
-    const uint32_t k_target = slot * 8u + ((slot & 1u) ? 7u - x : x);
+    const uint32_t j = blockIdx.x / 8u;
+    const uint32_t k_target = mh::seg_rank_of(blockIdx.x, nt);
     for (uint32_t c = threadIdx.x; c < C; c += blockDim.x) {
         if (blocks == nullptr) {  // dense: row segments of dense_bm, the last partial
             wts[c] = min(a.dense_bm, a.s_rows - c * a.dense_bm);
@@ -820,8 +818,10 @@ __device__ uint32_t balanced_entry(const GemmArgs& a, uint32_t n_entries, uint32
 }
 
 // Workgroup stamps of the stamped k_seg (thread 0): the 100 MHz constant
-// clock at the start and at the end (after every wave's last store was
-// issued), and the workgroup's entry (0xffffffff: padding) | row count << 32.
+// clock at the start (word 0), at the end after every wave's last store was
+// issued (word 1), and once the workgroup's entry is read (word 3; not for
+// padding or empty entries), and the workgroup's entry (0xffffffff: padding)
+// | row count << 32 (word 2).
 template <bool ST>
 __device__ __forceinline__ void seg_stamp(const GemmArgs& a, int which, uint64_t v) {
     if constexpr (ST) {
@@ -840,7 +840,9 @@ void k_seg(GemmArgs a, uint32_t n_entries) {
     const uint32_t lds0 = static_cast<uint32_t>((uintptr_t)((lds_ptr)lds));
     seg_stamp<ST>(a, 0, wall_clock64());
     const uint32_t nt = a.n / (kSegWaves * NBW * 32u);
-    const uint32_t ent = balanced_entry(a, n_entries, nt, lds, lane, wave);
+    // a launch-ordered map names this workgroup's entry directly; otherwise
+    // the groups are ranked here (mh::seg_rank_of)
+    const uint32_t ent = a.ordered ? static_cast<uint32_t>(blockIdx.x) : balanced_entry(a, n_entries, nt, lds, lane, wave);
     if (ent >= n_entries) {
         seg_stamp<ST>(a, 2, 0xffffffffull);
         seg_stamp<ST>(a, 1, wall_clock64());
@@ -859,6 +861,7 @@ void k_seg(GemmArgs a, uint32_t n_entries) {
         seg_stamp<ST>(a, 1, wall_clock64());
         return;
     }
+    seg_stamp<ST>(a, 3, wall_clock64());
     const uint32_t nrb = (m_end - m0 + 31u) / 32u;
     const uint32_t passes = (nrb + RBMAX - 1u) / RBMAX;
     uint32_t mp0 = m0;
@@ -952,13 +955,14 @@ int dispatch(const GemmArgs& a, uint32_t n_blocks, uint32_t bm, uint32_t bn, hip
                      static_cast<uint64_t>(a.w_rows) * a.k / 2u < (1ull << 32) &&
                      static_cast<uint64_t>(a.s_rows) * a.n * 2u < (1ull << 32) &&
                      mh::aligned(a.out0, 16) && (a.out1 == nullptr || mh::aligned(a.out1, 16));
-    if (a.stamps != nullptr) {  // measurement: the segment kernels only
+    if (a.stamps != nullptr || a.ordered) {  // launch-ordered maps, measurement: the segment kernels only
         if constexpr (EPI == EPI_STORE) {
             if (seg && bn == 256) return launch_seg<kSegRBMax, kSegStages, 2, 1, GATHER, EPI>(a, n_blocks, s);
         } else {
             if (seg && bn == 128) return launch_seg<kSegRBMax, kSegStages, 1, 2, GATHER, EPI>(a, n_blocks, s);
         }
-        return mh::set_error(MH_ERR_UNSUPPORTED, "grouped GEMM: stamps need the segment kernel's tiles");
+        return mh::set_error(MH_ERR_UNSUPPORTED, "grouped GEMM: launch-ordered maps and stamps need the segment "
+                                                 "kernel's tiles");
     }
     if constexpr (EPI == EPI_STORE) {
         if (bm == 32 && bn == 64) return launch_t<32, 2, 1, GATHER, EPI>(a, n_blocks, s);
@@ -1015,21 +1019,24 @@ GemmArgs make_args(const uint16_t* a, const uint32_t* gather, uint32_t a_rows,
 
 namespace mh {
 
-// The prefill step's two grouped GEMMs with workgroup stamps (measurement):
-// as mh_gemm_q4_grouped_gu_act and mh_gemm_q4_grouped, the segment kernels
-// only.
-int gemm_gu_act_stamped(const uint16_t* x, const uint32_t* ids_sorted, uint32_t x_rows, const mh_quant_weights* gate,
-                        const mh_quant_weights* up, uint16_t* act, const uint32_t* blocks, uint32_t n_blocks,
-                        uint32_t s_rows, uint32_t n, uint32_t bm, uint32_t bn, uint64_t* stamps, hipStream_t s) {
+// The prefill step's two grouped GEMMs (as mh_gemm_q4_grouped_gu_act and
+// mh_gemm_q4_grouped, the segment kernels only): on a launch-ordered map
+// (n_blocks: its map_grid entries) and / or with workgroup stamps.
+int gemm_gu_act_seg(const uint16_t* x, const uint32_t* ids_sorted, uint32_t x_rows, const mh_quant_weights* gate,
+                    const mh_quant_weights* up, uint16_t* act, const uint32_t* blocks, uint32_t n_blocks,
+                    uint32_t s_rows, uint32_t n, uint32_t bm, uint32_t bn, bool ordered, uint64_t* stamps,
+                    hipStream_t s) {
     GemmArgs g = make_args(x, ids_sorted, x_rows, gate, up, act, nullptr, blocks, s_rows, n);
+    g.ordered = ordered ? 1u : 0u;
     g.stamps = stamps;
     return dispatch<true, EPI_SWIGLU>(g, n_blocks, bm, bn, s);
 }
 
-int gemm_grouped_stamped(const uint16_t* a, const mh_quant_weights* w, uint16_t* c, const uint32_t* blocks,
-                         uint32_t n_blocks, uint32_t s_rows, uint32_t n, uint32_t bm, uint32_t bn, uint64_t* stamps,
-                         hipStream_t s) {
+int gemm_grouped_seg(const uint16_t* a, const mh_quant_weights* w, uint16_t* c, const uint32_t* blocks,
+                     uint32_t n_blocks, uint32_t s_rows, uint32_t n, uint32_t bm, uint32_t bn, bool ordered,
+                     uint64_t* stamps, hipStream_t s) {
     GemmArgs g = make_args(a, nullptr, s_rows, w, nullptr, c, nullptr, blocks, s_rows, n);
+    g.ordered = ordered ? 1u : 0u;
     g.stamps = stamps;
     return dispatch<false, EPI_STORE>(g, n_blocks, bm, bn, s);
 }

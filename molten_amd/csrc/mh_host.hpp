@@ -52,13 +52,39 @@ int check_quant_dequant(const mh_quant_weights* w, const char* op);
 // offsets and both block maps (three launches).
 constexpr uint32_t kPrefillRouteBlock = 16;  // tokens per routing block (histogram row)
 // routed: ids, gw and hb's block rows are already written (route_mma), only
-// the prefix and the scatter run.
+// the prefix and the scatter run.  gu_ord / dn_ord (or null): the two maps
+// again in the segment GEMMs' launch order (map_grid entries each; see
+// seg_rank_of), for launches that take entry b = workgroup b; the map rows
+// (max_gu / (gu_n / gu_bn)) must not exceed kMaxOrderedRows.
 int moe_route_sort_maps(const float* logits, const float* bias, int mode, float eps, uint32_t m,
                         uint32_t e, uint32_t topk, uint32_t* ids, uint16_t* gw, uint32_t* hb,
                         uint32_t* counts, uint32_t* offsets, uint32_t* gu_off, uint32_t* dn_off,
                         uint32_t* ids_sorted, uint32_t* slotpos, uint32_t* gu, uint32_t max_gu, uint32_t* dn,
                         uint32_t max_dn, uint32_t bm, uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n,
-                        uint32_t dn_n, mh_stream_t stream, bool routed = false);
+                        uint32_t dn_n, mh_stream_t stream, bool routed = false, uint32_t* gu_ord = nullptr,
+                        uint32_t* dn_ord = nullptr);
+
+// Launch order of the segment GEMMs (grouped_gemm.hip k_seg) over a block map
+// whose rows ("groups": one expert's row segment, nt column-tile entries
+// each) are ranked by row count, most first, lower map row first on ties.
+// The grid is whole units of 8 x nt workgroups; workgroup b takes rank
+// seg_rank_of(b, nt) (units in turn, the 8 XCDs' workgroups b % 8 walking
+// the ranks forward on even units and backward on odd ones, so each XCD gets
+// a heavy and a light group in turn) and column tile (b / 8) % nt of it.
+inline uint32_t map_grid(uint32_t n_blocks, uint32_t nt) {
+    const uint32_t unit = 8u * nt;
+    return (n_blocks + unit - 1u) / unit * unit;
+}
+__host__ __device__ inline uint32_t seg_rank_of(uint32_t b, uint32_t nt) {
+    const uint32_t x = b % 8u, slot = (b / 8u) / nt;
+    return slot * 8u + ((slot & 1u) ? 7u - x : x);
+}
+// the workgroup that takes column tile t of the group of rank r
+__host__ __device__ inline uint32_t seg_workgroup_of(uint32_t r, uint32_t t, uint32_t nt) {
+    const uint32_t slot = r / 8u, xr = r % 8u;
+    return ((slot * nt + t) * 8u) + ((slot & 1u) ? 7u - xr : xr);
+}
+constexpr uint32_t kMaxOrderedRows = 1024;  // map rows the scatter ranks in its LDS
 // The prefill router and top-k on the matrix cores with exact routing
 // (moe_route_mma.hip): logits (chunk-order values for every candidate), ids,
 // gw and the routing blocks' expert histograms hb, for a bf16 router.
@@ -79,14 +105,17 @@ int moe_decode_fused(const void* router, int router_dtype, const float* bias, in
 // Workgroups x waves of the fused decode step (the stamp buffer holds
 // kGrid * kWaves * MH_MOE_DECODE_STAMPS words).
 uint32_t moe_decode_fused_waves();
-// The prefill step's grouped GEMMs with workgroup stamps (grouped_gemm.hip;
-// measurement only, segment kernels only).
-int gemm_gu_act_stamped(const uint16_t* x, const uint32_t* ids_sorted, uint32_t x_rows, const mh_quant_weights* gate,
-                        const mh_quant_weights* up, uint16_t* act, const uint32_t* blocks, uint32_t n_blocks,
-                        uint32_t s_rows, uint32_t n, uint32_t bm, uint32_t bn, uint64_t* stamps, hipStream_t s);
-int gemm_grouped_stamped(const uint16_t* a, const mh_quant_weights* w, uint16_t* c, const uint32_t* blocks,
-                         uint32_t n_blocks, uint32_t s_rows, uint32_t n, uint32_t bm, uint32_t bn, uint64_t* stamps,
-                         hipStream_t s);
+// The prefill step's grouped GEMMs on the segment kernels (grouped_gemm.hip):
+// ordered, the map is in launch order (entry b for workgroup b, map_grid
+// entries, from moe_route_sort_maps' gu_ord / dn_ord); stamps (or null), per
+// workgroup MH_PREFILL_STAMPS words (measurement).
+int gemm_gu_act_seg(const uint16_t* x, const uint32_t* ids_sorted, uint32_t x_rows, const mh_quant_weights* gate,
+                    const mh_quant_weights* up, uint16_t* act, const uint32_t* blocks, uint32_t n_blocks,
+                    uint32_t s_rows, uint32_t n, uint32_t bm, uint32_t bn, bool ordered, uint64_t* stamps,
+                    hipStream_t s);
+int gemm_grouped_seg(const uint16_t* a, const mh_quant_weights* w, uint16_t* c, const uint32_t* blocks,
+                     uint32_t n_blocks, uint32_t s_rows, uint32_t n, uint32_t bm, uint32_t bn, bool ordered,
+                     uint64_t* stamps, hipStream_t s);
 // stamps: per-wave phase timestamps (measurement, batch 8 only), or null.
 int gemv_mfma(const mh_quant_weights* w, const uint16_t* x, uint16_t* y, uint64_t* slots, uint32_t* ids,
               uint32_t batch, hipStream_t stream, uint64_t* stamps = nullptr);

@@ -384,21 +384,36 @@ __global__ __launch_bounds__(256) void k_hist_prefix(uint32_t* hb, uint32_t* tot
     }
 }
 
+// The map rows of expert ex in launch order (gu_ord / dn_ord, see
+// mh::seg_rank_of): its row r's rank among all rows by row count (rows_l:
+// every map row's count), then its nt entries at their workgroups.
+__device__ void write_ordered(uint4* ord, uint32_t rank, uint32_t m0, uint32_t m_end, uint32_t ex, uint32_t bn,
+                              uint32_t n_cols) {
+    const uint32_t nt = n_cols / bn;
+    for (uint32_t t = threadIdx.x; t < nt; t += blockDim.x) {
+        ord[mh::seg_workgroup_of(rank, t, nt)] = make_uint4(m0, ex * n_cols + t * bn, t * bn, m_end);
+    }
+}
+
 // k_scatter_maps: workgroup j takes the expert totals (counts, offsets and
 // both block-map offsets by two workgroup scans) and its block's prefix row,
 // scatters block j's slots stably (slot order; ranks within each 64-slot
 // chunk from ballots), writes the block-map entries of experts j, j + G, ...
 // and zeroes its share of both maps' unused tails.  Workgroup 0 writes
-// counts, offsets and the block-map offsets.
+// counts, offsets and the block-map offsets.  With gu_ord / dn_ord, the same
+// entries again in launch order (unused workgroups' entries zero).
 __global__ __launch_bounds__(256) void k_scatter_maps(const uint32_t* ids, const uint32_t* pre, const uint32_t* tot,
                                                       uint32_t m, uint32_t e, uint32_t topk, uint32_t* counts,
                                                       uint32_t* offsets, uint32_t* gu_off, uint32_t* dn_off,
                                                       uint32_t* ids_sorted, uint32_t* slotpos, uint4* gu,
                                                       uint32_t max_gu, uint4* dn, uint32_t max_dn, uint32_t bm,
-                                                      uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n, uint32_t dn_n) {
+                                                      uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n, uint32_t dn_n,
+                                                      uint4* gu_ord, uint4* dn_ord, uint32_t gu_grid,
+                                                      uint32_t dn_grid) {
     __shared__ uint32_t tot_l[mh::kMaxExperts], off_l[mh::kMaxExperts], base_l[mh::kMaxExperts],
         rb_l[mh::kMaxExperts];
     __shared__ uint32_t chist[4][mh::kMaxExperts];
+    __shared__ uint32_t rows_l[mh::kMaxOrderedRows];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t j = blockIdx.x;
     const uint32_t total = tid < e ? tot[tid] : 0u;
@@ -443,6 +458,41 @@ __global__ __launch_bounds__(256) void k_scatter_maps(const uint32_t* ids, const
     }
     for (uint32_t i = rows_all * dn_tiles + j * 256u + tid; i < max_dn; i += gridDim.x * 256u) {
         dn[i] = make_uint4(0, 0, 0, 0);
+    }
+    if (gu_ord != nullptr) {
+        // every map row's count (rows_all <= kMaxOrderedRows, checked on the host)
+        for (uint32_t ex = tid; ex < e; ex += 256u) {
+            for (uint32_t r = 0; r * bm < tot_l[ex]; ++r) {
+                rows_l[rb_l[ex] + r] = min(bm, tot_l[ex] - r * bm);
+            }
+        }
+        __syncthreads();
+        for (uint32_t ex = j; ex < e; ex += gridDim.x) {
+            for (uint32_t r = 0; r * bm < tot_l[ex]; ++r) {
+                const uint32_t c = rb_l[ex] + r, w = rows_l[c];
+                uint32_t ahead = 0u;
+                for (uint32_t d = tid; d < rows_all; d += 256u) {
+                    const uint32_t v = rows_l[d];
+                    ahead += (v > w || (v == w && d < c)) ? 1u : 0u;
+                }
+                uint32_t rank;
+                (void)block_excl_scan_256(ahead, &rank);
+                const uint32_t m0 = off_l[ex] + r * bm, m_end = min(m0 + bm, off_l[ex] + tot_l[ex]);
+                write_ordered(gu_ord, rank, m0, m_end, ex, gu_bn, gu_n);
+                write_ordered(dn_ord, rank, m0, m_end, ex, dn_bn, dn_n);
+            }
+        }
+        // workgroups past the used rows' ranks take no entry
+        for (uint32_t b = j * 256u + tid; b < gu_grid; b += gridDim.x * 256u) {
+            if (mh::seg_rank_of(b, gu_tiles) >= rows_all) {
+                gu_ord[b] = make_uint4(0, 0, 0, 0);
+            }
+        }
+        for (uint32_t b = j * 256u + tid; b < dn_grid; b += gridDim.x * 256u) {
+            if (mh::seg_rank_of(b, dn_tiles) >= rows_all) {
+                dn_ord[b] = make_uint4(0, 0, 0, 0);
+            }
+        }
     }
     // rank within the wave's 64-slot chunk by ballots over the distinct experts
     const unsigned long long below = (1ull << lane) - 1ull;
@@ -567,7 +617,7 @@ int moe_route_sort_maps(const float* logits, const float* bias, int mode, float 
                         uint32_t* counts, uint32_t* offsets, uint32_t* gu_off, uint32_t* dn_off,
                         uint32_t* ids_sorted, uint32_t* slotpos, uint32_t* gu, uint32_t max_gu, uint32_t* dn,
                         uint32_t max_dn, uint32_t bm, uint32_t gu_bn, uint32_t dn_bn, uint32_t gu_n,
-                        uint32_t dn_n, mh_stream_t stream, bool routed) {
+                        uint32_t dn_n, mh_stream_t stream, bool routed, uint32_t* gu_ord, uint32_t* dn_ord) {
     static_assert(kRouteBlock * mh::kMaxTopk <= 256, "a block's slots, one per thread");
     MH_ENSURE(e >= 1 && e <= static_cast<uint32_t>(mh::kMaxExperts) && topk >= 1 &&
                   topk <= static_cast<uint32_t>(mh::kMaxTopk) && topk <= e,
@@ -597,9 +647,17 @@ int moe_route_sort_maps(const float* logits, const float* bias, int mode, float 
     uint32_t* tot = hb + static_cast<size_t>(nblk) * e;
     hipLaunchKernelGGL(k_hist_prefix, dim3(e), dim3(256), 0, st, hb, tot, nblk, e);
     MH_TRY(mh::launch_status("k_hist_prefix"));
+    const uint32_t gu_tiles = gu_n / gu_bn, dn_tiles = dn_n / dn_bn;
+    if (gu_ord != nullptr || dn_ord != nullptr) {
+        MH_ENSURE(gu_ord != nullptr && dn_ord != nullptr && max_gu / gu_tiles == max_dn / dn_tiles &&
+                      max_gu / gu_tiles <= mh::kMaxOrderedRows,
+                  MH_ERR_UNSUPPORTED, "prefill routing: launch-ordered maps of %u rows", max_gu / gu_tiles);
+    }
     hipLaunchKernelGGL(k_scatter_maps, dim3(nblk), dim3(256), 0, st, ids, hb, tot, m, e, topk, counts, offsets,
                        gu_off, dn_off, ids_sorted, slotpos, reinterpret_cast<uint4*>(gu), max_gu,
-                       reinterpret_cast<uint4*>(dn), max_dn, bm, gu_bn, dn_bn, gu_n, dn_n);
+                       reinterpret_cast<uint4*>(dn), max_dn, bm, gu_bn, dn_bn, gu_n, dn_n,
+                       reinterpret_cast<uint4*>(gu_ord), reinterpret_cast<uint4*>(dn_ord),
+                       mh::map_grid(max_gu, gu_tiles), mh::map_grid(max_dn, dn_tiles));
     return mh::launch_status("k_scatter_maps");
 }
 

@@ -4,7 +4,8 @@
 // Sequence (five launches and the combine): router logits (expert rows held
 // in the LDS, tokens streamed) -> per-token top-k with per-block expert
 // histograms -> counts, offsets, block-map offsets, the stable scatter and
-// the block maps (every workgroup sums the histograms) -> grouped gate/up
+// the block maps, also in the GEMMs' launch order (every workgroup sums the
+// histograms) -> grouped gate/up
 // GEMM with the ids_sorted row gather and the SwiGLU epilogue fused ->
 // grouped down GEMM -> weighted combine.  Compared with the reference's sequence this drops the
 // materialised gathered rows and the separate gate/up outputs (two 4-byte
@@ -26,6 +27,8 @@ struct Layout {
     size_t off[MH_PREFILL_WS_REGIONS];
     size_t total;
     uint32_t max_gu, max_dn;
+    bool ordered;              // launch-ordered maps (the map's rows fit the scatter's ranking)
+    uint32_t grid_gu, grid_dn;  // their entries: the GEMMs' workgroups
 };
 
 Layout layout_for(uint32_t m, uint32_t e, uint32_t topk, uint32_t d_model, uint32_t n_inter) {
@@ -34,6 +37,9 @@ Layout layout_for(uint32_t m, uint32_t e, uint32_t topk, uint32_t d_model, uint3
     Layout l{};
     l.max_gu = m_tiles * (n_inter / kGuBN);
     l.max_dn = m_tiles * (d_model / kDnBN);
+    l.ordered = m_tiles <= mh::kMaxOrderedRows;
+    l.grid_gu = mh::map_grid(l.max_gu, n_inter / kGuBN);
+    l.grid_dn = mh::map_grid(l.max_dn, d_model / kDnBN);
     const size_t sizes[MH_PREFILL_WS_REGIONS] = {
         static_cast<size_t>(m) * e * 4,  // logits f32 [m, e]
         s * 4,                           // ids u32 [m, topk]
@@ -50,6 +56,8 @@ Layout layout_for(uint32_t m, uint32_t e, uint32_t topk, uint32_t d_model, uint3
         std::max(s * d_model * 2,        // ed bf16 [s, d_model]; before the down GEMM, the
                                          // routing's block histograms and expert totals
                  (static_cast<size_t>((m + mh::kPrefillRouteBlock - 1) / mh::kPrefillRouteBlock) + 1) * e * 4),
+        l.ordered ? static_cast<size_t>(l.grid_gu) * 16 : 0,  // gate/up map in launch order
+        l.ordered ? static_cast<size_t>(l.grid_dn) * 16 : 0,  // down map in launch order
     };
     size_t at = 0;
     for (int i = 0; i < MH_PREFILL_WS_REGIONS; ++i) {
@@ -123,6 +131,8 @@ int prefill(const char* op, const void* router, int router_dtype, const float* b
     uint32_t* dn_map = reinterpret_cast<uint32_t*>(at(MH_PREFILL_WS_DN_MAP));
     uint16_t* act = reinterpret_cast<uint16_t*>(at(MH_PREFILL_WS_ACT));
     uint16_t* ed = reinterpret_cast<uint16_t*>(at(MH_PREFILL_WS_ED));
+    uint32_t* gu_ord = l.ordered ? reinterpret_cast<uint32_t*>(at(MH_PREFILL_WS_GU_ORD)) : nullptr;
+    uint32_t* dn_ord = l.ordered ? reinterpret_cast<uint32_t*>(at(MH_PREFILL_WS_DN_ORD)) : nullptr;
     const uint32_t s = m * topk;
 
     // the block histograms of the routing live in the down GEMM's output
@@ -142,13 +152,19 @@ int prefill(const char* op, const void* router, int router_dtype, const float* b
     MH_TRY(mh::moe_route_sort_maps(logits, bias, mode, eps, m, n_experts, topk, ids, gw,
                                    reinterpret_cast<uint32_t*>(ed), counts, offsets, gu_off, dn_off,
                                    ids_sorted, slotpos, gu_map, l.max_gu, dn_map, l.max_dn, kBM, kGuBN,
-                                   kDnBN, n_inter, d_model, stream, mma));
-    if (stamps != nullptr) {
+                                   kDnBN, n_inter, d_model, stream, mma, gu_ord, dn_ord));
+    if (l.ordered || stamps != nullptr) {
+        // the segment kernels: on the launch-ordered maps (each workgroup reads
+        // its entry, no ranking), and / or stamped
         const hipStream_t hs = mh::as_stream(stream);
-        MH_TRY(mh::gemm_gu_act_stamped(x, ids_sorted, m, gate, up, act, gu_map, l.max_gu, s, n_inter, kBM, kGuBN,
-                                       stamps, hs));
-        MH_TRY(mh::gemm_grouped_stamped(act, down, ed, dn_map, l.max_dn, s, d_model, kBM, kDnBN,
-                                        stamps + static_cast<size_t>(MH_PREFILL_STAMP_WGS) * MH_PREFILL_STAMPS, hs));
+        MH_TRY(mh::gemm_gu_act_seg(x, ids_sorted, m, gate, up, act, l.ordered ? gu_ord : gu_map,
+                                   l.ordered ? l.grid_gu : l.max_gu, s, n_inter, kBM, kGuBN, l.ordered, stamps, hs));
+        MH_TRY(mh::gemm_grouped_seg(act, down, ed, l.ordered ? dn_ord : dn_map, l.ordered ? l.grid_dn : l.max_dn, s,
+                                    d_model, kBM, kDnBN, l.ordered,
+                                    stamps != nullptr ? stamps + static_cast<size_t>(MH_PREFILL_STAMP_WGS) *
+                                                                     MH_PREFILL_STAMPS
+                                                      : nullptr,
+                                    hs));
     } else {
         MH_TRY(mh_gemm_q4_grouped_gu_act(x, ids_sorted, m, gate, up, act, gu_map, l.max_gu, s, n_inter,
                                          kBM, kGuBN, stream));

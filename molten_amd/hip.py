@@ -665,7 +665,7 @@ def gemm_q4_grouped_gu_act(x, ids_sorted, x_rows: int, gate: QuantWeights, up: Q
 
 
 PREFILL_WS_REGIONS = ["logits", "ids", "gw", "counts", "offsets", "ids_sorted", "slotpos",
-                      "gu_off", "dn_off", "gu_map", "dn_map", "act", "ed"]
+                      "gu_off", "dn_off", "gu_map", "dn_map", "act", "ed", "gu_ord", "dn_ord"]
 
 
 def moe_prefill_workspace(m: int, n_experts: int, topk: int, d_model: int, n_inter: int):

@@ -268,3 +268,8 @@ def test_python_mirrors_of_header_constants():
     assert hip.GEMV_STAMPS == define("MH_GEMV_STAMPS")
     assert hip.PREFILL_STAMP_WGS == define("MH_PREFILL_STAMP_WGS")
     assert hip.PREFILL_STAMPS == define("MH_PREFILL_STAMPS")
+    # the workspace regions, in the header's enum order
+    enum = re.search(r"enum \{\s*(MH_PREFILL_WS_LOGITS[^}]*)\}", text).group(1)
+    names = [w.strip().split("=")[0].strip() for w in enum.split(",") if w.strip()]
+    assert names[-1] == "MH_PREFILL_WS_REGIONS"
+    assert [n[len("MH_PREFILL_WS_"):].lower() for n in names[:-1]] == hip.PREFILL_WS_REGIONS

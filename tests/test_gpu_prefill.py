@@ -231,13 +231,41 @@ def _run_prefill(orc, m, mode, seed, sample=None):
     return got, want, mask
 
 
-def test_moe_prefill_stamped_matches_unstamped(dev, orc):
-    """The measurement form of the prefill step (grouped GEMMs stamped per
-    workgroup) gives the same bits as mh_moe_prefill; each GEMM's stamps form
-    one prefix of workgroups, each with its start before its end, and the
-    entries they name are exactly the block map's non-empty entries, once
-    each."""
-    _log("moe prefill stamped m=1024")
+def _launch_order(ents, nt):
+    """The segment GEMMs' launch order of a block map (CPU restatement of
+    mh::seg_rank_of / seg_workgroup_of): map rows (nt entries each) ranked by
+    row count, most first, lower row first on ties; rank r's column tile t at
+    workgroup ((r // 8) * nt + t) * 8 + x, x = r % 8 on even r // 8 and
+    7 - r % 8 on odd; the grid whole units of 8 x nt, other entries zero."""
+    n_rows = len(ents) // nt
+    counts = [int(ents[c * nt, 3]) - int(ents[c * nt, 0]) if ents[c * nt, 3] > ents[c * nt, 0] else 0
+              for c in range(n_rows)]
+    used = [c for c in range(n_rows) if counts[c] > 0]
+    order = sorted(used, key=lambda c: (-counts[c], c))
+    unit = 8 * nt
+    grid = -(-len(ents) // unit) * unit
+    out = np.zeros((grid, 4), np.uint32)
+    for r, c in enumerate(order):
+        slot, xr = divmod(r, 8)
+        x = 7 - xr if slot & 1 else xr
+        for t in range(nt):
+            out[(slot * nt + t) * 8 + x] = ents[c * nt + t]
+    return out
+
+
+@pytest.mark.parametrize("skewed", [False, True])
+def test_moe_prefill_stamped_matches_unstamped(dev, orc, skewed):
+    """The prefill step's grouped GEMMs run on the block maps in launch order
+    (gu_ord / dn_ord): those equal the CPU restatement of the order over the
+    reference-order maps (gu_map / dn_map), and the GEMMs over them give the
+    same bits as the public grouped GEMMs over the reference-order maps.  The
+    measurement form (stamped per workgroup) gives the same bits as
+    mh_moe_prefill; each GEMM's stamps form one prefix of workgroups, each
+    with its start before its end, and the workgroups with rows are exactly
+    the launch-ordered map's non-empty entries, with their row counts.
+    Skewed: sigmoid + bias routing whose bias sends every token to experts 5,
+    9 and 40 (1024 rows each: two map rows of 512, tied) and one other."""
+    _log(f"moe prefill stamped m=1024 skewed={skewed}")
     rng = np.random.default_rng(77)
     E, H, I, topk, m = 64, 2048, 1536, 4, 1024
     gate, up, down = moe_weights(rng, E, H, I)
@@ -246,6 +274,11 @@ def test_moe_prefill_stamped_matches_unstamped(dev, orc):
     dg, kg = dev_quant(gate)
     du, ku = dev_quant(up)
     dd, kd = dev_quant(down)
+    bias, mode = None, 1
+    if skewed:
+        b = np.zeros(E, np.float32)
+        b[[5, 9, 40]] = 1.0e4
+        bias, mode = to_dev(b), 0
     total, offs = hip.moe_prefill_workspace(m, E, topk, H, I)
     outs, wss = [], []
     stamps = zeros_dev((2 * hip.PREFILL_STAMP_WGS * hip.PREFILL_STAMPS,), np.uint64)
@@ -254,28 +287,56 @@ def test_moe_prefill_stamped_matches_unstamped(dev, orc):
         out = zeros_dev((m, H), np.uint16)
         r = to_dev(router)
         if stamped:
-            hip.moe_prefill_stamped(r, None, dg, du, dd, E, topk, x, m, out, ws, total, stamps, mode=1)
+            hip.moe_prefill_stamped(r, bias, dg, du, dd, E, topk, x, m, out, ws, total, stamps, mode=mode)
         else:
-            hip.moe_prefill(r, None, dg, du, dd, E, topk, x, m, out, ws, total, mode=1)
+            hip.moe_prefill(r, bias, dg, du, dd, E, topk, x, m, out, ws, total, mode=mode)
         outs.append(from_dev(out, np.uint16))
         wss.append(from_dev(ws, np.uint32).view(np.uint8))
     np.testing.assert_array_equal(outs[1], outs[0])
-    st = from_dev(stamps, np.uint64).reshape(2, hip.PREFILL_STAMP_WGS, hip.PREFILL_STAMPS)
-    for g, key in ((0, "gu_map"), (1, "dn_map")):
+    np.testing.assert_array_equal(wss[1], wss[0])
+
+    def region(key):
         o = offs[key]
-        nxt = min(v for v in offs.values() if v > o)
-        ents = wss[1][o:nxt].view(np.uint32).reshape(-1, 4)
-        live = set(int(i) for i in np.nonzero(ents[:, 3] > ents[:, 0])[0])
+        nxt = min([v for v in offs.values() if v > o] + [total])
+        return wss[1][o:nxt].view(np.uint32).reshape(-1, 4)
+
+    s = m * topk
+    counts = region("counts").reshape(-1)[:E]
+    if skewed:
+        assert (counts[[5, 9, 40]] == m).all() and counts.sum() == s
+    gu_nt, dn_nt = I // hip.MoeTile.GU512[1], H // hip.MoeTile.DN512[1]
+    n_rows = -(-s // hip.MoeTile.GU512[0]) + E
+    # the public GEMMs over the reference-order maps, on the step's own ids_sorted
+    base = ws.data_ptr()
+    act = zeros_dev((s, I), np.uint16)
+    ed = zeros_dev((s, H), np.uint16)
+    hip.gemm_q4_grouped_gu_act(x, base + offs["ids_sorted"], m, dg, du, act, base + offs["gu_map"],
+                               n_rows * gu_nt, s, I, hip.MoeTile.GU512)
+    hip.gemm_q4_grouped_mlx(base + offs["act"], dd, ed, base + offs["dn_map"], n_rows * dn_nt, s, H,
+                            hip.MoeTile.DN512)
+    np.testing.assert_array_equal(from_dev(act, np.uint16).reshape(-1), wss[1][offs["act"]:].view(np.uint16)[:s * I])
+    np.testing.assert_array_equal(from_dev(ed, np.uint16).reshape(-1), wss[1][offs["ed"]:].view(np.uint16)[:s * H])
+
+    st = from_dev(stamps, np.uint64).reshape(2, hip.PREFILL_STAMP_WGS, hip.PREFILL_STAMPS)
+    for g, key, nt in ((0, "gu", gu_nt), (1, "dn", dn_nt)):
+        ents = region(key + "_map")[:n_rows * nt]
+        ordm = region(key + "_ord")
+        want = _launch_order(ents, nt)
+        np.testing.assert_array_equal(ordm[:len(want)], want, err_msg=key + "_ord")
+        live = set(int(i) for i in np.nonzero(want[:, 3] > want[:, 0])[0])
         s_g = st[g]
         n_wg = int((s_g[:, 0] != 0).sum())
-        assert n_wg > 0 and (s_g[:n_wg, 0] != 0).all() and not s_g[n_wg:].any()
+        assert n_wg == len(want) and (s_g[:n_wg, 0] != 0).all() and not s_g[n_wg:].any()
         assert (s_g[:n_wg, 1] >= s_g[:n_wg, 0]).all()
-        named = s_g[:n_wg, 2] & 0xffffffff
-        rows = s_g[:n_wg, 2] >> 32
-        real = named[(named != 0xffffffff) & (rows > 0)].astype(np.int64)
-        assert sorted(real.tolist()) == sorted(live)
-        assert (rows[named != 0xffffffff] == (ents[named[named != 0xffffffff].astype(np.int64), 3] -
-                                               ents[named[named != 0xffffffff].astype(np.int64), 0])).all()
+        named = (s_g[:n_wg, 2] & 0xffffffff).astype(np.int64)
+        rows = (s_g[:n_wg, 2] >> 32).astype(np.int64)
+        assert (named == np.arange(n_wg)).all()
+        assert set(np.nonzero(rows > 0)[0].tolist()) == live
+        assert (rows == (want[:, 3].astype(np.int64) - want[:, 0].astype(np.int64)).clip(0)).all()
+        got_entry = s_g[:n_wg, 3]
+        has = rows > 0
+        assert (got_entry[~has] == 0).all()
+        assert ((got_entry[has] >= s_g[:n_wg, 0][has]) & (got_entry[has] <= s_g[:n_wg, 1][has])).all()
 
 
 @pytest.mark.parametrize("mode", [1, 0])
