@@ -391,7 +391,10 @@ def timeline_head(torch, hip, dev, gen, bits, launches, copies, batch=1):
 def timeline_config4(torch, hip, dev, gen, launches):
     """Config 4's prefill step run `launches` times back to back with the two
     grouped GEMMs stamped per workgroup (start, end, block-map entry and its
-    rows).  Per GEMM (medians over launches): the span from the first start
+    rows), replayed from a HIP graph as the bench times the step; the stamps
+    are those of the sixth replay (the first ones run while the GPU's clocks
+    ramp up: ~0.46 against ~0.41 ms per step).  Per GEMM (medians over
+    launches): the span from the first start
     to the last end, the workgroups' busy time over span x CUs (one workgroup
     per CU at a time), the time from a workgroup's start to its entry read
     (workgroups with rows), and each workgroup's duration by its entry's
@@ -406,11 +409,24 @@ def timeline_config4(torch, hip, dev, gen, launches):
     ws = torch.zeros(total, dtype=torch.uint8, device=dev)
     nst = 2 * hip.PREFILL_STAMP_WGS * hip.PREFILL_STAMPS
     stamps = torch.zeros((launches + 1, nst), dtype=torch.int64, device=dev)
-    for i in range(launches + 1):
-        g, u, d, r = sets[i % len(sets)]
-        hip.moe_prefill_stamped(r, None, g[0], u[0], d[0], E, topk, x, m, out, ws, total, stamps[i],
-                                mode=hip.ROUTE_SOFTMAX)
+
+    def run():
+        for i in range(launches + 1):
+            g, u, d, r = sets[i % len(sets)]
+            hip.moe_prefill_stamped(r, None, g[0], u[0], d[0], E, topk, x, m, out, ws, total, stamps[i],
+                                    mode=hip.ROUTE_SOFTMAX)
+
+    run()
     torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    for _ in range(5):
+        graph.replay()
+    stamps.zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    del graph
     allst = stamps.cpu().numpy().reshape(launches + 1, 2, hip.PREFILL_STAMP_WGS, hip.PREFILL_STAMPS)[1:]
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     res = {}
@@ -451,25 +467,33 @@ def bench_config4(torch, hip, dev, gen, steps, warmup):
                         mode=hip.ROUTE_SOFTMAX)
 
     ms_step = timed(torch, step, max(2, steps // 4), max(1, warmup // 4))
-    # the two grouped GEMMs alone, replayed on the workspace of the last step
-    # through the public entry points (the reference-order maps, each
-    # workgroup ranking the map rows; the step reads the launch-ordered maps)
+    # the two grouped GEMMs alone, replayed on the workspace of the last step:
+    # as the step runs them (the launch-ordered maps), and through the
+    # reference-order entry points (each workgroup ranks the map rows)
     g, u, d, r = sets[(max(2, steps // 4) + max(1, warmup // 4) - 1) % len(sets)]
     base = ws.data_ptr()
     s = m * topk
     gu_bn, dn_bn, bm = hip.MoeTile.GU512[1], hip.MoeTile.DN512[1], hip.MoeTile.GU512[0]
     m_tiles = -(-s // bm) + E
     max_gu, max_dn = m_tiles * I // gu_bn, m_tiles * H // dn_bn
+    grid_gu, grid_dn = hip.map_grid(max_gu, I // gu_bn), hip.map_grid(max_dn, H // dn_bn)
 
     def gemms(i):
+        hip.gemm_q4_grouped_gu_act_ordered(x, base + offs["ids_sorted"], m, g[0], u[0], base + offs["act"],
+                                           base + offs["gu_ord"], grid_gu, s, I, hip.MoeTile.GU512)
+        hip.gemm_q4_grouped_ordered(base + offs["act"], d[0], base + offs["ed"], base + offs["dn_ord"], grid_dn,
+                                    s, H, hip.MoeTile.DN512)
+
+    def gemms_public(i):
         hip.gemm_q4_grouped_gu_act(x, base + offs["ids_sorted"], m, g[0], u[0], base + offs["act"],
                                    base + offs["gu_map"], max_gu, s, I, hip.MoeTile.GU512)
         hip.gemm_q4_grouped_mlx(base + offs["act"], d[0], base + offs["ed"], base + offs["dn_map"],
                                 max_dn, s, H, hip.MoeTile.DN512)
 
     ms_gemm = timed(torch, gemms, max(2, steps // 4), 1)
+    ms_public = timed(torch, gemms_public, max(2, steps // 4), 1)
     del sets, ws
-    return ms_step, ms_gemm
+    return ms_step, ms_gemm, ms_public
 
 
 def measure_ceilings(torch, dev, steps, warmup):
@@ -777,10 +801,11 @@ def main() -> int:
     if args.only is not None and args.calibrate_copy_mib > 0:
         calibrate_copy(torch, dev, args.calibrate_copy_mib)
     if args.only == "config4":
-        ms4, ms4g = bench_config4(torch, hip, dev, gen, steps, warmup)
+        ms4, ms4g, ms4p = bench_config4(torch, hip, dev, gen, steps, warmup)
         print(json.dumps({"only": "config4_prefill_moe", "ms_per_step": round(ms4, 4),
                           "grouped_gemm_only_ms": round(ms4g, 4),
-                          "grouped_gemm_only_tflops": round(FLOPS_CONFIG4 / (ms4g * 1e-3) / 1e12, 2)}), flush=True)
+                          "grouped_gemm_only_tflops": round(FLOPS_CONFIG4 / (ms4g * 1e-3) / 1e12, 2),
+                          "grouped_gemm_reference_order_ms": round(ms4p, 4)}), flush=True)
         return 0
     if args.only == "config2":
         ms2 = bench_lm_head(torch, hip, dev, gen, 4, 1, steps, warmup, copies=5)
@@ -842,12 +867,13 @@ def main() -> int:
                                                       ms_per_step=round(ms5, 5),
                                                       frac_of_hbm_peak=round(v5 / HBM_PEAK_GBS, 4))
         log("config 4: prefill MoE (4096 tokens)")
-        ms4, ms4g = bench_config4(torch, hip, dev, gen, steps, warmup)
+        ms4, ms4g, ms4p = bench_config4(torch, hip, dev, gen, steps, warmup)
         others["config4_prefill_moe"] = dict(
             value=round(FLOPS_CONFIG4 / (ms4 * 1e-3) / 1e12, 2), unit="TFLOP/s",
             ms_per_step=round(ms4, 4),
             grouped_gemm_only_tflops=round(FLOPS_CONFIG4 / (ms4g * 1e-3) / 1e12, 2),
             grouped_gemm_only_ms=round(ms4g, 4),
+            grouped_gemm_reference_order_ms=round(ms4p, 4),
             frac_of_bf16_peak=round(FLOPS_CONFIG4 / (ms4g * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
 
     log("ceilings: streaming read, bf16 matrix cores, exchange latency, the vendor bf16 GEMM")

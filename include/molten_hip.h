@@ -505,6 +505,23 @@ int mh_gemm_q4_grouped_gu_act(const uint16_t* x, const uint32_t* ids_sorted, uin
                               uint32_t s_rows, uint32_t n, uint32_t bm, uint32_t bn,
                               mh_stream_t stream);
 
+/* No reference counterpart: the two grouped GEMMs above on a block map in
+ * launch order, for callers that hold one (mh_moe_prefill's workspace regions
+ * MH_PREFILL_WS_GU_ORD / DN_ORD): entry b is workgroup b's, the map holds a
+ * whole number of 8 x (n / bn) entries, all-zero entries for workgroups
+ * without one.  Each workgroup reads its entry with one load instead of
+ * ranking the map's rows.  Segment tiles only: bm 256 or 512 (rows per
+ * entry), bn 256 (down) or 128 (gate/up + SwiGLU, with ids_sorted); K a
+ * multiple of 512.  Same outputs as the reference-order calls over the same
+ * entries. */
+int mh_gemm_q4_grouped_ordered(const uint16_t* a, const mh_quant_weights* w, uint16_t* c, const uint32_t* ord,
+                               uint32_t n_entries, uint32_t s_rows, uint32_t n, uint32_t bm, uint32_t bn,
+                               mh_stream_t stream);
+int mh_gemm_q4_grouped_gu_act_ordered(const uint16_t* x, const uint32_t* ids_sorted, uint32_t x_rows,
+                                      const mh_quant_weights* gate, const mh_quant_weights* up, uint16_t* act,
+                                      const uint32_t* ord, uint32_t n_entries, uint32_t s_rows, uint32_t n,
+                                      uint32_t bm, uint32_t bn, mh_stream_t stream);
+
 /* ------------------------------------------------- prefill MoE step ---
  * src/lfm.rs:847-965 moe_prefill for m tokens on a caller workspace
  * (no allocation): router -> route -> sort -> maps -> gate/up+SwiGLU ->

@@ -773,23 +773,36 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
 // 8 XCDs in snake order (rank k -> XCD k % 8 on even rounds, 7 - k % 8 on
 // odd ones; slot k / 8), so XCD totals come out nearly equal and each XCD
 // runs its largest groups first; workgroup i (XCD i % 8, j = i / 8) takes
-// column tile j % nt of the group in slot j / nt of its XCD.  Every
-// workgroup computes the same ranking (a few hundred instructions; the
-// group weights go through the LDS, which is free before the pass starts).
-// Returns n_entries for padding workgroups.
-__device__ uint32_t balanced_entry(const GemmArgs& a, uint32_t n_entries, uint32_t nt, char* lds,
-                                   int lane, int wave) {
+// column tile j % nt of the group in slot j / nt of its XCD (mh::seg_rank_of).
+// Every workgroup ranks the groups itself (a few hundred instructions; the
+// weights and its tile's entries go through the LDS, which is free before
+// the pass starts).  Returns n_entries for padding workgroups; blk: the
+// entry (with a block map).
+__device__ uint32_t balanced_entry(const GemmArgs& a, uint32_t n_entries, uint32_t nt, char* lds, uint4& blk) {
     const uint4* blocks = a.blocks;
-    uint32_t* wts = reinterpret_cast<uint32_t*>(lds);  // [C] group weights
     __shared__ uint32_t s_group;
+    __shared__ uint4 s_blk;
     const uint32_t C = (n_entries + nt - 1u) / nt;
-    const uint32_t j = blockIdx.x / 8u;
+    const uint32_t t = (blockIdx.x / 8u) % nt;
     const uint32_t k_target = mh::seg_rank_of(blockIdx.x, nt);
-    for (uint32_t c = threadIdx.x; c < C; c += blockDim.x) {
-        if (blocks == nullptr) {  // dense: row segments of dense_bm, the last partial
+    // each group's entry of this workgroup's column tile t and its rows (for
+    // a well-formed map every entry of a group has the group's rows; ranked
+    // per tile, the (group, tile) pairs are dealt out once each either way),
+    // so the chosen entry needs no second read of the map
+    // weights padded with zeros to a multiple of 4 (read 16 bytes at a time;
+    // a zero at d >= C never ranks ahead of any group)
+    const uint32_t C4 = (C + 3u) & ~3u;
+    uint4* ents = reinterpret_cast<uint4*>(lds);                 // [C]
+    uint32_t* wts = reinterpret_cast<uint32_t*>(lds + 16u * C);  // [C4] group weights
+    for (uint32_t c = threadIdx.x; c < C4; c += blockDim.x) {
+        if (c >= C) {
+            wts[c] = 0u;
+        } else if (blocks == nullptr) {  // dense: row segments of dense_bm, the last partial
             wts[c] = min(a.dense_bm, a.s_rows - c * a.dense_bm);
         } else {
-            const uint4 e = blocks[c * nt];
+            const uint32_t i = c * nt + t;
+            const uint4 e = i < n_entries ? blocks[i] : make_uint4(0u, 0u, 0u, 0u);
+            ents[c] = e;
             wts[c] = e.x < e.w ? e.w - e.x : 0u;
         }
     }
@@ -798,23 +811,32 @@ __device__ uint32_t balanced_entry(const GemmArgs& a, uint32_t n_entries, uint32
     }
     __syncthreads();
     if (k_target < C) {
+        const uint4* w4 = reinterpret_cast<const uint4*>(wts);
         for (uint32_t c = threadIdx.x; c < C; c += blockDim.x) {
             const uint32_t w = wts[c];
             uint32_t rank = 0;
-            for (uint32_t d = 0; d < C; ++d) {
-                const uint32_t v = wts[d];
-                rank += (v > w || (v == w && d < c)) ? 1u : 0u;
+#pragma unroll 4
+            for (uint32_t d = 0; d < C4; d += 4u) {
+                const uint4 v = w4[d / 4u];
+                rank += (v.x > w || (v.x == w && d < c)) ? 1u : 0u;
+                rank += (v.y > w || (v.y == w && d + 1u < c)) ? 1u : 0u;
+                rank += (v.z > w || (v.z == w && d + 2u < c)) ? 1u : 0u;
+                rank += (v.w > w || (v.w == w && d + 3u < c)) ? 1u : 0u;
             }
             if (rank == k_target) {
                 s_group = c;
+                if (blocks != nullptr) {
+                    s_blk = ents[c];
+                }
             }
         }
     }
     __syncthreads();
     const uint32_t g = s_group;
-    (void)lane;
-    (void)wave;
-    return g == 0xffffffffu ? n_entries : g * nt + j % nt;
+    if (blocks != nullptr) {
+        blk = s_blk;  // (a static variable: the staging reuses the dynamic LDS)
+    }
+    return g == 0xffffffffu ? n_entries : g * nt + t;
 }
 
 // Workgroup stamps of the stamped k_seg (thread 0): the 100 MHz constant
@@ -842,17 +864,17 @@ void k_seg(GemmArgs a, uint32_t n_entries) {
     const uint32_t nt = a.n / (kSegWaves * NBW * 32u);
     // a launch-ordered map names this workgroup's entry directly; otherwise
     // the groups are ranked here (mh::seg_rank_of)
-    const uint32_t ent = a.ordered ? static_cast<uint32_t>(blockIdx.x) : balanced_entry(a, n_entries, nt, lds, lane, wave);
+    uint4 blk;
+    const uint32_t ent = a.ordered ? static_cast<uint32_t>(blockIdx.x) : balanced_entry(a, n_entries, nt, lds, blk);
     if (ent >= n_entries) {
         seg_stamp<ST>(a, 2, 0xffffffffull);
         seg_stamp<ST>(a, 1, wall_clock64());
         return;
     }
-    uint4 blk;
     if (a.blocks == nullptr) {  // dense: entry = (row segment, column tile)
         const uint32_t mr = (ent / nt) * a.dense_bm, nc = (ent % nt) * (kSegWaves * NBW * 32u);
         blk = make_uint4(mr, nc, nc, min(mr + a.dense_bm, a.s_rows));
-    } else {
+    } else if (a.ordered) {
         blk = a.blocks[ent];
     }
     const uint32_t m0 = blk.x, brow = blk.y, n0 = blk.z, m_end = blk.w;
@@ -894,6 +916,10 @@ template <int RBMAX, int NS, int NBW, int NMAT, bool GATHER, int EPI>
 int launch_seg(const GemmArgs& a, uint32_t n_blocks, hipStream_t s) {
     constexpr size_t lds = SegLayout<RBMAX, NBW, NMAT, NS>::LDS;
     static_assert(lds <= 160 * 1024, "LDS per workgroup");
+    // the ranking's entries and weights (balanced_entry) fit the LDS
+    const size_t groups = n_blocks / (a.n / (kSegWaves * NBW * 32u)) + 4u;
+    MH_ENSURE(a.ordered || groups * 20u <= lds, MH_ERR_UNSUPPORTED, "k_seg: %zu map rows exceed the LDS ranking",
+              groups);
     if (a.stamps != nullptr) {
         const uint32_t grid = grid_for_map(n_blocks, a.n / (kSegWaves * NBW * 32u));
         MH_ENSURE(grid <= MH_PREFILL_STAMP_WGS, MH_ERR_UNSUPPORTED, "k_seg: %u workgroups exceed the stamp buffer",
@@ -1116,6 +1142,41 @@ int mh_gemm_q4_grouped_gu_act(const uint16_t* x, const uint32_t* ids_sorted, uin
     const hipStream_t s = mh::as_stream(stream);
     return ids_sorted ? dispatch<true, EPI_SWIGLU>(g, n_blocks, bm, bn, s)
                       : dispatch<false, EPI_SWIGLU>(g, n_blocks, bm, bn, s);
+}
+
+// The launch-ordered forms: entry b of the map is workgroup b's (a whole
+// number of 8 x (n / bn) units), segment tiles only.
+static int ordered_checks(const char* op, uint32_t n_entries, uint32_t n, uint32_t bn) {
+    MH_ENSURE(n_entries % (8u * (n / bn)) == 0u, MH_ERR_INVALID,
+              "%s: a launch-ordered map holds whole units of 8 x %u entries, not %u", op, n / bn, n_entries);
+    return MH_OK;
+}
+
+int mh_gemm_q4_grouped_ordered(const uint16_t* a, const mh_quant_weights* w, uint16_t* c, const uint32_t* ord,
+                               uint32_t n_entries, uint32_t s_rows, uint32_t n, uint32_t bm, uint32_t bn,
+                               mh_stream_t stream) {
+    const char* op = "mh_gemm_q4_grouped_ordered";
+    MH_TRY(gemm_checks(op, a, w, c, ord, n_entries, s_rows, n));
+    MH_ENSURE(bn == 256u && n % bn == 0u, MH_ERR_UNSUPPORTED, "%s: tile width %u (256 only)", op, bn);
+    MH_TRY(ordered_checks(op, n_entries, n, bn));
+    return mh::gemm_grouped_seg(a, w, c, ord, n_entries, s_rows, n, bm, bn, true, nullptr, mh::as_stream(stream));
+}
+
+int mh_gemm_q4_grouped_gu_act_ordered(const uint16_t* x, const uint32_t* ids_sorted, uint32_t x_rows,
+                                      const mh_quant_weights* gate, const mh_quant_weights* up, uint16_t* act,
+                                      const uint32_t* ord, uint32_t n_entries, uint32_t s_rows, uint32_t n,
+                                      uint32_t bm, uint32_t bn, mh_stream_t stream) {
+    const char* op = "mh_gemm_q4_grouped_gu_act_ordered";
+    MH_TRY(gemm_checks(op, x, gate, act, ord, n_entries, s_rows, n));
+    MH_TRY(mh::check_quant(up, op));
+    MH_ENSURE(ids_sorted != nullptr && x_rows > 0, MH_ERR_INVALID, "%s: needs ids_sorted and x rows", op);
+    MH_ENSURE(up->out_features == gate->out_features && up->in_features == gate->in_features &&
+                  up->bits == 4 && up->group_size == 64,
+              MH_ERR_INVALID, "%s: gate/up shapes differ", op);
+    MH_ENSURE(bn == 128u && n % bn == 0u, MH_ERR_UNSUPPORTED, "%s: tile width %u (128 only)", op, bn);
+    MH_TRY(ordered_checks(op, n_entries, n, bn));
+    return mh::gemm_gu_act_seg(x, ids_sorted, x_rows, gate, up, act, ord, n_entries, s_rows, n, bm, bn, true,
+                               nullptr, mh::as_stream(stream));
 }
 
 }  // extern "C"

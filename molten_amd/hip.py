@@ -135,6 +135,9 @@ _SIGNATURES = {
     "mh_gemm_q4_grouped_gu": [_vp, _qw, _qw, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp],
     "mh_gemm_q4_grouped_gu_act": [_vp, _vp, _u32, _qw, _qw, _vp, _vp, _u32, _u32, _u32, _u32,
                                   _u32, _vp],
+    "mh_gemm_q4_grouped_ordered": [_vp, _qw, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp],
+    "mh_gemm_q4_grouped_gu_act_ordered": [_vp, _vp, _u32, _qw, _qw, _vp, _vp, _u32, _u32, _u32, _u32,
+                                          _u32, _vp],
     "mh_moe_prefill_workspace": [_u32, _u32, _u32, _u32, _u32, ctypes.POINTER(_sz)],
     "mh_moe_prefill": [_vp, _i32, _vp, _i32, _f32, _qw, _qw, _qw, _u32, _u32, _vp, _u32, _vp,
                        _vp, _sz, _vp],
@@ -662,6 +665,32 @@ def gemm_q4_grouped_gu_act(x, ids_sorted, x_rows: int, gate: QuantWeights, up: Q
                                            _qref(up), _ptr(act), _ptr(blocks), n_blocks, s_rows,
                                            n, tile[0], tile[1], _stream(stream)),
           "gemm_q4_grouped_gu_act")
+
+
+def map_grid(n_entries: int, nt: int) -> int:
+    """Workgroups of a grouped-GEMM launch over n_entries map entries of nt
+    column tiles each: whole units of 8 x nt (the entries of a launch-ordered
+    map)."""
+    unit = 8 * nt
+    return -(-n_entries // unit) * unit
+
+
+def gemm_q4_grouped_ordered(a, w: QuantWeights, c, ord_map, n_entries: int, s_rows: int, n: int,
+                            tile=MoeTile.DN512, stream=None) -> None:
+    """The grouped GEMM over a launch-ordered block map (no reference
+    counterpart): entry b is workgroup b's; n_entries = map_grid(...)."""
+    check(load().mh_gemm_q4_grouped_ordered(_ptr(a), _qref(w), _ptr(c), _ptr(ord_map), n_entries, s_rows, n,
+                                            tile[0], tile[1], _stream(stream)), "gemm_q4_grouped_ordered")
+
+
+def gemm_q4_grouped_gu_act_ordered(x, ids_sorted, x_rows: int, gate: QuantWeights, up: QuantWeights, act,
+                                   ord_map, n_entries: int, s_rows: int, n: int, tile=MoeTile.GU512,
+                                   stream=None) -> None:
+    """gate/up + SwiGLU with the row gather, over a launch-ordered block map
+    (no reference counterpart)."""
+    check(load().mh_gemm_q4_grouped_gu_act_ordered(_ptr(x), _ptr(ids_sorted), x_rows, _qref(gate), _qref(up),
+                                                   _ptr(act), _ptr(ord_map), n_entries, s_rows, n, tile[0],
+                                                   tile[1], _stream(stream)), "gemm_q4_grouped_gu_act_ordered")
 
 
 PREFILL_WS_REGIONS = ["logits", "ids", "gw", "counts", "offsets", "ids_sorted", "slotpos",

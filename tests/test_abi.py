@@ -222,6 +222,28 @@ def test_grouped_gemm_rejects_operands_past_4_gib():
     assert ei.value.code == hip.MH_ERR_UNSUPPORTED
 
 
+def test_ordered_grouped_gemm_arguments():
+    """The launch-ordered grouped GEMMs take whole 8 x (n / bn) units of
+    entries, segment tile widths only and (gate/up) the row gather; all
+    refused on the host."""
+    w = _qw(out_features=512)
+    with pytest.raises(hip.MoltenError, match="whole units") as ei:  # nt = 2: units of 16
+        hip.gemm_q4_grouped_ordered(0x4000, w, 0x6000, 0x7000, 24, 64, 512, hip.MoeTile.DN512, stream=0)
+    assert ei.value.code == hip.MH_ERR_INVALID
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.gemm_q4_grouped_ordered(0x4000, w, 0x6000, 0x7000, 32, 64, 512, (512, 128), stream=0)
+    assert ei.value.code == hip.MH_ERR_UNSUPPORTED
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.gemm_q4_grouped_gu_act_ordered(0x4000, None, 64, w, w, 0x6000, 0x7000, 32, 64, 256,
+                                           hip.MoeTile.GU512, stream=0)
+    assert ei.value.code == hip.MH_ERR_INVALID
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.gemm_q4_grouped_gu_act_ordered(0x4000, 0x5000, 64, w, w, 0x6000, 0x7000, 32, 64, 256,
+                                           (512, 256), stream=0)
+    assert ei.value.code == hip.MH_ERR_UNSUPPORTED
+    assert hip.map_grid(1152, 12) == 1152 and hip.map_grid(1153, 12) == 1248 and hip.map_grid(1, 8) == 64
+
+
 def test_sample_draw_arguments():
     p = hip.sample_params(1.0, 1, 0, top_k=40)
     with pytest.raises(hip.MoltenError, match="workspace holds 16 bytes"):

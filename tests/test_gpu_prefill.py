@@ -262,7 +262,8 @@ def test_moe_prefill_stamped_matches_unstamped(dev, orc, skewed):
     measurement form (stamped per workgroup) gives the same bits as
     mh_moe_prefill; each GEMM's stamps form one prefix of workgroups, each
     with its start before its end, and the workgroups with rows are exactly
-    the launch-ordered map's non-empty entries, with their row counts.
+    the launch-ordered map's non-empty entries, with their row counts.  The
+    launch-ordered grouped-GEMM entry points give the same bits too.
     Skewed: sigmoid + bias routing whose bias sends every token to experts 5,
     9 and 40 (1024 rows each: two map rows of 512, tied) and one other."""
     _log(f"moe prefill stamped m=1024 skewed={skewed}")
@@ -314,6 +315,15 @@ def test_moe_prefill_stamped_matches_unstamped(dev, orc, skewed):
                                n_rows * gu_nt, s, I, hip.MoeTile.GU512)
     hip.gemm_q4_grouped_mlx(base + offs["act"], dd, ed, base + offs["dn_map"], n_rows * dn_nt, s, H,
                             hip.MoeTile.DN512)
+    np.testing.assert_array_equal(from_dev(act, np.uint16).reshape(-1), wss[1][offs["act"]:].view(np.uint16)[:s * I])
+    np.testing.assert_array_equal(from_dev(ed, np.uint16).reshape(-1), wss[1][offs["ed"]:].view(np.uint16)[:s * H])
+    # the launch-ordered entry points over the workspace's launch-ordered maps
+    act.zero_()
+    ed.zero_()
+    hip.gemm_q4_grouped_gu_act_ordered(x, base + offs["ids_sorted"], m, dg, du, act, base + offs["gu_ord"],
+                                       hip.map_grid(n_rows * gu_nt, gu_nt), s, I, hip.MoeTile.GU512)
+    hip.gemm_q4_grouped_ordered(base + offs["act"], dd, ed, base + offs["dn_ord"], hip.map_grid(n_rows * dn_nt, dn_nt),
+                                s, H, hip.MoeTile.DN512)
     np.testing.assert_array_equal(from_dev(act, np.uint16).reshape(-1), wss[1][offs["act"]:].view(np.uint16)[:s * I])
     np.testing.assert_array_equal(from_dev(ed, np.uint16).reshape(-1), wss[1][offs["ed"]:].view(np.uint16)[:s * H])
 
