@@ -1093,15 +1093,17 @@ int mh_gemm_q4_dense(const uint16_t* a, uint32_t m, const mh_quant_weights* w, u
     const uint32_t n = w->out_features;
     GemmArgs g = make_args(a, nullptr, m, w, nullptr, c, nullptr, nullptr, m, n);
     const hipStream_t s = mh::as_stream(stream);
-    // 256 x 256 segment entries when they fill the chip (>= one per CU) and
+    // segment entries of 256 x 256 when they fill the chip (>= one per CU),
+    // else of 128 x 256 when those do (one 4-row-block pass each), provided
     // the segment kernel's 32-bit offsets hold; else 128 x 256 tiles
     const uint32_t segs = (m + 255u) / 256u * (n / 256u);
-    if (n % 256 == 0 && segs >= 256u && w->in_features % 512u == 0 &&
+    const uint32_t segs128 = (m + 127u) / 128u * (n / 256u);
+    if (n % 256 == 0 && segs128 >= 256u && w->in_features % 512u == 0 &&
         static_cast<uint64_t>(m) * w->in_features * 2u < (1ull << 32) &&
         static_cast<uint64_t>(n) * w->in_features / 2u < (1ull << 32) &&
         static_cast<uint64_t>(m) * n * 2u < (1ull << 32) && mh::aligned(c, 16)) {
-        g.dense_bm = 256;
-        return launch_seg<kSegRBMax, kSegStages, 2, 1, false, EPI_STORE>(g, segs, s);
+        g.dense_bm = segs >= 256u ? 256u : 128u;
+        return launch_seg<kSegRBMax, kSegStages, 2, 1, false, EPI_STORE>(g, segs >= 256u ? segs : segs128, s);
     }
     const uint32_t mt = (m + 127u) / 128u;
     if (n % 256 == 0) {

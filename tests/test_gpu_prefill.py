@@ -468,13 +468,15 @@ def test_dense_gemm_one_hot_is_exact_dequant(dev, orc):
     np.testing.assert_array_equal(from_dev(c, np.uint16), orc.dequant_bf16(w)[:, cols].T)
 
 
-def test_dense_gemm_segment_path(dev, orc):
-    """A shape with >= 256 segment entries of 256 x 256 (the segment kernel in
-    dense mode): one-hot rows reproduce the dequantized columns exactly over
-    every tile, and the first and the last (partial) row segments match the
-    oracle within tolerance."""
+@pytest.mark.parametrize("m,n,k", [(1100, 13312, 512), (1100, 7936, 512)])
+def test_dense_gemm_segment_path(dev, orc, m, n, k):
+    """Shapes with >= 256 segment entries of 256 x 256 (13312 columns: 5 row
+    segments, the last of 76 rows, x 52 column tiles) or, below that, of
+    128 x 256 (7936 columns: 9 row segments, the last of 76 rows, x 31): the
+    segment kernel in dense mode.  One-hot rows reproduce the dequantized
+    columns exactly over every tile, and the first and the last (partial)
+    row segments match the oracle within tolerance."""
     rng = np.random.default_rng(11)
-    m, n, k = 1100, 13312, 512  # 5 row segments (the last 76 rows) x 52 column tiles
     w = layout.synth_quant(rng, n, k, 4)
     wd, keep = dev_quant(w)
     cols = rng.integers(0, k, m)
@@ -491,4 +493,4 @@ def test_dense_gemm_segment_path(dev, orc):
     blocks = np.array(ents, np.uint32).reshape(-1, 4)
     want = orc.gemm_q4_grouped(a, w, blocks, len(ents), n, 64)
     rows = np.r_[0:256, 1024:m]
-    assert_close(got[rows], want[rows], "dense segment path")
+    assert_close(got[rows], want[rows], f"dense segment path {m}x{n}x{k}")
