@@ -328,7 +328,9 @@ def timeline_head(torch, hip, dev, gen, bits, launches, copies, batch=1):
     first workgroup finished (the first generation) and the time of the last
     of them, the time of the last start, the last workgroup key published,
     the collector's end, and the collector's end minus the last publication
-    (its detection)."""
+    (its detection); at batch 8 the last summary published, the finisher's
+    detection and its collection + recomputes, the end, and the rows the
+    finisher recomputed in chunk order per batch row (median, max)."""
     import numpy as np
 
     n, k = 65536, 2048
@@ -370,7 +372,9 @@ def timeline_head(torch, hip, dev, gen, bits, launches, copies, batch=1):
             last_pub = rel[:, 3][st[:, 3] != 0].max()
             words = rel[:, 4][st[:, 4] != 0].max()
             end = rel[:, 5][st[:, 5] != 0].max()
-            scal.append([len(starts), starts.max(), last_pub, words - last_pub, end - words, end])
+            cand = st[st[:, 5] != 0, 6].astype(np.float64)  # the finisher waves' recomputed rows
+            scal.append([len(starts), starts.max(), last_pub, words - last_pub, end - words, end,
+                         float(np.median(cand)), float(cand.max())])
     med = np.median(np.array(per), axis=0)
     ms = np.median(np.array(scal), axis=0)
     del ws
@@ -383,7 +387,8 @@ def timeline_head(torch, hip, dev, gen, bits, launches, copies, batch=1):
         out.update(waves_started=int(ms[0]), last_start_us=round(float(ms[1]), 2),
                    last_summary_published_us=round(float(ms[2]), 2),
                    finisher_detection_us=round(float(ms[3]), 2), finisher_collect_recompute_us=round(float(ms[4]), 2),
-                   end_us=round(float(ms[5]), 2))
+                   end_us=round(float(ms[5]), 2), recomputed_rows_median=float(ms[6]),
+                   recomputed_rows_max=float(ms[7]))
     out.update(launches=launches)
     return out
 

@@ -206,7 +206,8 @@ int mh_gemv_quant_argmax(const mh_quant_weights* w, const uint16_t* x, uint16_t*
  *   batch 8 (the matrix-core kernel: 256 workgroups of 8 waves): wave start,
  *   x staged, main loop done, batch row b's summary published (waves b < 8),
  *   then in the finisher (the last workgroup) wave b: every workgroup's words
- *   read, row b's id written.
+ *   read, row b's id written, and in word 6 not a time but the number of
+ *   rows whose chunk-order values it formed for row b (0: one candidate).
  * Outputs are mh_gemv_quant_argmax's. */
 #define MH_GEMV_STAMP_WAVES 8192u
 #define MH_GEMV_STAMPS 8u

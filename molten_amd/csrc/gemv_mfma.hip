@@ -70,6 +70,7 @@ enum MfmaStamp {
     MS_SUMMARY = 3,    // waves b < B: batch row b's summary published (or kept, the finisher)
     MS_WORDS = 4,      // finisher wave b: every workgroup's words read
     MS_ID = 5,         // finisher wave b: batch row b's id written
+    MS_CAND = 6,       // finisher wave b: the rows recomputed in chunk order (a count)
     MS_XCC = 7         // the XCD the workgroup ran on
 };
 static_assert(MS_XCC + 1 == MH_GEMV_STAMPS, "stamp words");
@@ -755,6 +756,12 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         }
     }
     mfma_stamp<ST>(a, gw, lane, MS_ID);
+    if constexpr (ST) {
+        if (lane == 0) {
+            a.stamps[static_cast<size_t>(gw) * MH_GEMV_STAMPS + MS_CAND] =
+                (!all_rows && nc == 1u) ? 0u : (all_rows ? a.n : nc);
+        }
+    }
     // clear the words for the next launch (last: no later load waits on them)
 #pragma unroll
     for (int j = 0; j < kWords; ++j) {

@@ -424,7 +424,8 @@ def test_stamped_batch8_head_matches_oracle(dev, orc, bits):
     oracle's, logits within the kernel's tolerance, the scratch re-zeroed and
     counted; every wave of the 256 x 8 launch stamps its start, x staging and
     main loop in order, waves 0..7 of every workgroup their summary, and only
-    the last workgroup's waves 0..7 the finisher's two phases."""
+    the last workgroup's waves 0..7 the finisher's two phases and their count
+    of recomputed rows."""
     _log(f"stamped batch-8 head bits={bits}")
     rng = np.random.default_rng(4343 + bits)
     n, k, batch = 8192, 2048, 8
@@ -452,6 +453,8 @@ def test_stamped_batch8_head_matches_oracle(dev, orc, bits):
     assert (st[:, 4:6] > 0).all(axis=1).tolist() == last.tolist()
     assert (st[last, 5] >= st[last, 4]).all() and (st[last, 4] >= st[last, 3]).all()
     assert (st[:, 7] < 16).all()
+    # word 6: the finisher waves' count of rows recomputed in chunk order
+    assert not st[~last, 6].any() and (st[last, 6] <= n).all()
 
 
 def _argmax_case(dev, orc, h, x, batch):
