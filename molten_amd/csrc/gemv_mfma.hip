@@ -412,29 +412,49 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         a.slots != nullptr
             ? __hip_atomic_load(a.slots + static_cast<size_t>(B) * kArgSlots, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
             : 0ull;
-    // ---- x to LDS in operand order (columns >= B zero), clamped addresses,
-    // no branches
-    constexpr int kXPer = kMaxG * 8 * 16 / kThreads;
-    mh::u32x4 xv[kXPer];
+    // ---- x to LDS in operand order (columns >= B zero), clamped addresses.
+    // Waves 0..3 stage x (each thread B of its 256 x B live entries, then
+    // 16 - B zero entries; groups >= G hold group 0's x and are never read)
+    // and issue their first stages' code loads once x has arrived: issued
+    // after a wave's code loads, its x would wait behind tens of MB of HBM
+    // reads in flight across the chip.  Waves 4..7 issue their first stages
+    // at once and take no part in staging x.
+    static_assert(kWaves == 8 && kMaxG * 8 * 16 == (kThreads / 2) * 16, "x staged by four waves, 16 entries each");
+    const bool xwave = wave < kWaves / 2;
+    if (!xwave) {
 #pragma unroll
-    for (int j = 0; j < kXPer; ++j) {
-        const uint32_t u = threadIdx.x + j * kThreads;
-        const uint32_t nb = u % 16u, qq = (u / 16u) % 4u, t = (u / 64u) % 2u, g = u / 128u;
-        const uint32_t nc = nb < static_cast<uint32_t>(B) ? nb : 0u, gcl = g < G ? g : 0u;
-        const uint4 v = *reinterpret_cast<const uint4*>(a.x + static_cast<size_t>(nc) * K + 64u * gcl + 16u * qq + 8u * t);
-        xv[j] = mh::u32x4{v.x, v.y, v.z, v.w};
-    }
-    // (every entry is stored, groups >= G included: those hold group 0's x and
-    // are never read).  The first stages' code loads go out only after x has
-    // arrived: queued behind them, x would wait for tens of MB of HBM reads
-    // in flight across the chip.
+        for (int u = 0; u < kDepth - 1; ++u) {
+            issue(tile_c(u), stage_c(u), pbuf[u], svbuf[u], bvbuf[u]);
+        }
+    } else {
+        const uint32_t tx = threadIdx.x;  // 0 .. 255
+        mh::u32x4 xv[B];
 #pragma unroll
-    for (int j = 0; j < kXPer; ++j) {
-        const uint32_t u = threadIdx.x + j * kThreads;
-        const bool live_col = u % 16u < static_cast<uint32_t>(B);
-        xl[u] = live_col ? xv[j] : mh::u32x4{0u, 0u, 0u, 0u};
+        for (int j = 0; j < B; ++j) {
+            const uint32_t L = tx + j * (kThreads / 2u);
+            const uint32_t nb = L % static_cast<uint32_t>(B), rest = L / static_cast<uint32_t>(B);
+            const uint32_t qq = rest % 4u, t = (rest / 4u) % 2u, g = rest / 8u;
+            const uint32_t gcl = g < G ? g : 0u;
+            const uint4 v = *reinterpret_cast<const uint4*>(a.x + static_cast<size_t>(nb) * K + 64u * gcl + 16u * qq + 8u * t);
+            xv[j] = mh::u32x4{v.x, v.y, v.z, v.w};
+        }
+#pragma unroll
+        for (int j = 0; j < B; ++j) {
+            const uint32_t L = tx + j * (kThreads / 2u);
+            xl[(L / static_cast<uint32_t>(B)) * 16u + L % static_cast<uint32_t>(B)] = xv[j];
+        }
+        constexpr uint32_t kDead = 16u - static_cast<uint32_t>(B);
+#pragma unroll
+        for (uint32_t j = 0; j < kDead; ++j) {
+            const uint32_t D = tx + j * (kThreads / 2u);
+            xl[(D / kDead) * 16u + static_cast<uint32_t>(B) + D % kDead] = mh::u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < kDepth - 1; ++u) {
+            issue(tile_c(u), stage_c(u), pbuf[u], svbuf[u], bvbuf[u]);
+        }
     }
-    // (uniform, taken now that x is in: no later wait for the count)
+    // (uniform; its load went out before every other, so no later wait)
     const unsigned long long launches =
         (static_cast<unsigned long long>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(launches_v >> 32))) << 32) |
         __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(launches_v));
@@ -442,10 +462,6 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
     // finisher)
     const bool poisoned = (launches >> 63) != 0ull;
     const uint32_t tag = static_cast<uint32_t>((launches & ~(1ull << 63)) % 255ull) + 1u;
-#pragma unroll
-    for (int u = 0; u < kDepth - 1; ++u) {
-        issue(tile_c(u), stage_c(u), pbuf[u], svbuf[u], bvbuf[u]);
-    }
     __syncthreads();
     static_assert(kMaxG * 16 == kThreads, "one group sum per thread");
     {
