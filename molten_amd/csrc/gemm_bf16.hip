@@ -6,9 +6,9 @@
 // GEMMs) and src/kernels/quant.rs:126-146 gemm_quant_bf16_nt, so that
 // src/lfm.rs:649-675 `project` keeps all three of its branches.
 //
-// Work split: 128 x 128 output tiles, one workgroup of 4 waves each (a 2 x 2
-// grid of 64 x 64 wave tiles, four v_mfma_f32_32x32x16_bf16 accumulators per
-// wave).  K advances 64 at a time through a 3-slot LDS ring filled by
+// Work split: 256 x 128 output tiles (128 x 128 when the larger ones give
+// fewer tiles than CUs), one workgroup of 4 waves each (a 2 x 2 grid of
+// 128 x 64 or 64 x 64 wave tiles, v_mfma_f32_32x32x16_bf16 accumulators).  K advances 64 at a time through a 3-slot LDS ring filled by
 // direct-to-LDS 16-byte loads (global_load_lds_dwordx4): the A and B tiles
 // are both rows of K, so both are staged the same way, 16-byte chunks
 // XOR-swizzled by row so that the fragment reads are bank-conflict free.
@@ -28,14 +28,27 @@
 
 namespace {
 
-constexpr int kTile = 128;
+constexpr int kTileN = 128;  // output columns per tile
 constexpr int kBK = 64;
 constexpr int kThreads = 256;
 constexpr int kStages = 3;
-constexpr uint32_t kTileBytes = kTile * kBK * 2;  // one operand's 128 x 64 bf16 block
-constexpr uint32_t kStageBytes = 2 * kTileBytes;
-constexpr uint32_t kLds = kStages * kStageBytes;  // 96 KB
-constexpr int kStageOps = 8;                      // direct-to-LDS loads per wave per stage
+
+// Tiles of TM (128 or 256) rows x 128 columns: the 4 waves form a 2 x 2 grid
+// of (TM / 2) x 64 wave tiles, RB = TM / 64 row blocks of 32 by two column
+// blocks of 32 each.  The larger tile reads 0.75 KB of LDS fragments per
+// MFMA instead of 1 KB.
+template <int TM>
+struct NtShape {
+    static constexpr int RB = TM / 64;                          // 32-row blocks per wave
+    static constexpr uint32_t A_BYTES = TM * kBK * 2;           // A's TM x 64 bf16 block
+    static constexpr uint32_t B_BYTES = kTileN * kBK * 2;       // B's 128 x 64 bf16 block
+    static constexpr uint32_t STAGE = A_BYTES + B_BYTES;
+    static constexpr uint32_t LDS = kStages * STAGE;            // 96 KB (TM 128), 144 KB (TM 256)
+    static constexpr int QA = TM / 32, QB = kTileN / 32;        // 1 KB loads per wave per stage
+    static constexpr int OPS = QA + QB;
+    static constexpr int HALF_READS = 2 * (RB + 2);             // fragment reads of steps 0-1
+    static_assert(HALF_READS <= 15, "lgkmcnt field");
+};
 
 struct NtArgs {
     const uint16_t* a;  // [m, k]
@@ -45,13 +58,16 @@ struct NtArgs {
     uint32_t tiles_n, tiles, per_xcd;
 };
 
+template <int TM>
 __global__ __launch_bounds__(kThreads, 1) void k_gemm_nt(NtArgs p) {
+    using S = NtShape<TM>;
+    constexpr int RB = S::RB;
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const uint32_t t = (blockIdx.x % 8u) * p.per_xcd + blockIdx.x / 8u;
     if (t >= p.tiles) {
         return;
     }
-    const uint32_t m0 = (t / p.tiles_n) * kTile, n0 = (t % p.tiles_n) * kTile;
+    const uint32_t m0 = (t / p.tiles_n) * TM, n0 = (t % p.tiles_n) * kTileN;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int i32 = lane & 31, h = lane >> 5;
@@ -60,46 +76,54 @@ __global__ __launch_bounds__(kThreads, 1) void k_gemm_nt(NtArgs p) {
     const mh::gbytes abase = mh::uniform_ptr(p.a);
     const mh::gbytes bbase = mh::uniform_ptr(p.b);
 
-    // this lane's four A and four B loads per stage: row r of the tile,
-    // 16-byte chunk (lane & 7) of its LDS row, holding global chunk
-    // (lane & 7) ^ (r & 7)
-    uint32_t aoff[4], boff[4];
+    // this lane's A and B loads per stage: row r of the block, 16-byte chunk
+    // (lane & 7) of its LDS row, holding global chunk (lane & 7) ^ (r & 7)
+    uint32_t aoff[S::QA], boff[S::QB];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t r = 8u * static_cast<uint32_t>(wave * 4 + q) + static_cast<uint32_t>(lane >> 3);
+    for (int q = 0; q < S::QA; ++q) {
+        const uint32_t r = 8u * static_cast<uint32_t>(wave * S::QA + q) + static_cast<uint32_t>(lane >> 3);
         const uint32_t chunk = static_cast<uint32_t>(lane & 7) ^ (r & 7u);
         aoff[q] = min(m0 + r, p.m - 1u) * K * 2u + chunk * 16u;
+    }
+#pragma unroll
+    for (int q = 0; q < S::QB; ++q) {
+        const uint32_t r = 8u * static_cast<uint32_t>(wave * S::QB + q) + static_cast<uint32_t>(lane >> 3);
+        const uint32_t chunk = static_cast<uint32_t>(lane & 7) ^ (r & 7u);
         boff[q] = min(n0 + r, p.n - 1u) * K * 2u + chunk * 16u;
     }
     auto issue = [&](uint32_t kb, int slot) {
-        const uint32_t base = lds0 + static_cast<uint32_t>(slot) * kStageBytes;
+        const uint32_t base = lds0 + static_cast<uint32_t>(slot) * S::STAGE;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            mh::dma16(abase + aoff[q] + kb * 128u, base + static_cast<uint32_t>(wave * 4 + q) * 1024u);
+        for (int q = 0; q < S::QA; ++q) {
+            mh::dma16(abase + aoff[q] + kb * 128u, base + static_cast<uint32_t>(wave * S::QA + q) * 1024u);
         }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            mh::dma16(bbase + boff[q] + kb * 128u, base + kTileBytes + static_cast<uint32_t>(wave * 4 + q) * 1024u);
+        for (int q = 0; q < S::QB; ++q) {
+            mh::dma16(bbase + boff[q] + kb * 128u, base + S::A_BYTES + static_cast<uint32_t>(wave * S::QB + q) * 1024u);
         }
     };
 
     // fragment addresses inside a stage: row (col) of the wave's block, chunk 4h + j
-    const uint32_t wr = static_cast<uint32_t>(wave >> 1) * 64u, wc = static_cast<uint32_t>(wave & 1) * 64u;
-    uint32_t afr[2][4], bfr[2][4];
+    const uint32_t wr = static_cast<uint32_t>(wave >> 1) * (TM / 2u), wc = static_cast<uint32_t>(wave & 1) * 64u;
+    uint32_t afr[RB][4], bfr[2][4];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t c = static_cast<uint32_t>(4 * h + j);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t c = static_cast<uint32_t>(4 * h + j);
+        for (int rb = 0; rb < RB; ++rb) {
             const uint32_t ra = wr + rb * 32u + static_cast<uint32_t>(i32);
-            const uint32_t rbn = wc + rb * 32u + static_cast<uint32_t>(i32);
             afr[rb][j] = ra * 128u + ((c ^ (ra & 7u)) * 16u);
-            bfr[rb][j] = kTileBytes + rbn * 128u + ((c ^ (rbn & 7u)) * 16u);
         }
-
-    mh::f32x16_t acc[2][2];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+        for (int cb = 0; cb < 2; ++cb) {
+            const uint32_t rbn = wc + cb * 32u + static_cast<uint32_t>(i32);
+            bfr[cb][j] = S::A_BYTES + rbn * 128u + ((c ^ (rbn & 7u)) * 16u);
+        }
+    }
+
+    mh::f32x16_t acc[RB][2];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
@@ -122,7 +146,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_gemm_nt(NtArgs p) {
             // in flight); the barrier publishes every wave's and frees the
             // slot the next issue overwrites
             if (kb + 1 < nkb) {
-                mh::wait_vmcnt<kStageOps>();
+                mh::wait_vmcnt<S::OPS>();
             } else {
                 mh::wait_vmcnt<0>();
             }
@@ -130,34 +154,51 @@ __global__ __launch_bounds__(kThreads, 1) void k_gemm_nt(NtArgs p) {
             if (kb + kStages - 1 < nkb) {
                 issue(kb + kStages - 1, (u + kStages - 1) % kStages);
             }
-            const uint32_t base = lds0 + static_cast<uint32_t>(u) * kStageBytes;
-            uint4 av[4][2], bv[4][2];
+            const uint32_t base = lds0 + static_cast<uint32_t>(u) * S::STAGE;
+            // two halves of the stage (steps 0-1, 2-3): the second half's
+            // fragment reads are in flight under the first half's MFMAs
+            uint4 av[2][2][RB], bv[2][2][2];  // [half][step][rb / cb]
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-                for (int r = 0; r < 2; ++r) {
-                    av[j][r] = mh::lds_read16(base + afr[r][j]);
-                    bv[j][r] = mh::lds_read16(base + bfr[r][j]);
+                for (int jj = 0; jj < 2; ++jj) {
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb) {
+                        av[hf][jj][rb] = mh::lds_read16(base + afr[rb][2 * hf + jj]);
+                    }
+#pragma unroll
+                    for (int cb = 0; cb < 2; ++cb) {
+                        bv[hf][jj][cb] = mh::lds_read16(base + bfr[cb][2 * hf + jj]);
+                    }
                 }
-            // the wait is tied to the fragment registers, so that no MFMA
-            // reading them is scheduled above it
-            mh::lgkm_wait<0>(reinterpret_cast<uint4(&)[8]>(av));
-            mh::lgkm_wait<0>(reinterpret_cast<uint4(&)[8]>(bv));
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int hf = 0; hf < 2; ++hf) {
+                // the waits are tied to the fragment registers, so that no
+                // MFMA reading them is scheduled above them (hf 0: the
+                // second half's reads may still be in flight)
+                if (hf == 0) {
+                    mh::lgkm_wait<S::HALF_READS>(reinterpret_cast<uint4(&)[2 * RB]>(av[0]));
+                    mh::lgkm_wait<S::HALF_READS>(reinterpret_cast<uint4(&)[4]>(bv[0]));
+                } else {
+                    mh::lgkm_wait<0>(reinterpret_cast<uint4(&)[2 * RB]>(av[1]));
+                    mh::lgkm_wait<0>(reinterpret_cast<uint4(&)[4]>(bv[1]));
+                }
 #pragma unroll
-                for (int rb = 0; rb < 2; ++rb)
+                for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-                    for (int cb = 0; cb < 2; ++cb)
-                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                            __builtin_bit_cast(mh::bf16x8_t, av[j][rb]), __builtin_bit_cast(mh::bf16x8_t, bv[j][cb]),
-                            acc[rb][cb], 0, 0, 0);
+                    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                        for (int cb = 0; cb < 2; ++cb)
+                            acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                                __builtin_bit_cast(mh::bf16x8_t, av[hf][jj][rb]),
+                                __builtin_bit_cast(mh::bf16x8_t, bv[hf][jj][cb]), acc[rb][cb], 0, 0, 0);
+            }
         }
     }
 
     // D lane layout: row 8 (q / 4) + 4 h + q % 4, column i32
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
@@ -170,7 +211,6 @@ __global__ __launch_bounds__(kThreads, 1) void k_gemm_nt(NtArgs p) {
             }
 }
 
-// Any shape: one output element per thread, f32 fma in ascending k.
 __global__ __launch_bounds__(256) void k_gemm_nt_plain(const uint16_t* a, const uint16_t* b, uint16_t* c, uint32_t m,
                                                        uint32_t n, uint32_t k) {
     const size_t total = static_cast<size_t>(m) * n;
@@ -200,13 +240,6 @@ int gemm_nt(const char* op, const uint16_t* a, const uint16_t* b, uint16_t* c, u
                            b, c, m, n, k);
         return mh::launch_status(op);
     }
-    // set on every tiled launch (a cheap host call): no shared flag for
-    // concurrent callers to race on, and right on every device
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_nt),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLds));
-    if (e != hipSuccess) {
-        return mh::hip_error(e, op);
-    }
     NtArgs p{};
     p.a = a;
     p.b = b;
@@ -214,10 +247,26 @@ int gemm_nt(const char* op, const uint16_t* a, const uint16_t* b, uint16_t* c, u
     p.m = m;
     p.n = n;
     p.k = k;
-    p.tiles_n = (n + kTile - 1) / kTile;
-    p.tiles = ((m + kTile - 1) / kTile) * p.tiles_n;
+    p.tiles_n = (n + kTileN - 1) / kTileN;
+    // 256-row tiles when they still give every CU one
+    const uint32_t tiles256 = ((m + 255u) / 256u) * p.tiles_n;
+    const bool big = tiles256 >= static_cast<uint32_t>(mh::cu_count());
+    const uint32_t tm = big ? 256u : 128u;
+    p.tiles = ((m + tm - 1) / tm) * p.tiles_n;
     p.per_xcd = (p.tiles + 7u) / 8u;
-    hipLaunchKernelGGL(k_gemm_nt, dim3(8u * p.per_xcd), dim3(kThreads), kLds, s, p);
+    // the attribute is set on every tiled launch (a cheap host call): no
+    // shared flag for concurrent callers to race on, and right on every device
+    const void* kern = big ? reinterpret_cast<const void*>(k_gemm_nt<256>) : reinterpret_cast<const void*>(k_gemm_nt<128>);
+    const uint32_t lds = big ? NtShape<256>::LDS : NtShape<128>::LDS;
+    const hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess) {
+        return mh::hip_error(e, op);
+    }
+    if (big) {
+        hipLaunchKernelGGL(k_gemm_nt<256>, dim3(8u * p.per_xcd), dim3(kThreads), lds, s, p);
+    } else {
+        hipLaunchKernelGGL(k_gemm_nt<128>, dim3(8u * p.per_xcd), dim3(kThreads), lds, s, p);
+    }
     return mh::launch_status(op);
 }
 

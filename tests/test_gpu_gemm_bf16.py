@@ -23,8 +23,9 @@ def _gemm_ref(a, b):
 
 
 @pytest.mark.parametrize("m,n,k", [
-    (4096, 2048, 2048),   # a prefill attention projection (tile path)
-    (300, 200, 1536),     # ragged M and N on the tile path
+    (4096, 2048, 2048),   # a prefill attention projection (256-row tiles)
+    (2085, 4160, 192),    # ragged M and N on the 256-row tiles (297 tiles)
+    (300, 200, 1536),     # ragged M and N on the 128-row tiles
     (128, 128, 64),       # one tile, one k block
     (33, 17, 40),         # K % 64 != 0: the per-element path
     (5, 11776, 192),      # few rows, wide N
@@ -39,7 +40,7 @@ def test_gemm_bf16_nt_matches_float64(dev, m, n, k):
     assert_tolerance(from_dev(c, np.uint16), _gemm_ref(a, b), f"gemm_bf16_nt {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("m,n,k", [(256, 384, 2048), (70, 50, 128), (9, 13, 72)])
+@pytest.mark.parametrize("m,n,k", [(256, 384, 2048), (2085, 4160, 128), (70, 50, 128), (9, 13, 72)])
 def test_gemm_bf16_nt_one_hot_exact(dev, m, n, k):
     """One-hot rows of A pick columns of B exactly (any summation order)."""
     rng = np.random.default_rng(k + m)
