@@ -349,13 +349,16 @@ def test_moe_prefill_stamped_matches_unstamped(dev, orc, skewed):
         assert ((got_entry[has] >= s_g[:n_wg, 0][has]) & (got_entry[has] <= s_g[:n_wg, 1][has])).all()
 
 
+@pytest.mark.parametrize("m", [256, 300])
 @pytest.mark.parametrize("mode", [1, 0])
-def test_moe_prefill_small(dev, orc, mode):
-    _log(f"moe prefill m=256 mode={mode}")
-    got, want, _ = _run_prefill(orc, 256, mode, 40 + mode)
+def test_moe_prefill_small(dev, orc, mode, m):
+    """The whole step (routing, sort, launch-ordered maps, GEMMs, combine) at
+    256 tokens and at 300 (a partial last routing block of 12 tokens)."""
+    _log(f"moe prefill m={m} mode={mode}")
+    got, want, _ = _run_prefill(orc, m, mode, 40 + mode + m)
     for key in ("ids", "gw", "counts", "offsets", "ids_sorted", "slotpos"):
         np.testing.assert_array_equal(got[key], want[key], err_msg=key)
-    assert_close(got["out"], want["out"], f"prefill out m=256 mode={mode}")
+    assert_close(got["out"], want["out"], f"prefill out m={m} mode={mode}")
 
 
 @pytest.mark.parametrize("mode", [1, 0])
