@@ -323,20 +323,41 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 2 : 1) void k_grouped(GemmArgs a
 // ------------------------------------------------------------------------
 // Segment kernel: one workgroup per block-map entry of any row count (maps
 // built with bm = 256 or 512), 4 waves, one workgroup per CU.  The entry's
-// rows are covered in passes of RB <= 8 row blocks of 32 (passes balanced:
-// a 270-row segment runs as 5 + 4 blocks, not 8 + 1); RB is a template
+// rows are covered in passes of RB <= 9 row blocks of 32 (passes balanced:
+// a 300-row segment runs as 5 + 5 blocks, not 9 + 1); RB is a template
 // argument of the pass, so the K loop has no per-row-block branches.  The
-// accumulators (RB x NMAT x NBW tiles of 32x32 f32, up to 256 registers)
-// live in AGPRs.  Per K-step of 16 the wave issues the next step's A
-// fragment reads before this step's MFMAs and dequantizes the next step's B
-// words between them, so LDS latency and the dequant VALU work run under
-// the matrix pipe.
+// accumulators (RB x NMAT x NBW tiles of 32x32 f32) of the first 8 row
+// blocks fill the 256 AGPRs; a ninth row block's 32 live in arch VGPRs
+// (mfma_vacc), so an expert of up to 288 rows -- nearly every expert of a
+// 4096-token, 64-expert, top-4 routing -- runs in one pass and its B codes
+// are loaded and dequantized once.  Per K-step of 16 the wave issues the
+// next step's A fragment reads before this step's MFMAs and dequantizes the
+// next step's B words between them, so LDS latency and the dequant VALU
+// work run under the matrix pipe.
 
 constexpr int kSegWaves = 4;
 #ifndef MH_SEG_RBMAX
-#define MH_SEG_RBMAX 8
+#define MH_SEG_RBMAX 9
 #endif
 constexpr int kSegRBMax = MH_SEG_RBMAX;  // row blocks of 32 per pass (max)
+constexpr int kSegAgprBlocks = 8;        // row blocks whose accumulators fit the AGPRs (NMAT * NBW == 2)
+
+// v_mfma_f32_32x32x16_bf16 with its accumulator in arch VGPRs.  The
+// compiler keeps every accumulator of the builtin in AGPRs and, once they
+// exceed the 256 AGPRs, shuffles them through VGPRs on every iteration
+// (v_accvgpr moves); the "+v" operand pins these 16 to VGPRs instead.  As
+// inline asm the MFMA is outside the compiler's hazard tracking: its
+// operands are written long before it (a step earlier) and the accumulator
+// is read by VALU only after mfma_vacc_drain().
+__device__ __forceinline__ f32x16_t mfma_vacc(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+    return c;
+}
+// Wait states between the last mfma_vacc and a VALU read of its result (an
+// 8-pass XDL op needs fewer than these 24).
+__device__ __forceinline__ void mfma_vacc_drain() {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+}
 #ifndef MH_SEG_STAGES
 #define MH_SEG_STAGES 3
 #endif
@@ -421,12 +442,15 @@ struct SegLayout {
 // fragments and B words are then read under step 3's MFMAs.
 template <int RB, int RBMAX, int NS, int NBW, int NMAT, bool GATHER, int EPI>
 __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint32_t n0,
-                                         uint32_t mp0, uint32_t m_end, uint32_t lds0, int lane,
+                                         uint32_t mp0, uint32_t m_end, uint32_t lds0, int lane_in,
                                          int wave) {
     using L = SegLayout<RBMAX, NBW, NMAT, NS>;
     static_assert(NS == 3, "loads run two stages ahead through a 3-slot A ring");
     constexpr int NB = L::NB;
     constexpr int QA = RB;  // A loads (8 rows each) per wave per stage
+    // the lane-derived offsets are recomputed in every pass (a few VALU ops):
+    // hoisted out of the pass loop they outlive the registers and are spilled
+    const int lane = static_cast<int>(mh::opaque(static_cast<uint32_t>(lane_in)));
     const int i32 = lane & 31, h = lane >> 5;
     const uint32_t K = a.k, nkb = K / kBK, groups = K / 64u;
 
@@ -539,6 +563,11 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
         }
     };
 
+    // accumulators of row blocks past kSegAgprBlocks stay in arch VGPRs
+    static_assert(NMAT * NBW * 16 * kSegAgprBlocks == 256, "the first kSegAgprBlocks row blocks fill the AGPRs");
+    auto seg_mma = [](int rb, bf16x8_t bw, bf16x8_t af, f32x16_t c) {
+        return rb >= kSegAgprBlocks ? mfma_vacc(bw, af, c) : __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw, af, c, 0, 0, 0);
+    };
     f32x16_t acc[NMAT][RB][NBW];
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat)
@@ -638,8 +667,7 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
                 for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
                     for (int cb = 0; cb < NBW; ++cb)
-                        acc[mat][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                            bfr[cur][mat * NBW + cb], af, acc[mat][rb][cb], 0, 0, 0);
+                        acc[mat][rb][cb] = seg_mma(rb, bfr[cur][mat * NBW + cb], af, acc[mat][rb][cb]);
                 if (rb == 0) {
 #pragma unroll
                     for (int t = 0; t < NB; ++t) {
@@ -673,8 +701,7 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
             for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
                 for (int cb = 0; cb < NBW; ++cb)
-                    acc[mat][rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                        bfr[1][mat * NBW + cb], af, acc[mat][rb][cb], 0, 0, 0);
+                    acc[mat][rb][cb] = seg_mma(rb, bfr[1][mat * NBW + cb], af, acc[mat][rb][cb]);
             if constexpr (NEXT) {
                 if (rb == (RB - 1) / 2) {
                     // (the RB A reads issued after them may still be in flight)
@@ -697,6 +724,9 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
     }
     stage(kb, no{}, yes{});
     stage(kb + 1, no{}, no{});
+    if constexpr (RB > kSegAgprBlocks) {
+        mfma_vacc_drain();
+    }
     // every wave is done with the ring before another pass refills it
     __builtin_amdgcn_s_barrier();
 

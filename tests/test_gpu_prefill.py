@@ -129,11 +129,12 @@ def test_grouped_gemm_one_hot_is_exact_dequant(dev, orc, tile):
     bf16(fma(s, q, b)) dequant must match the oracle's bit for bit."""
     bm, bn = tile
     rng = np.random.default_rng(bm + bn)
-    e, n, k = 4, 512, 2048
+    e, n, k = 5, 512, 2048
     w = layout.synth_quant(rng, e * n, k, 4)
     # 300 rows: two balanced passes of the segment kernels (5 + 5 blocks);
-    # 513: two map entries at bm = 512, one of a single row
-    counts = np.array([40, 0, 300, 513], np.uint32)
+    # 513: two map entries at bm = 512, one of a single row; 280: one pass of
+    # 9 row blocks (the ninth block's accumulators in arch VGPRs)
+    counts = np.array([40, 0, 300, 513, 280], np.uint32)
     s = int(counts.sum())
     cols = rng.integers(0, k, s)
     a = np.zeros((s, k), np.uint16)
@@ -157,6 +158,7 @@ def test_grouped_gemm_vs_oracle(dev, orc, tile):
     counts = rng.integers(0, 300, e).astype(np.uint32)
     counts[2] = 0
     counts[5] = 1
+    counts[6] = 288  # nine full row blocks: one pass of the segment kernel
     s = int(counts.sum())
     a = layout.synth_bf16(rng, (s, k), std=3.0)
     blocks, max_e, _ = _map(orc, counts, tile[0], tile[1], n)
@@ -174,7 +176,11 @@ def test_grouped_gate_up_and_fused_act(dev, orc, tile):
     gate = layout.synth_quant(rng, e * n, k, 4)
     up = layout.synth_quant(rng, e * n, k, 4)
     x = layout.synth_bf16(rng, (t, k))
-    ids = rng.integers(0, e, (t, 2)).astype(np.uint32)
+    # expert 3 gets exactly 270 rows (one 9-row-block pass of the segment
+    # kernel), the others share the rest
+    ids = rng.integers(0, e - 1, (t, 2)).astype(np.uint32)
+    ids[ids >= 3] += 1
+    ids[:270, 0] = 3
     counts = orc.moe_count(ids, e)
     offsets = orc.moe_offsets(counts)
     ids_sorted, _ = orc.moe_sorted(ids, offsets, t, e, 2)
