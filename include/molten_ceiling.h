@@ -45,6 +45,13 @@ int mhc_mfma(float* out, uint32_t workgroups, uint32_t iters, void* stream);
 int mhc_exchange(uint64_t* words, uint64_t* out, uint32_t workgroups, uint64_t value, int mode, uint32_t delay,
                  uint32_t spins, void* stream);
 
+/* Every word of the LDS of the CUs `workgroups` workgroups run on set to
+ * `pattern` (each workgroup takes a CU's whole 160 KB, so with workgroups
+ * >= the CU count every CU's LDS is written): the state a kernel that reads
+ * LDS before writing it would see after such a kernel.  A test's
+ * precondition, not a measurement. */
+int mhc_lds_fill(uint32_t pattern, uint32_t workgroups, void* stream);
+
 /* The bf16 FLOPs of one mhc_mfma launch. */
 uint64_t mhc_mfma_flops(uint32_t workgroups, uint32_t iters);
 

@@ -153,6 +153,18 @@ __global__ __launch_bounds__(64) void k_exchange(uint64_t* words, uint64_t* out,
 
 }  // namespace
 
+// Every word of a workgroup's LDS (the whole 160 KB of a CU: one such
+// workgroup fits a CU at a time) set to `pattern`; the stores are volatile,
+// so they are not dropped as never read.
+constexpr uint32_t kLdsBytes = 160u * 1024u;
+__global__ __launch_bounds__(256) void k_lds_fill(uint32_t pattern) {
+    extern __shared__ uint32_t lds_words[];
+    volatile uint32_t* const w = lds_words;
+    for (uint32_t i = threadIdx.x; i < kLdsBytes / 4u; i += blockDim.x) {
+        w[i] = pattern;
+    }
+}
+
 extern "C" {
 
 int mhc_read(const void* src, size_t bytes, uint32_t grid, uint32_t unroll, int nontemporal, uint32_t* sink,
@@ -205,6 +217,19 @@ int mhc_exchange(uint64_t* words, uint64_t* out, uint32_t workgroups, uint64_t v
 
 uint64_t mhc_mfma_flops(uint32_t workgroups, uint32_t iters) {
     return static_cast<uint64_t>(workgroups) * 4u * iters * 8u * (32u * 32u * 16u * 2u);
+}
+
+int mhc_lds_fill(uint32_t pattern, uint32_t workgroups, void* stream) {
+    if (workgroups == 0) {
+        return -1;
+    }
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_lds_fill),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kLdsBytes));
+    if (e != hipSuccess) {
+        return static_cast<int>(e);
+    }
+    hipLaunchKernelGGL(k_lds_fill, dim3(workgroups), dim3(256), kLdsBytes, static_cast<hipStream_t>(stream), pattern);
+    return status();
 }
 
 }  // extern "C"

@@ -343,7 +343,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
     float u1 = -__builtin_inff();          // greatest upper bound, its row
     uint32_t r1 = 0xffffffffu;
     float du = -__builtin_inff();          // greatest upper bound of the other rows
-    const float an = col ? xa[n] : 0.0f;
+    float an = 0.0f;  // sum |x| of batch row n: set once xa is staged (below), before any tile
 
     // a tile's rows 4q .. 4q + 3 of batch row n: store, bounds, candidates
     auto finish_tile = [&](uint32_t tile) {
@@ -501,6 +501,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_mfma(MfmaArgs a) {
         }
     }
     __syncthreads();
+    an = col ? xa[n] : 0.0f;
     mfma_stamp<ST>(a, gw, lane, MS_X);
 
     for (uint32_t s0 = 0; s0 < n_stages; s0 += kDepth) {

@@ -563,6 +563,7 @@ int moe_decode_fused(const void* router, int router_dtype, const float* bias, in
     // all kGrid workgroups resident (one per CU), one wave per output and
     // per router row, the activations fit the LDS stage
     if (mh::cu_count() < static_cast<int>(kGrid) || K > 2048u || K % 64u != 0 || NI % 64u != 0 ||
+        NI > 64u * 32u ||  // a slot's down chunks are one butterfly's lanes (lane = chunk)
         topk < 1 || topk > static_cast<uint32_t>(kMaxTk) || topk * NI > kMaxAct ||
         gate->group_size % 32u != 0 || down->group_size != gate->group_size ||
         up->group_size != gate->group_size || n_experts > static_cast<uint32_t>(kMaxExperts) ||

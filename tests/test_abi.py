@@ -39,7 +39,7 @@ def test_ceiling_library_exports():
     text = open(os.path.join(root, "include", "molten_ceiling.h")).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     names = sorted(set(re.findall(r"\b(mhc_[a-z0-9_]+)\s*\(", text)))
-    assert names == ["mhc_copy", "mhc_exchange", "mhc_mfma", "mhc_mfma_flops", "mhc_read"]
+    assert names == ["mhc_copy", "mhc_exchange", "mhc_lds_fill", "mhc_mfma", "mhc_mfma_flops", "mhc_read"]
     hip.load()
     lib = ctypes.CDLL(os.path.join(root, "molten_amd", "libmolten_ceiling.so"))
     for n in names:
@@ -54,6 +54,8 @@ def test_ceiling_library_exports():
     assert lib.mhc_exchange(0x1000, 0x2000, 256, 1, 2, 100, 16, None) == -1   # mode 2
     assert lib.mhc_exchange(0x1004, 0x2000, 256, 1, 0, 100, 16, None) == -1   # words not 8-byte aligned
     assert lib.mhc_exchange(0x1000, 0x2000, 256, 1, 0, 100, 0, None) == -1    # no polls
+    lib.mhc_lds_fill.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
+    assert lib.mhc_lds_fill(0, 0, None) == -1  # no workgroups
     lib.mhc_mfma_flops.restype = ctypes.c_uint64
     assert lib.mhc_mfma_flops(2, 3) == 2 * 4 * 3 * 8 * 32 * 32 * 16 * 2
 

@@ -513,6 +513,41 @@ def test_mfma_argmax_near_ties(dev, orc, bits):
     _argmax_case(dev, orc, h, x, batch)
 
 
+@pytest.mark.parametrize("pattern", [0xC7800000, 0x00000000])
+def test_mfma_argmax_after_lds_garbage(dev, orc, pattern):
+    """The matrix-core head after a kernel that left every CU's LDS holding
+    one word pattern (-65536.0f or 0): its error bound uses the staged sum
+    |x| of each batch row, which must be read after it is staged, never the
+    LDS an earlier kernel left (a sum of -65536 turns every interval inside
+    out: no candidate reaches the lower bound and every id comes out 0).
+    Ids are the oracle's, logits within tolerance."""
+    import ctypes
+    import os
+
+    import torch
+
+    _log(f"mfma argmax after LDS fill {pattern:#010x}")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    lib = ctypes.CDLL(os.path.join(root, "molten_amd", "libmolten_ceiling.so"))
+    lib.mhc_lds_fill.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
+    rng = np.random.default_rng(1701 + pattern % 7)
+    n, k, batch = 16384, 2048, 8
+    h = layout.synth_quant(rng, n, k, 6)
+    x = layout.synth_bf16(rng, (batch, k))
+    w, keep = dev_quant(h)
+    want = orc.gemv_quant(h, x, batch)
+    y = empty_dev((batch, n), np.uint16)
+    scratch = zeros_dev((hip.argmax_scratch_words(batch),), np.uint64)
+    ids = empty_dev((batch,), np.uint32)
+    xd = to_dev(x)
+    for call in range(2):
+        assert lib.mhc_lds_fill(pattern, 4 * 256, torch.cuda.current_stream().cuda_stream) == 0
+        hip.gemv_quant_argmax(w, xd, y, scratch, ids, batch)
+        got_ids = from_dev(ids, np.uint32)
+        assert got_ids.tolist() == [orc.argmax_bf16(want[b]) for b in range(batch)], call
+    assert_logits(from_dev(y, np.uint16), want, n, k, batch)
+
+
 @pytest.mark.parametrize("tie", [False, True])
 def test_model_head_128000_rows(dev, orc, tie):
     """The reference model's own LM head: Q6 128000 x 2048 at batch 1

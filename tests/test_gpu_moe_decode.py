@@ -226,6 +226,35 @@ def test_moe_decode_step_shapes(dev, orc, e, h, i, topk, shifted):
     del kg, ku, kd
 
 
+def test_moe_decode_wide_intermediate_is_rejected(dev, orc):
+    """An intermediate size above 2048 (a slot's down chunks no longer fit one
+    butterfly's 64 lanes, and the three-launch path holds act in registers)
+    is refused with MH_ERR_UNSUPPORTED instead of a partial down dot."""
+    _log("moe decode e=4 h=512 i=4096 topk=2 (rejected)")
+    e, h, i, topk = 4, 512, 4096, 2
+    rng = np.random.default_rng(4096)
+    gate, up, down = moe_weights(rng, e, h, i)
+    dg, kg = dev_quant(gate)
+    du, ku = dev_quant(up)
+    dd, kd = dev_quant(down)
+    rd = to_dev(router_weights(rng, e, h, False))
+    out = empty_dev((h,), np.uint16)
+    logits = empty_dev((e,), np.float32)
+    ids = empty_dev((topk,), np.uint32)
+    wt = empty_dev((topk,), np.uint16)
+    act = empty_dev((topk * i,), np.uint16)
+    scratch = zeros_dev((hip.MOE_DECODE_SCRATCH_WORDS,), np.uint32)
+    x = layout.synth_bf16(rng, (1, h))[0]
+    with pytest.raises(hip.MoltenError) as ei:
+        hip.moe_decode(rd, None, dg, du, dd, e, topk, to_dev(x), out, logits, ids, wt, act, scratch,
+                       mode=1)
+    assert ei.value.code == hip.MH_ERR_UNSUPPORTED
+    import torch
+
+    torch.cuda.synchronize()
+    del kg, ku, kd
+
+
 def test_prefill_router_and_route_batch(dev, orc):
     rng = np.random.default_rng(77)
     m = 300
