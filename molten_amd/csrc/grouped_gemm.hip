@@ -354,9 +354,15 @@ __device__ __forceinline__ f32x16_t mfma_vacc(bf16x8_t a, bf16x8_t b, f32x16_t c
     return c;
 }
 // Wait states between the last mfma_vacc and a VALU read of its result (an
-// 8-pass XDL op needs fewer than these 24).
-__device__ __forceinline__ void mfma_vacc_drain() {
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+// 8-pass XDL op needs fewer than these 24), and between the VALU writes that
+// zero the accumulators and the first mfma_vacc reading them.  The
+// accumulators pass through the asm, so every use of them on the far side
+// is ordered after the wait states.
+__device__ __forceinline__ void mfma_vacc_drain(f32x16_t& c0, f32x16_t& c1) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(c0), "+v"(c1) : : "memory");
+}
+__device__ __forceinline__ void mfma_vacc_ready(f32x16_t& c0, f32x16_t& c1) {
+    asm volatile("s_nop 4" : "+v"(c0), "+v"(c1));
 }
 #ifndef MH_SEG_STAGES
 #define MH_SEG_STAGES 3
@@ -577,6 +583,9 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
             for (int cb = 0; cb < NBW; ++cb)
 #pragma unroll
                 for (int q = 0; q < 16; ++q) acc[mat][rb][cb][q] = 0.0f;
+    if constexpr (RB > kSegAgprBlocks) {
+        mfma_vacc_ready(acc[0][kSegAgprBlocks][0], acc[NMAT - 1][kSegAgprBlocks][NBW - 1]);
+    }
 
     uint32_t aoff[4];
 #pragma unroll
@@ -725,7 +734,8 @@ __device__ __forceinline__ void seg_pass(const GemmArgs& a, uint32_t brow, uint3
     stage(kb, no{}, yes{});
     stage(kb + 1, no{}, no{});
     if constexpr (RB > kSegAgprBlocks) {
-        mfma_vacc_drain();
+        static_assert(RB == kSegAgprBlocks + 1 && NMAT * NBW == 2, "one VGPR row block of two tiles");
+        mfma_vacc_drain(acc[0][kSegAgprBlocks][0], acc[NMAT - 1][kSegAgprBlocks][NBW - 1]);
     }
     // every wave is done with the ring before another pass refills it
     __builtin_amdgcn_s_barrier();
