@@ -405,13 +405,16 @@ __device__ __forceinline__ float q6_chunk_dot(const uint32_t (&w)[6], const floa
     return p;
 }
 
-// The same with x pre-scaled by q6_scale_x (positions 4j + 3 times 1/4,
-// exact).  Of every 3 bytes (4 codes), code 4j sits in bits 0-5 of the first
-// byte and code 4j + 3 in bits 2-7 of the third: both are converted straight
-// from their byte of the word masked once (v_cvt_f32_ubyte: q and 4q), the
-// two codes between them with a field extract and a conversion.  q x and
+// The same with x pre-scaled by q6_scale_x (odd positions times 1/4,
+// exact).  Of every 3 bytes (4 codes) of the chunk, code 4j sits in bits 0-5
+// of the first byte and code 4j + 3 in bits 2-7 of the third: both are
+// converted straight from their byte of the word masked once (v_cvt_f32_ubyte:
+// q and 4q).  The two codes between them straddle bytes; in the chunk's bit
+// stream shifted right by 4 (v_alignbit of two words) code 4j + 1 sits in
+// bits 2-7 of byte 3j and code 4j + 2 in bits 0-5 of byte 3j + 1, so they too
+// are converted from the shifted word masked once (4q and q).  q x and
 // (4q)(x / 4) are the same reals, so the chain equals fma(q_k, x_k, p) in
-// ascending k with one VALU op less for half the codes.
+// ascending k with every code one conversion.
 __host__ __device__ constexpr uint32_t q6_byte_mask(int d) {
     uint32_t m = 0;
     for (int k = 0; k < 4; ++k) {
@@ -420,25 +423,39 @@ __host__ __device__ constexpr uint32_t q6_byte_mask(int d) {
     }
     return m;
 }
+// Mask of word d of the stream shifted right by 4: bytes 3j (code 4j + 1 as
+// 4q) and 3j + 1 (code 4j + 2).
+__host__ __device__ constexpr uint32_t q6_shift_mask(int d) {
+    uint32_t m = 0;
+    for (int k = 0; k < 4; ++k) {
+        const int b = 4 * d + k;
+        m |= (b % 3 == 0 ? 0xfcu : (b % 3 == 1 ? 0x3fu : 0u)) << (8 * k);
+    }
+    return m;
+}
 __device__ __forceinline__ float q6_chunk_dot_s(const uint32_t (&w)[6], const float* xr) {
-    uint32_t m[6];
+    uint32_t m[6], ms[6];
 #pragma unroll
     for (int d = 0; d < 6; ++d) {
         m[d] = opaque(w[d] & q6_byte_mask(d));
+        // word d of the stream >> 4 (the last word's top bits lie past the
+        // chunk and are never used)
+        const uint32_t sh = d < 5 ? __builtin_amdgcn_alignbit(w[d + 1], w[d], 4) : (w[5] >> 4);
+        ms[d] = opaque(sh & q6_shift_mask(d));
     }
     float p = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-        const int bit = 6 * i;
-        const int d = bit >> 5;
-        const int o = bit & 31;
+        const int j = i >> 2, r = i & 3;
         float v;
-        if ((bit & 7) == 0 || (bit & 7) == 2) {
-            v = ubyte_f32(m[(bit >> 3) >> 2], (bit >> 3) & 3);
-        } else if (o + 6 <= 32) {
-            v = static_cast<float>((w[d] >> o) & 63u);
+        if (r == 0) {
+            v = ubyte_f32(m[(3 * j) >> 2], (3 * j) & 3);
+        } else if (r == 3) {
+            v = ubyte_f32(m[(3 * j + 2) >> 2], (3 * j + 2) & 3);
+        } else if (r == 1) {
+            v = ubyte_f32(ms[(3 * j) >> 2], (3 * j) & 3);
         } else {
-            v = static_cast<float>(__builtin_amdgcn_alignbit(w[d + 1], w[d], o) & 63u);
+            v = ubyte_f32(ms[(3 * j + 1) >> 2], (3 * j + 1) & 3);
         }
         p = __builtin_fmaf(v, xr[i], p);
     }
@@ -514,10 +531,11 @@ __device__ __forceinline__ void load_x_chunk(const uint16_t* xp, float (&xr)[32]
     x_words_to_f32(xw, xr, xs);
 }
 
-// Scale a raw x chunk for q6_chunk_dot_s: positions 4j + 3 times 1/4 (exact).
+// Scale a raw x chunk for q6_chunk_dot_s: odd positions (codes 4j + 1 and
+// 4j + 3, converted as 4q) times 1/4 (exact).
 __device__ __forceinline__ void q6_scale_x(float (&xr)[32]) {
 #pragma unroll
-    for (int i = 3; i < 32; i += 4) {
+    for (int i = 1; i < 32; i += 2) {
         xr[i] = xr[i] * 0.25f;
     }
 }
