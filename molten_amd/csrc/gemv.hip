@@ -300,8 +300,12 @@ constexpr int kMaxGroups = 64;  // K / group size <= 2048 / 32
 // bests, a DPP wave argmax, then the finisher (or the reference's atomic
 // max).  WV: waves per workgroup (2 only without the argmax, whose
 // publication and collector take 4).  ST: phase timestamps (measurement).
+// The Q4 head (FAST, ARGMAX, two groups) is held to five workgroups per CU:
+// 94 VGPRs instead of 99 (no spills), so five waves share a SIMD instead of
+// four and 1280 of its 2048 workgroups start at once (26 KB of LDS each).
+// The Q6 head spills at that bound and keeps four.
 template <int BITS, bool FAST, bool ARGMAX, int NG, int WV = kWaves, bool ST = false>
-__global__ __launch_bounds__(kThreads) void k_gemv_rows(GemvArgs a) {
+__global__ __launch_bounds__(kThreads, (BITS == 4 && FAST && ARGMAX && NG == 2) ? 5 : 1) void k_gemv_rows(GemvArgs a) {
     static_assert(NG == 1 || NG == 2, "one or two 4-row groups per block");
     static_assert(WV == kWaves || (WV == 2 && !ARGMAX), "two-wave workgroups only without the argmax");
     constexpr int R = kGroupRows, BR = NG * R;
