@@ -548,20 +548,23 @@ def test_mfma_argmax_after_lds_garbage(dev, orc, pattern):
     assert_logits(from_dev(y, np.uint16), want, n, k, batch)
 
 
+@pytest.mark.parametrize("bits", [6, 4])
 @pytest.mark.parametrize("tie", [False, True])
-def test_model_head_128000_rows(dev, orc, tie):
+def test_model_head_128000_rows(dev, orc, tie, bits):
     """The reference model's own LM head: Q6 128000 x 2048 at batch 1
     (vocab 128000, src/lfm.rs:22-42, through gemv_head_argmax,
-    src/kernels/lfm.rs:826-844), past the 65536 rows of the BASELINE configs.
-    Both entry points: mh_gemv_quant_argmax (logits bit-exact, id) and the
-    reference pair mh_gemv_head_argmax + mh_token_tail.  With `tie` the
-    winning row is copied to rows 65535 and 65536 and to row 127999 (the
-    rows on both sides of the 65536-row boundary and the last row), and the
-    original winner is made smaller: the lowest copy, 65535, must win."""
-    _log(f"model head 128000x2048 q6 tie={tie}")
-    rng = np.random.default_rng(128000 + tie)
+    src/kernels/lfm.rs:826-844), past the 65536 rows of the BASELINE configs;
+    bits 4 runs the same rows through the Q4 head instantiation (held to five
+    workgroups per CU).  Both entry points: mh_gemv_quant_argmax (logits
+    bit-exact, id) and the reference pair mh_gemv_head_argmax +
+    mh_token_tail.  With `tie` the winning row is copied to rows 65535 and
+    65536 and to row 127999 (the rows on both sides of the 65536-row boundary
+    and the last row), and the original winner is made smaller: the lowest
+    copy, 65535, must win."""
+    _log(f"model head 128000x2048 q{bits} tie={tie}")
+    rng = np.random.default_rng(128000 + tie + 10 * bits)
     n, k = 128000, 2048
-    h = layout.synth_quant(rng, n, k, 6)
+    h = layout.synth_quant(rng, n, k, bits)
     x = layout.synth_bf16(rng, (1, k))
     if tie:
         top = orc.argmax_bf16(orc.gemv_quant(h, x, 1)[0])
